@@ -1,0 +1,176 @@
+/*
+ * nsg_spec.h -- C ABI of the MI355X (gfx950) speculative-decoding verify step.
+ *
+ * One shared library, libnsg_spec.so, built from the HIP sources in nanosglang_amd/csrc/.
+ * Every entry point:
+ *   - takes plain device pointers, sizes and a hipStream_t (as void*);
+ *   - enqueues on that stream and never synchronises the host;
+ *   - returns 0 on success or an NSG_ERR_* code, with a message available from
+ *     nsg_last_error() (thread-local).  No C++ exception crosses the ABI.
+ * All tensors are borrowed; the library frees nothing it did not allocate and
+ * keeps no global mutable state besides the per-thread error string.
+ *
+ * Layouts follow the reference (xiehuanyi/nanoSGLang):
+ *   KV pool per layer: [num_pages, page_size, num_kv_heads, head_dim] bf16
+ *     ("NHD", nano_sglang/engine/paged_kv_cache.py:60-69);
+ *   page table: CSR kv_indptr int32[B+1], kv_indices int32[nnz],
+ *     kv_last_page_len int32[B] (nano_sglang/engine/engine.py:419-448);
+ *   queries / outputs: [total_q, num_qo_heads, head_dim] bf16 with
+ *     qo_indptr int32[B+1] (nano_sglang/engine/engine.py:340-342).
+ */
+#ifndef NSG_SPEC_H
+#define NSG_SPEC_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* nsg_stream_t; /* a hipStream_t; NULL = the null stream */
+
+enum {
+  NSG_OK = 0,
+  NSG_ERR_ARG = 1,         /* bad shape, size, pointer or index argument */
+  NSG_ERR_UNSUPPORTED = 2, /* valid input outside what the kernels implement */
+  NSG_ERR_WORKSPACE = 3,   /* workspace or work-list buffer too small */
+  NSG_ERR_HIP = 4          /* a HIP runtime call failed */
+};
+
+/* Message for the last failing call on this thread ("" after success). */
+const char* nsg_last_error(void);
+/* ABI version of this header (NSG_ABI_VERSION). */
+int32_t nsg_abi_version(void);
+#define NSG_ABI_VERSION 1
+
+/* ------------------------------------------------------------------------
+ * Verify attention: ragged multi-query attention over the paged KV cache
+ * with GQA and the bottom-right causal rule (row r of a request with q_len
+ * query tokens and L KV tokens sees KV positions <= L - q_len + r).
+ *
+ * Replaces FlashInfer's BatchPrefillWithPagedKVCacheWrapper as the reference
+ * uses it: .plan(...) at nano_sglang/engine/engine.py:451-462 (host, once per
+ * step) and .run(q, (k_cache[layer], v_cache[layer])) at
+ * nano_sglang/model/causal_lm.py:340 (device, once per layer).
+ * ---------------------------------------------------------------------- */
+
+#define NSG_ATTN_WORK_INTS 8
+
+typedef struct {
+  int32_t num_work;        /* work items: (request, query tile, KV split)        */
+  int32_t num_groups;      /* (request, query tile) pairs                        */
+  int32_t row_tiles;       /* 16-row MFMA tiles per work item, 1..4              */
+  int32_t q_tile_tokens;   /* query tokens per query tile                        */
+  int32_t max_splits;      /* largest KV split count of any group                */
+  int32_t head_dim;
+  int32_t num_qo_heads;
+  int32_t num_kv_heads;
+  int64_t workspace_bytes; /* device workspace nsg_attn_run needs for this plan  */
+} nsg_attn_plan_t;
+
+/* Host-side planner (replaces BatchPrefillWithPagedKVCacheWrapper.plan,
+ * engine.py:451-462).  Reads HOST copies of the CSR metadata and writes the
+ * work list (num_work * NSG_ATTN_WORK_INTS int32) into work_h, which the
+ * caller copies to device memory for nsg_attn_run.  num_cus sizes the KV
+ * split (256 on MI355X).  head_dim must be 64 or 128; num_qo_heads a multiple
+ * of num_kv_heads with a group of at most 64; page_size a power of two. */
+int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
+                      const int32_t* kv_last_page_len_h, int32_t batch,
+                      int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                      int32_t page_size, int32_t causal, int32_t num_cus,
+                      int32_t* work_h, int32_t work_capacity, nsg_attn_plan_t* plan);
+
+/* Device workspace must be zero-filled once before its first use (the kernels
+ * leave their counters at zero on exit).  Returns the number of bytes. */
+int64_t nsg_attn_workspace_bytes(const nsg_attn_plan_t* plan);
+
+/* Runs one layer (replaces wrapper.run, causal_lm.py:340).
+ * q/out: [total_q, Hq, D] bf16; k_cache/v_cache: [num_pages, P, Hkv, D] bf16;
+ * work_d: device copy of the planner's work list.  Page ids outside
+ * [0, num_pages) read as zeros and raise a flag returned by
+ * nsg_attn_check_flags. */
+int32_t nsg_attn_run(const nsg_attn_plan_t* plan, const int32_t* work_d,
+                     const void* q, const void* k_cache, const void* v_cache, void* out,
+                     const int32_t* qo_indptr, const int32_t* kv_indptr,
+                     const int32_t* kv_indices, const int32_t* kv_last_page_len,
+                     int32_t page_size, int32_t num_pages, float sm_scale, int32_t causal,
+                     void* workspace, int64_t workspace_bytes, nsg_stream_t stream);
+
+/* Copies the workspace's error flags (bit 0: page id out of range) to
+ * *flags_h after synchronising the stream, and clears them. */
+int32_t nsg_attn_check_flags(void* workspace, int32_t* flags_h, nsg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Fused acceptance: ratio test, residual resample, bonus token and rollback
+ * slots for one verify step of B requests.
+ *
+ * Replaces nano_sglang/decode/speculative.py:130-184 (the per-position
+ * Python loop) and gives the paged counterpart of reset_draft_cache
+ * (speculative.py:186-196).
+ *
+ * target_logits: B x (k+1) rows of `vocab` logits; draft_logits: B x k rows
+ *   (may be NULL when temperature < 1e-6, the greedy rule of
+ *   nano_sglang/engine/sampling.py:44).  Row r of request b starts at
+ *   element b*req_stride + r*row_stride; logits_dtype 0 = bf16, 1 = fp32.
+ * draft_tokens int64 [B, k]; uniforms fp32 [B, k+1] (columns 0..k-1 for the
+ *   ratio tests, column k for the residual / bonus draw).
+ * Page table (may be NULL, then no rollback slots): kv_indptr / kv_indices
+ *   as in the attention entry points, start_pos int32 [B] = position of the
+ *   first verify token (the cache length before verify).
+ * Outputs: num_emitted int32 [B] in [1, k+1]; emitted int64 [B, k+1] padded
+ *   with -1; rollback_slots int64 [B, k] padded with -1 = flat slots
+ *   block*P + offset of positions start+n .. start+k.
+ * k may be 0: the call then samples one token per request from row 0
+ *   (argmax when greedy), which is the reference's sample_token
+ *   (sampling.py:25-50) without top-k / top-p.
+ * ---------------------------------------------------------------------- */
+int64_t nsg_spec_accept_workspace_bytes(int32_t batch, int32_t k, int32_t vocab);
+
+int32_t nsg_spec_accept(const void* target_logits, int64_t target_req_stride,
+                        int64_t target_row_stride, const void* draft_logits,
+                        int64_t draft_req_stride, int64_t draft_row_stride,
+                        int32_t logits_dtype, const int64_t* draft_tokens,
+                        const float* uniforms, int32_t batch, int32_t k, int32_t vocab,
+                        float temperature, const int32_t* kv_indptr,
+                        const int32_t* kv_indices, const int32_t* start_pos,
+                        int32_t page_size, int32_t* num_emitted, int64_t* emitted,
+                        int64_t* rollback_slots, void* workspace, int64_t workspace_bytes,
+                        nsg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * KV slot writes and rollback.
+ * ---------------------------------------------------------------------- */
+
+/* Scatter num_tokens rows of K and V ([num_kv_heads, head_dim] bf16 each,
+ * consecutive rows src_token_stride elements apart) into flat slots of one
+ * layer's pool ([num_slots, num_kv_heads, head_dim]); slot < 0 skips the
+ * row.  Replaces `k_flat[write_indices] = k; v_flat[write_indices] = v`
+ * (nano_sglang/model/causal_lm.py:335-338). */
+int32_t nsg_kv_write(const void* k, const void* v, int64_t src_token_stride,
+                     const int64_t* slots, int32_t num_tokens, void* k_cache,
+                     void* v_cache, int32_t num_kv_heads, int32_t head_dim,
+                     int64_t num_slots, nsg_stream_t stream);
+
+/* Zero the K and V rows of `count` flat slots (negative slots are skipped)
+ * in `num_layers` consecutive layer pools, layer_stride elements apart.
+ * Used after nsg_spec_accept so rolled-back positions hold no stale data. */
+int32_t nsg_kv_clear_slots(const int64_t* slots, int32_t count, void* k_cache, void* v_cache,
+                           int32_t num_layers, int64_t layer_stride, int32_t num_kv_heads,
+                           int32_t head_dim, int64_t num_slots, nsg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Philox4x32-10 uniforms: out[i] = u(seed, stream_id, offset + i) with
+ * u = (word >> 8) * 2^-24 and word n of a stream = component n % 4 of
+ * philox(ctr = [n/4 lo, n/4 hi, stream_id, 0], key = [seed lo, seed hi]).
+ * Supplies the verify step's uniforms in place of torch.rand
+ * (nano_sglang/decode/speculative.py:150).
+ * ---------------------------------------------------------------------- */
+int32_t nsg_philox_uniform(uint64_t seed, uint32_t stream_id, uint64_t offset, int64_t n,
+                           float* out, nsg_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NSG_SPEC_H */

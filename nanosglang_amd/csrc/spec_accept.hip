@@ -1,0 +1,657 @@
+// Fused acceptance for one speculative verify step on gfx950: greedy or
+// stochastic ratio test, textbook residual resample, bonus token and
+// rollback slots, for B requests at once.
+//
+// Reference: nano_sglang/decode/speculative.py:130-184 (per-position Python
+// loop: softmax over the vocabulary, ratio test, resample, bonus) and
+// speculative.py:186-196 (rollback, a no-op there).  Parity decisions:
+//   greedy (T < 1e-6, nano_sglang/engine/sampling.py:44): T->0 limit of the
+//     ratio test -- accept d_i iff d_i == argmax(target row i) (lowest index on
+//     ties); the first mismatch emits that argmax; all-match emits
+//     argmax(target row k);
+//   stochastic: p = softmax(logits / T); accept iff u_i < min(1, pt/pd)
+//     (pd == 0 accepts); on rejection sample max(0, pt - pd) (falls back to pt
+//     if that sums to 0) by inverse CDF with u_k; else the bonus from pt_k.
+//
+// Two launches, both bandwidth-bound streaming passes:
+//   stats_kernel  grid (chunks, rows): every target row (and draft row when
+//     stochastic) is cut into chunks; a workgroup reduces its chunk to
+//     (max, sum exp2) -- or (max, first argmax) when greedy -- with 16-byte
+//     loads and wave-shuffle reductions.  The last workgroup of a request
+//     (atomic counter) combines the chunk stats, runs the k ratio tests and
+//     writes the accepted prefix, the decision and the rollback slots.
+//   sample_kernel grid (chunks, B), stochastic only: chunk sums of the
+//     residual (or bonus) weights over the one decided row pair; the last
+//     workgroup of a request picks the chunk by a sequential prefix and the
+//     token by a block scan over contiguous per-thread runs, so the search
+//     re-reads one chunk only.  These rows were just streamed by stats_kernel.
+#include <cfloat>
+#include <climits>
+
+#include "common.hpp"
+
+namespace nsg {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxK = 32;
+constexpr int kMaxBatch = 1 << 14;
+constexpr int kMaxChunks = 64;
+constexpr int kTargetWgs = 2048;
+constexpr int64_t kFlagBytes = 256;
+constexpr int64_t kCounterBytes = 2LL * kMaxBatch * 4;
+constexpr float kLog2e = 1.4426950408889634f;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct AccParams {
+  const void* tl;
+  int64_t t_req, t_row;
+  const void* dl;
+  int64_t d_req, d_row;
+  const int64_t* dtok;
+  const float* u;
+  int B, k, V;
+  float c;  // log2(e) / T
+  int greedy;
+  const int* kv_indptr;
+  const int* kv_indices;
+  const int* start_pos;
+  int log2P;
+  int* n_out;
+  int64_t* emitted;
+  int64_t* rollback;
+  int nch, cs;    // stats chunks / chunk size
+  int nch2, cs2;  // sample chunks / chunk size
+  float2* stats;  // [rows][nch]
+  int* cnt_a;     // [kMaxBatch]
+  int* cnt_b;     // [kMaxBatch]
+  float* dec;     // [B][8]
+  float* psum;    // [B][nch2]
+  int* flags;
+};
+
+template <typename T>
+struct Logit;
+template <>
+struct Logit<bf16> {
+  static __device__ __forceinline__ float at(const void* base, int64_t off) {
+    return bf16_bits_to_float(reinterpret_cast<const uint16_t*>(base)[off]);
+  }
+  // 8 consecutive values from a 16-byte aligned element offset
+  static __device__ __forceinline__ void load8(const void* base, int64_t off, float* x) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(base) + off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = __uint_as_float(v[i] << 16);
+      x[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+    }
+  }
+  static constexpr int kAlign = 8;
+};
+template <>
+struct Logit<float> {
+  static __device__ __forceinline__ float at(const void* base, int64_t off) {
+    return reinterpret_cast<const float*>(base)[off];
+  }
+  static __device__ __forceinline__ void load8(const void* base, int64_t off, float* x) {
+    const float* p = reinterpret_cast<const float*>(base) + off;
+    const floatx4 a = *reinterpret_cast<const floatx4*>(p);
+    const floatx4 b = *reinterpret_cast<const floatx4*>(p + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[i] = a[i];
+      x[4 + i] = b[i];
+    }
+  }
+  static constexpr int kAlign = 4;
+};
+
+// (max, sum 2^(x - max)) pair merge.
+__device__ __forceinline__ void ms_merge(float& m, float& s, float m2, float s2) {
+  const float M = fmaxf(m, m2);
+  if (M == -INFINITY) {  // both empty (or all -inf): keep s = 0, no inf - inf
+    s = 0.f;
+    m = M;
+    return;
+  }
+  s = s * exp2f(m - M) + s2 * exp2f(m2 - M);
+  m = M;
+}
+
+// (value, index) argmax merge: larger value wins, ties -> lower index.
+__device__ __forceinline__ void am_merge(float& v, int& i, float v2, int i2) {
+  if (v2 > v || (v2 == v && i2 < i)) {
+    v = v2;
+    i = i2;
+  }
+}
+
+__device__ __forceinline__ void wave_ms(float& m, float& s) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float m2 = __shfl_xor(m, o, 64);
+    const float s2 = __shfl_xor(s, o, 64);
+    ms_merge(m, s, m2, s2);
+  }
+}
+
+__device__ __forceinline__ void wave_am(float& v, int& i) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float v2 = __shfl_xor(v, o, 64);
+    const int i2 = __shfl_xor(i, o, 64);
+    am_merge(v, i, v2, i2);
+  }
+}
+
+__device__ __forceinline__ void row_of(const AccParams& p, int r, int& b, int& i, bool& draft) {
+  const int nt = p.B * (p.k + 1);
+  if (r < nt) {
+    b = r / (p.k + 1);
+    i = r - b * (p.k + 1);
+    draft = false;
+  } else {
+    const int r2 = r - nt;
+    b = r2 / p.k;
+    i = r2 - b * p.k;
+    draft = true;
+  }
+}
+
+__device__ __forceinline__ int64_t trow(const AccParams& p, int b, int i) {
+  return (int64_t)b * p.t_req + (int64_t)i * p.t_row;
+}
+__device__ __forceinline__ int64_t drow(const AccParams& p, int b, int i) {
+  return (int64_t)b * p.d_req + (int64_t)i * p.d_row;
+}
+
+// Flat slots of the rejected verify positions start+n .. start+k.
+__device__ void write_rollback(const AccParams& p, int b, int n) {
+  if (!p.rollback) return;
+  for (int i = 0; i < p.k; ++i) {
+    int64_t slot = -1;
+    const int pos = p.start_pos[b] + n + i;
+    if (n + i <= p.k && p.kv_indptr) {
+      const int pb = p.kv_indptr[b];
+      const int np = p.kv_indptr[b + 1] - pb;
+      const int pg = pos >> p.log2P;
+      if (pos >= 0 && pg < np) {
+        slot = ((int64_t)p.kv_indices[pb + pg] << p.log2P) + (pos & ((1 << p.log2P) - 1));
+      } else {
+        atomicOr(p.flags, 2);
+      }
+    }
+    p.rollback[(int64_t)b * p.k + i] = slot;
+  }
+}
+
+// The decision for request b, run by one wave of the last stats workgroup.
+template <typename T>
+__device__ void decide(const AccParams& p, int b) {
+  const int lane = threadIdx.x & 63;
+  const int k = p.k;
+  int64_t* em = p.emitted + (int64_t)b * (k + 1);
+  if (p.greedy) {
+    int n = k + 1;
+    for (int i = 0; i <= k; ++i) {
+      const int r = b * (k + 1) + i;
+      float v = -INFINITY;
+      int ix = INT_MAX;
+      for (int c = lane; c < p.nch; c += 64) {
+        const float2 st = p.stats[(int64_t)r * p.nch + c];
+        am_merge(v, ix, st.x, __float_as_int(st.y));
+      }
+      wave_am(v, ix);
+      if (lane == 0) {
+        if (i < k && p.dtok[(int64_t)b * k + i] == (int64_t)ix) {
+          em[i] = ix;
+        } else {
+          em[i] = ix;
+          n = i + 1;
+        }
+      }
+      n = __shfl(n, 0, 64);
+      if (n == i + 1) break;
+    }
+    if (lane == 0) {
+      for (int i = n; i <= k; ++i) em[i] = -1;
+      p.n_out[b] = n;
+      write_rollback(p, b, n);
+    }
+    return;
+  }
+  // stochastic: normalisers of target rows 0..k and draft rows 0..k-1
+  __shared__ float sM[2 * kMaxK + 1], sZ[2 * kMaxK + 1];
+  for (int i = 0; i < 2 * k + 1; ++i) {
+    const int r = i <= k ? b * (k + 1) + i : p.B * (k + 1) + b * k + (i - k - 1);
+    float m = -INFINITY, s = 0.f;
+    for (int c = lane; c < p.nch; c += 64) {
+      const float2 st = p.stats[(int64_t)r * p.nch + c];
+      ms_merge(m, s, st.x, st.y);
+    }
+    wave_ms(m, s);
+    if (lane == 0) {
+      sM[i] = m;
+      sZ[i] = s;
+    }
+  }
+  if (lane != 0) return;
+  int j = k;  // first rejected position, k = none
+  for (int i = 0; i < k; ++i) {
+    const int64_t x = p.dtok[(int64_t)b * k + i];
+    bool acc;
+    if (x < 0 || x >= p.V) {
+      atomicOr(p.flags, 4);
+      acc = false;
+    } else {
+      const float lt = Logit<T>::at(p.tl, trow(p, b, i) + x) * p.c;
+      const float ld = Logit<T>::at(p.dl, drow(p, b, i) + x) * p.c;
+      const float pt = exp2f(lt - sM[i]) / sZ[i];
+      const float pd = exp2f(ld - sM[k + 1 + i]) / sZ[k + 1 + i];
+      acc = pd > 0.f ? (p.u[(int64_t)b * (k + 1) + i] < fminf(1.f, pt / pd)) : true;
+    }
+    if (acc) {
+      em[i] = x;
+    } else {
+      j = i;
+      break;
+    }
+  }
+  for (int i = j; i <= k; ++i) em[i] = -1;
+  float* d = p.dec + (int64_t)b * 8;
+  d[0] = __int_as_float(j);
+  d[1] = __int_as_float(j < k ? 0 : 1);  // 0 = residual of row j, 1 = target row j alone
+  d[2] = sM[j];
+  d[3] = 1.f / sZ[j];
+  d[4] = j < k ? sM[k + 1 + j] : 0.f;
+  d[5] = j < k ? 1.f / sZ[k + 1 + j] : 0.f;
+  p.n_out[b] = j + 1;
+  write_rollback(p, b, j + 1);
+}
+
+template <typename T, bool GREEDY>
+__global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
+  __shared__ float sm_a[kThreads / 64];
+  __shared__ float sm_b[kThreads / 64];
+  __shared__ int s_last;
+  const int r = blockIdx.y;
+  const int chunk = blockIdx.x;
+  int b, i;
+  bool draft;
+  row_of(p, r, b, i, draft);
+  const void* base = draft ? p.dl : p.tl;
+  const int64_t roff = draft ? drow(p, b, i) : trow(p, b, i);
+  const int v0 = chunk * p.cs;
+  const int v1 = min(p.V, v0 + p.cs);
+  const int tid = threadIdx.x;
+  const bool vec = ((roff % Logit<T>::kAlign) == 0);
+
+  float m = -INFINITY, s = 0.f;  // stochastic: running max / sum of 2^(x c - m)
+  float bv = -INFINITY;          // greedy: best value / index
+  int bi = INT_MAX;
+  auto take = [&](float x, int v) {
+    if constexpr (GREEDY) {
+      am_merge(bv, bi, x, v);
+    } else {
+      const float y = x * p.c;
+      if (y > m) {
+        s = s * exp2f(m - y);
+        m = y;
+      }
+      s += exp2f(y - (m == -INFINITY ? 0.f : m));
+    }
+  };
+  int v = v0 + tid * 8;
+  if (vec) {
+    for (; v + 8 <= v1; v += kThreads * 8) {
+      float x[8];
+      Logit<T>::load8(base, roff + v, x);
+      if constexpr (GREEDY) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) am_merge(bv, bi, x[e], v + e);
+      } else {
+        float mx = x[0] * p.c;
+#pragma unroll
+        for (int e = 1; e < 8; ++e) mx = fmaxf(mx, x[e] * p.c);
+        if (mx > m) {
+          s = s * exp2f(m - mx);
+          m = mx;
+        }
+        const float mm = m == -INFINITY ? 0.f : m;  // all -inf so far: adds 0
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += exp2f(x[e] * p.c - mm);
+      }
+    }
+  }
+  // tail (and unaligned rows): scalar, still in increasing index per thread
+  for (; v < v1; v += kThreads * 8) {
+    for (int e = 0; e < 8 && v + e < v1; ++e) take(Logit<T>::at(base, roff + v + e), v + e);
+  }
+
+  const int lane = tid & 63, wave = tid >> 6;
+  if constexpr (GREEDY) {
+    wave_am(bv, bi);
+    if (lane == 0) {
+      sm_a[wave] = bv;
+      sm_b[wave] = __int_as_float(bi);
+    }
+  } else {
+    if (m == -INFINITY) s = 0.f;
+    wave_ms(m, s);
+    if (lane == 0) {
+      sm_a[wave] = m;
+      sm_b[wave] = s;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float a = sm_a[0], c2 = sm_b[0];
+    for (int w = 1; w < kThreads / 64; ++w) {
+      if constexpr (GREEDY) {
+        int ia = __float_as_int(c2);
+        am_merge(a, ia, sm_a[w], __float_as_int(sm_b[w]));
+        c2 = __int_as_float(ia);
+      } else {
+        ms_merge(a, c2, sm_a[w], sm_b[w]);
+      }
+    }
+    p.stats[(int64_t)r * p.nch + chunk] = make_float2(a, c2);
+  }
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    const int per_req = (p.k + 1 + (GREEDY ? 0 : p.k)) * p.nch;
+    s_last = atomicAdd(&p.cnt_a[b], 1) == per_req - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  if (wave == 0) decide<T>(p, b);
+  if (tid == 0) p.cnt_a[b] = 0;
+}
+
+// Weight of vocabulary entry v for the decided row pair.
+template <typename T>
+__device__ __forceinline__ float weight(const AccParams& p, int64_t to, int64_t dof, int mode,
+                                        float Mt, float iZt, float Md, float iZd, int v) {
+  const float pt = exp2f(Logit<T>::at(p.tl, to + v) * p.c - Mt) * iZt;
+  if (mode != 0) return pt;
+  const float pd = exp2f(Logit<T>::at(p.dl, dof + v) * p.c - Md) * iZd;
+  return fmaxf(0.f, pt - pd);
+}
+
+// Block-wide inclusive scan of one float per thread (fixed order).
+__device__ float block_incl_scan(float x, float* sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) sh[wave] = x;
+  __syncthreads();
+  float pre = 0.f;
+  for (int w = 0; w < wave; ++w) pre += sh[w];
+  __syncthreads();
+  return pre + x;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void sample_kernel(AccParams p) {
+  __shared__ float sh[kThreads / 64];
+  __shared__ int s_last, s_tok, s_chunk, s_full;
+  __shared__ float s_rem;
+  const int b = blockIdx.y;
+  const int chunk = blockIdx.x;
+  const int tid = threadIdx.x;
+  const float* d = p.dec + (int64_t)b * 8;
+  const int j = __float_as_int(d[0]);
+  int mode = __float_as_int(d[1]);
+  const float Mt = d[2], iZt = d[3], Md = d[4], iZd = d[5];
+  const int64_t to = trow(p, b, j);
+  const int64_t dof = mode == 0 ? drow(p, b, j) : 0;
+
+  // ---- chunk sum of the weights (coalesced, any order) ----
+  const int v0 = chunk * p.cs2;
+  const int v1 = min(p.V, v0 + p.cs2);
+  float acc = 0.f;
+  for (int v = v0 + tid; v < v1; v += kThreads) acc += weight<T>(p, to, dof, mode, Mt, iZt, Md, iZd, v);
+  acc = wave_sum(acc);
+  if ((tid & 63) == 0) sh[tid >> 6] = acc;
+  __syncthreads();
+  if (tid == 0) {
+    float t = 0.f;
+    for (int w = 0; w < kThreads / 64; ++w) t += sh[w];
+    p.psum[(int64_t)b * p.nch2 + chunk] = t;
+  }
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) s_last = atomicAdd(&p.cnt_b[b], 1) == p.nch2 - 1;
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+
+  // ---- last workgroup: pick the chunk, then the token ----
+  if (tid == 0) {
+    const float* ps = p.psum + (int64_t)b * p.nch2;
+    float tot = 0.f;
+    for (int c = 0; c < p.nch2; ++c) tot += ps[c];
+    s_full = 0;
+    if (tot > 0.f) {
+      const float target = p.u[(int64_t)b * (p.k + 1) + p.k] * tot;
+      float pre = 0.f;
+      int cs = -1, lastnz = -1;
+      for (int c = 0; c < p.nch2; ++c) {
+        if (ps[c] > 0.f) lastnz = c;
+        if (cs < 0 && pre + ps[c] > target) {
+          cs = c;
+          s_rem = target - pre;
+        }
+        pre += ps[c];
+      }
+      if (cs < 0) {
+        cs = lastnz;
+        s_rem = INFINITY;  // take the last positive weight of that chunk
+      }
+      s_chunk = cs;
+    } else {
+      // residual summed to zero: sample the target row itself over the whole
+      // vocabulary (mirrors speculative.py:163-169)
+      s_full = 1;
+    }
+  }
+  __syncthreads();
+  int a, e;
+  if (s_full) {
+    mode = 1;
+    a = 0;
+    e = p.V;
+  } else {
+    a = s_chunk * p.cs2;
+    e = min(p.V, a + p.cs2);
+  }
+  // per-thread contiguous runs, sequential sums, block scan (fixed order)
+  const int R = (e - a + kThreads - 1) / kThreads;
+  const int ra = min(e, a + tid * R), rb = min(e, ra + R);
+  float run = 0.f;
+  for (int v = ra; v < rb; ++v) run += weight<T>(p, to, dof, mode, Mt, iZt, Md, iZd, v);
+  const float incl = block_incl_scan(run, sh);
+  const float excl = incl - run;
+  if (s_full && tid == kThreads - 1) {
+    s_rem = p.u[(int64_t)b * (p.k + 1) + p.k] * incl;
+  }
+  if (tid == 0) s_tok = -1;
+  __syncthreads();
+  const float rem = s_rem;
+  if (run > 0.f && incl > rem && !(excl > rem)) {
+    // recompute the prefix in the same order as `run`
+    float cum = 0.f;
+    for (int v = ra; v < rb; ++v) {
+      cum += weight<T>(p, to, dof, mode, Mt, iZt, Md, iZd, v);
+      if (excl + cum > rem) {
+        atomicMax(&s_tok, v);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+  if (s_tok < 0) {
+    // rounding left no crossing: last positive weight in the range
+    int last = -1;
+    for (int v = rb - 1; v >= ra; --v) {
+      if (weight<T>(p, to, dof, mode, Mt, iZt, Md, iZd, v) > 0.f) {
+        last = v;
+        break;
+      }
+    }
+    atomicMax(&s_tok, last);
+    __syncthreads();
+  }
+  if (tid == 0) {
+    p.emitted[(int64_t)b * (p.k + 1) + j] = s_tok;
+    p.cnt_b[b] = 0;
+  }
+}
+
+struct Layout {
+  int rows, nch, cs, nch2, cs2;
+  int64_t stats_off, dec_off, psum_off, total;
+};
+
+Layout layout(int B, int k, int V, bool greedy) {
+  Layout L;
+  L.rows = B * (k + 1) + (greedy ? 0 : B * k);
+  const int max_ch = std::max(1, std::min(kMaxChunks, (V + 2047) / 2048));
+  L.nch = std::max(1, std::min(max_ch, (kTargetWgs + L.rows - 1) / std::max(1, L.rows)));
+  L.cs = ((V + L.nch - 1) / L.nch + 7) / 8 * 8;
+  L.nch = (V + L.cs - 1) / L.cs;
+  L.nch2 = std::max(1, std::min(max_ch, (kTargetWgs + B - 1) / std::max(1, B)));
+  L.cs2 = ((V + L.nch2 - 1) / L.nch2 + 7) / 8 * 8;
+  L.nch2 = (V + L.cs2 - 1) / L.cs2;
+  auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
+  // stats sized for the stochastic row count so one workspace serves both modes
+  const int rows_max = B * (2 * k + 1);
+  L.stats_off = kFlagBytes + kCounterBytes;
+  L.dec_off = L.stats_off + al((int64_t)rows_max * kMaxChunks * 8);
+  L.psum_off = L.dec_off + al((int64_t)B * 8 * 4);
+  L.total = L.psum_off + al((int64_t)B * kMaxChunks * 4);
+  return L;
+}
+
+template <typename T>
+int32_t launch_accept(const AccParams& p, int rows, hipStream_t s) {
+  dim3 g1(p.nch, rows);
+  if (p.greedy) {
+    hipLaunchKernelGGL((stats_kernel<T, true>), g1, dim3(kThreads), 0, s, p);
+    return launch_status("stats_kernel");
+  }
+  hipLaunchKernelGGL((stats_kernel<T, false>), g1, dim3(kThreads), 0, s, p);
+  int32_t rc = launch_status("stats_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL((sample_kernel<T>), dim3(p.nch2, p.B), dim3(kThreads), 0, s, p);
+  return launch_status("sample_kernel");
+}
+
+}  // namespace
+}  // namespace nsg
+
+using namespace nsg;
+
+extern "C" int64_t nsg_spec_accept_workspace_bytes(int32_t batch, int32_t k, int32_t vocab) {
+  if (batch < 0 || k < 0 || vocab <= 0) return -1;
+  return layout(batch, k, vocab, false).total;
+}
+
+extern "C" int32_t nsg_spec_accept(const void* target_logits, int64_t target_req_stride,
+                                   int64_t target_row_stride, const void* draft_logits,
+                                   int64_t draft_req_stride, int64_t draft_row_stride,
+                                   int32_t logits_dtype, const int64_t* draft_tokens,
+                                   const float* uniforms, int32_t batch, int32_t k,
+                                   int32_t vocab, float temperature, const int32_t* kv_indptr,
+                                   const int32_t* kv_indices, const int32_t* start_pos,
+                                   int32_t page_size, int32_t* num_emitted, int64_t* emitted,
+                                   int64_t* rollback_slots, void* workspace,
+                                   int64_t workspace_bytes, nsg_stream_t stream) {
+  NSG_CHECK_ARG(batch >= 0 && batch <= kMaxBatch, "batch %d outside [0, %d]", batch, kMaxBatch);
+  NSG_CHECK_ARG(k >= 0 && k <= kMaxK, "k %d outside [0, %d]", k, kMaxK);
+  NSG_CHECK_ARG(vocab > 0, "vocab %d", vocab);
+  NSG_CHECK_ARG(logits_dtype == 0 || logits_dtype == 1, "logits_dtype %d (0 bf16, 1 fp32)",
+                logits_dtype);
+  if (batch == 0) {
+    clear_error();
+    return NSG_OK;
+  }
+  const bool greedy = temperature < 1e-6f;
+  NSG_CHECK_ARG(target_logits && num_emitted && emitted && workspace, "null pointer argument");
+  NSG_CHECK_ARG(greedy || k == 0 || draft_logits, "draft_logits required when temperature > 0");
+  NSG_CHECK_ARG(k == 0 || draft_tokens, "draft_tokens required when k > 0");
+  NSG_CHECK_ARG(greedy || uniforms, "uniforms required when temperature > 0");
+  NSG_CHECK_ARG(target_row_stride >= vocab && target_req_stride >= (int64_t)(k + 1) * vocab,
+                "target logits strides too small");
+  NSG_CHECK_ARG(greedy || k == 0 || (draft_row_stride >= vocab &&
+                                     draft_req_stride >= (int64_t)k * vocab),
+                "draft logits strides too small");
+  int log2P = 0;
+  if (rollback_slots && k > 0) {
+    NSG_CHECK_ARG(kv_indptr && kv_indices && start_pos,
+                  "rollback slots need kv_indptr, kv_indices and start_pos");
+    NSG_CHECK_ARG(page_size > 0 && (page_size & (page_size - 1)) == 0,
+                  "page_size %d must be a power of two", page_size);
+    while ((1 << log2P) < page_size) ++log2P;
+  }
+  const Layout L = layout(batch, k, vocab, greedy);
+  if (workspace_bytes < L.total) {
+    set_error("workspace has %lld bytes, needs %lld", (long long)workspace_bytes,
+              (long long)L.total);
+    return NSG_ERR_WORKSPACE;
+  }
+  AccParams p;
+  p.tl = target_logits;
+  p.t_req = target_req_stride;
+  p.t_row = target_row_stride;
+  p.dl = draft_logits;
+  p.d_req = draft_req_stride;
+  p.d_row = draft_row_stride;
+  p.dtok = draft_tokens;
+  p.u = uniforms;
+  p.B = batch;
+  p.k = k;
+  p.V = vocab;
+  p.c = greedy ? 0.f : kLog2e / temperature;
+  p.greedy = greedy ? 1 : 0;
+  p.kv_indptr = kv_indptr;
+  p.kv_indices = kv_indices;
+  p.start_pos = start_pos;
+  p.log2P = log2P;
+  p.n_out = num_emitted;
+  p.emitted = emitted;
+  p.rollback = k > 0 ? rollback_slots : nullptr;
+  p.nch = L.nch;
+  p.cs = L.cs;
+  p.nch2 = L.nch2;
+  p.cs2 = L.cs2;
+  char* ws = static_cast<char*>(workspace);
+  p.flags = reinterpret_cast<int*>(ws);
+  p.cnt_a = reinterpret_cast<int*>(ws + kFlagBytes);
+  p.cnt_b = p.cnt_a + kMaxBatch;
+  p.stats = reinterpret_cast<float2*>(ws + L.stats_off);
+  p.dec = reinterpret_cast<float*>(ws + L.dec_off);
+  p.psum = reinterpret_cast<float*>(ws + L.psum_off);
+  // 16-byte vector loads need 16-byte aligned bases; rows are checked per row
+  const uintptr_t mis = reinterpret_cast<uintptr_t>(target_logits) |
+                        (greedy ? 0 : reinterpret_cast<uintptr_t>(draft_logits));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (logits_dtype == 0) {
+    if (mis & 15) {
+      set_error("logits base pointers must be 16-byte aligned");
+      return NSG_ERR_ARG;
+    }
+    return launch_accept<bf16>(p, L.rows, s);
+  }
+  if (mis & 15) {
+    set_error("logits base pointers must be 16-byte aligned");
+    return NSG_ERR_ARG;
+  }
+  return launch_accept<float>(p, L.rows, s);
+}

@@ -1,0 +1,327 @@
+"""PyTorch-facing wrappers of the verify-step C ABI (include/nsg_spec.h).
+
+torch supplies device memory and the current HIP stream only; every
+computation runs in the HIP kernels of libnsg_spec.so.  Nothing here falls
+back to PyTorch or the CPU: a missing library or a non-GPU tensor raises.
+
+* :class:`BatchPrefillWithPagedKVCacheWrapper` -- drop-in for the FlashInfer
+  wrapper the reference uses for paged attention (constructed at
+  nano_sglang/engine/engine.py:106-108, planned at engine.py:451-462, run at
+  nano_sglang/model/causal_lm.py:340).
+* :func:`spec_accept` -- fused acceptance / resample / bonus / rollback slots,
+  replacing the loop at nano_sglang/decode/speculative.py:130-184.
+* :func:`kv_write` -- replaces the index_put scatter at causal_lm.py:335-338.
+* :func:`kv_clear_slots`, :func:`philox_uniform`.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+import numpy as np
+import torch
+
+from . import _native
+from ._native import NSG_ATTN_WORK_INTS, AttnPlan, check
+
+MI355X_CUS = 256
+
+
+def _lib():
+    return _native.load()
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_gpu(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a GPU tensor (no CPU path exists)")
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _host_i32(t) -> np.ndarray:
+    if isinstance(t, torch.Tensor):
+        t = t.detach().to("cpu", torch.int32)
+        return np.ascontiguousarray(t.numpy())
+    return np.ascontiguousarray(np.asarray(t, dtype=np.int32))
+
+
+def _dev_i32(t, device) -> torch.Tensor:
+    if isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == torch.int32 and t.is_contiguous():
+        return t
+    if isinstance(t, np.ndarray):
+        t = torch.from_numpy(np.ascontiguousarray(t, dtype=np.int32))
+    return torch.as_tensor(t, dtype=torch.int32).contiguous().to(device, non_blocking=True)
+
+
+class BatchPrefillWithPagedKVCacheWrapper:
+    """Ragged multi-query attention over an NHD paged KV cache.
+
+    Same constructor / plan / run shape as the FlashInfer wrapper the
+    reference calls (engine.py:106-108, 451-462; causal_lm.py:340):
+
+    >>> w = BatchPrefillWithPagedKVCacheWrapper(workspace_u8, kv_layout="NHD")
+    >>> w.plan(qo_indptr, kv_indptr, kv_indices, kv_last_page_len,
+    ...        num_qo_heads, num_kv_heads, head_dim, page_size, causal=True)
+    >>> out = w.run(q, (k_cache[layer], v_cache[layer]))
+
+    ``plan`` reads the CSR metadata on the host once per step; ``run`` enqueues
+    one kernel per layer on the current stream and never syncs the host.
+    The workspace is zero-filled here once; the kernel leaves it reusable.
+    """
+
+    def __init__(self, float_workspace_buffer: torch.Tensor, kv_layout: str = "NHD",
+                 num_cus: int = MI355X_CUS):
+        if kv_layout != "NHD":
+            raise ValueError(f"kv_layout {kv_layout!r}: only 'NHD' (the reference's layout)")
+        _require_gpu(float_workspace_buffer, "workspace")
+        self._ws = float_workspace_buffer
+        self._ws.zero_()
+        self._device = float_workspace_buffer.device
+        self._num_cus = num_cus
+        self._work_cap = 0
+        self._work_d: torch.Tensor | None = None
+        self._work_h = np.zeros(0, np.int32)
+        self._plan: AttnPlan | None = None
+
+    def plan(self, qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len,
+             num_qo_heads: int, num_kv_heads: int, head_dim_qk: int, page_size: int,
+             causal: bool = True, q_data_type=torch.bfloat16, sm_scale: float | None = None):
+        if q_data_type not in (torch.bfloat16, "bfloat16"):
+            raise NotImplementedError(f"q_data_type {q_data_type}: the kernel is bf16")
+        qo_h = _host_i32(qo_indptr)
+        kvp_h = _host_i32(paged_kv_indptr)
+        last_h = _host_i32(paged_kv_last_page_len)
+        B = len(qo_h) - 1
+        if len(kvp_h) != B + 1 or len(last_h) != B:
+            raise ValueError("qo_indptr, paged_kv_indptr and last_page_len disagree on batch")
+        lib = _lib()
+        # an upper bound on work items: every query tile split into every 32-token step
+        bound = 0
+        G = max(1, num_qo_heads // max(1, num_kv_heads))
+        T = max(1, min(64 // G, int(np.diff(qo_h).max(initial=1))))
+        for b in range(B):
+            ql = int(qo_h[b + 1] - qo_h[b])
+            npg = int(kvp_h[b + 1] - kvp_h[b])
+            L = (npg - 1) * page_size + int(last_h[b]) if npg else 0
+            bound += math.ceil(ql / T) * max(1, math.ceil(L / 32))
+        if bound > self._work_cap:
+            self._work_cap = max(bound, 2 * self._work_cap, 64)
+            self._work_h = np.zeros(self._work_cap * NSG_ATTN_WORK_INTS, np.int32)
+            self._work_d = torch.empty(self._work_cap * NSG_ATTN_WORK_INTS, dtype=torch.int32,
+                                       device=self._device)
+        pl = AttnPlan()
+        rc = lib.nsg_attn_plan(qo_h.ctypes.data, kvp_h.ctypes.data, last_h.ctypes.data, B,
+                               num_qo_heads, num_kv_heads, head_dim_qk, page_size,
+                               1 if causal else 0, self._num_cus, self._work_h.ctypes.data,
+                               self._work_cap, C.byref(pl))
+        check(rc, "nsg_attn_plan")
+        if pl.workspace_bytes > self._ws.numel() * self._ws.element_size():
+            raise RuntimeError(
+                f"attention workspace too small: plan needs {pl.workspace_bytes} bytes, "
+                f"buffer has {self._ws.numel() * self._ws.element_size()}")
+        n = pl.num_work * NSG_ATTN_WORK_INTS
+        if n:
+            self._work_d[:n].copy_(torch.from_numpy(self._work_h[:n]), non_blocking=False)
+        self._plan = pl
+        self._qo_indptr = _dev_i32(qo_indptr, self._device)
+        self._kv_indptr = _dev_i32(paged_kv_indptr, self._device)
+        self._kv_indices = _dev_i32(paged_kv_indices, self._device)
+        self._kv_last = _dev_i32(paged_kv_last_page_len, self._device)
+        self._total_q = int(qo_h[-1])
+        self._page_size = page_size
+        self._causal = causal
+        self._sm_scale = (1.0 / math.sqrt(head_dim_qk)) if sm_scale is None else float(sm_scale)
+        self._dims = (num_qo_heads, num_kv_heads, head_dim_qk)
+
+    @property
+    def plan_info(self) -> AttnPlan:
+        return self._plan
+
+    def run(self, q: torch.Tensor, paged_kv_cache, out: torch.Tensor | None = None) -> torch.Tensor:
+        if self._plan is None:
+            raise RuntimeError("run() before plan()")
+        k_cache, v_cache = paged_kv_cache
+        Hq, Hkv, D = self._dims
+        for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
+            _require_gpu(t, name)
+            if t.dtype != torch.bfloat16:
+                raise TypeError(f"{name} must be bfloat16, got {t.dtype}")
+            if not t.is_contiguous():
+                raise ValueError(f"{name} must be contiguous")
+        if tuple(q.shape) != (self._total_q, Hq, D):
+            raise ValueError(f"q shape {tuple(q.shape)} != planned {(self._total_q, Hq, D)}")
+        if (k_cache.dim() != 4 or k_cache.shape[1] != self._page_size or k_cache.shape[2] != Hkv
+                or k_cache.shape[3] != D or v_cache.shape != k_cache.shape):
+            raise ValueError(f"KV cache shape {tuple(k_cache.shape)} is not "
+                             f"[pages, {self._page_size}, {Hkv}, {D}]")
+        if out is None:
+            out = torch.empty_like(q)
+        rc = _lib().nsg_attn_run(
+            C.byref(self._plan), self._work_d.data_ptr(), q.data_ptr(), k_cache.data_ptr(),
+            v_cache.data_ptr(), out.data_ptr(), self._qo_indptr.data_ptr(),
+            self._kv_indptr.data_ptr(), self._kv_indices.data_ptr(), self._kv_last.data_ptr(),
+            self._page_size, k_cache.shape[0], self._sm_scale, 1 if self._causal else 0,
+            self._ws.data_ptr(), self._ws.numel() * self._ws.element_size(),
+            _stream_ptr(q.device))
+        check(rc, "nsg_attn_run")
+        return out
+
+    def check_flags(self) -> int:
+        """Synchronises and returns (then clears) the kernel's error flags."""
+        f = C.c_int32(0)
+        check(_lib().nsg_attn_check_flags(self._ws.data_ptr(), C.byref(f),
+                                          _stream_ptr(self._device)), "nsg_attn_check_flags")
+        return f.value
+
+
+class AcceptWorkspace:
+    """Device scratch of :func:`spec_accept` (zero-filled once, grown on demand).
+    Calls that share one workspace must not overlap on different streams."""
+
+    def __init__(self, device):
+        self.device = torch.device(device)
+        self.buf = torch.zeros(0, dtype=torch.uint8, device=self.device)
+
+    def get(self, nbytes: int) -> torch.Tensor:
+        if self.buf.numel() < nbytes:
+            self.buf = torch.zeros(max(nbytes, 2 * self.buf.numel()), dtype=torch.uint8,
+                                   device=self.device)
+        return self.buf
+
+
+_default_ws: dict[torch.device, AcceptWorkspace] = {}
+
+
+def _accept_ws(device) -> AcceptWorkspace:
+    device = torch.device(device)
+    if device not in _default_ws:
+        _default_ws[device] = AcceptWorkspace(device)
+    return _default_ws[device]
+
+
+def spec_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor | None,
+                draft_tokens: torch.Tensor | None, uniforms: torch.Tensor | None,
+                temperature: float, kv_indptr: torch.Tensor | None = None,
+                kv_indices: torch.Tensor | None = None, start_pos: torch.Tensor | None = None,
+                page_size: int = 16, workspace: AcceptWorkspace | None = None,
+                out: tuple | None = None):
+    """Fused verify-step acceptance for B requests (C ABI: nsg_spec_accept).
+
+    target_logits (B, k+1, V) and draft_logits (B, k, V) in bf16 or fp32 with a
+    unit stride along V; draft_tokens int64 (B, k); uniforms fp32 (B, k+1).
+    Greedy when ``temperature < 1e-6`` (draft_logits / uniforms may be None).
+    Returns (num_emitted int32 (B,), emitted int64 (B, k+1) padded -1,
+    rollback_slots int64 (B, k) padded -1).
+    """
+    _require_gpu(target_logits, "target_logits")
+    dev = target_logits.device
+    if target_logits.dim() != 3:
+        raise ValueError("target_logits must be (B, k+1, V)")
+    B, k1, V = target_logits.shape
+    k = k1 - 1
+    dt = {torch.bfloat16: 0, torch.float32: 1}.get(target_logits.dtype)
+    if dt is None:
+        raise TypeError(f"logits dtype {target_logits.dtype}: bf16 or fp32")
+    if target_logits.stride(2) != 1:
+        raise ValueError("target_logits must be contiguous along the vocabulary")
+    greedy = temperature < 1e-6
+    if not greedy and k > 0:
+        if draft_logits is None:
+            raise ValueError("draft_logits required when temperature > 0")
+        _require_gpu(draft_logits, "draft_logits")
+        if draft_logits.dtype != target_logits.dtype or tuple(draft_logits.shape) != (B, k, V):
+            raise ValueError("draft_logits must match target_logits' dtype with shape (B, k, V)")
+        if draft_logits.stride(2) != 1:
+            raise ValueError("draft_logits must be contiguous along the vocabulary")
+        d_req, d_row = draft_logits.stride(0), draft_logits.stride(1)
+    else:
+        draft_logits, d_req, d_row = None, 0, 0
+    if k > 0:
+        if draft_tokens is None or tuple(draft_tokens.shape) != (B, k):
+            raise ValueError("draft_tokens must be (B, k)")
+        _require_gpu(draft_tokens, "draft_tokens")
+        draft_tokens = draft_tokens.to(torch.int64).contiguous()
+    if not greedy:
+        if uniforms is None or tuple(uniforms.shape) != (B, k + 1):
+            raise ValueError("uniforms must be (B, k+1) float32")
+        _require_gpu(uniforms, "uniforms")
+        uniforms = uniforms.to(torch.float32).contiguous()
+    rb_ok = kv_indptr is not None and k > 0
+    if rb_ok:
+        for name, t in (("kv_indptr", kv_indptr), ("kv_indices", kv_indices),
+                        ("start_pos", start_pos)):
+            if t is None:
+                raise ValueError(f"{name} required for rollback slots")
+            _require_gpu(t, name)
+        kv_indptr = kv_indptr.to(torch.int32).contiguous()
+        kv_indices = kv_indices.to(torch.int32).contiguous()
+        start_pos = start_pos.to(torch.int32).contiguous()
+    if out is None:
+        n_out = torch.empty(B, dtype=torch.int32, device=dev)
+        emitted = torch.empty(B, k + 1, dtype=torch.int64, device=dev)
+        rollback = torch.full((B, k), -1, dtype=torch.int64, device=dev)
+    else:
+        n_out, emitted, rollback = out
+    lib = _lib()
+    need = lib.nsg_spec_accept_workspace_bytes(B, k, V)
+    ws = (workspace or _accept_ws(dev)).get(need)
+    rc = lib.nsg_spec_accept(
+        target_logits.data_ptr(), target_logits.stride(0), target_logits.stride(1),
+        _ptr(draft_logits), d_req, d_row, dt, _ptr(draft_tokens) if k > 0 else None,
+        _ptr(uniforms) if not greedy else None, B, k, V, float(temperature),
+        _ptr(kv_indptr) if rb_ok else None, _ptr(kv_indices) if rb_ok else None,
+        _ptr(start_pos) if rb_ok else None, page_size, n_out.data_ptr(), emitted.data_ptr(),
+        rollback.data_ptr() if rb_ok else None, ws.data_ptr(), ws.numel(), _stream_ptr(dev))
+    check(rc, "nsg_spec_accept")
+    return n_out, emitted, rollback
+
+
+def kv_write(k: torch.Tensor, v: torch.Tensor, slots: torch.Tensor, k_cache: torch.Tensor,
+             v_cache: torch.Tensor) -> None:
+    """k, v: (T, Hkv, D) bf16 (rows may be strided views); slots int64 (T,);
+    caches: one layer's (N, P, Hkv, D) pool."""
+    for name, t in (("k", k), ("v", v), ("slots", slots), ("k_cache", k_cache),
+                    ("v_cache", v_cache)):
+        _require_gpu(t, name)
+    T, Hkv, D = k.shape
+    if v.shape != k.shape or v.stride() != k.stride():
+        raise ValueError("k and v must have the same shape and strides")
+    if k.stride(2) != 1 or k.stride(1) != D:
+        raise ValueError("each K/V row must be a contiguous (Hkv, D) block")
+    if k_cache.dtype != torch.bfloat16 or k.dtype != torch.bfloat16:
+        raise TypeError("K/V and caches must be bfloat16")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous")
+    if k_cache.shape[-2:] != (Hkv, D):
+        raise ValueError("cache head layout does not match K/V")
+    slots = slots.to(torch.int64).contiguous()
+    num_slots = k_cache.numel() // (Hkv * D)
+    check(_lib().nsg_kv_write(k.data_ptr(), v.data_ptr(), k.stride(0), slots.data_ptr(), T,
+                              k_cache.data_ptr(), v_cache.data_ptr(), Hkv, D, num_slots,
+                              _stream_ptr(k.device)), "nsg_kv_write")
+
+
+def kv_clear_slots(slots: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
+    """Zero flat slots in every layer of (L, N, P, Hkv, D) pools."""
+    _require_gpu(slots, "slots")
+    L, N, P, Hkv, D = k_cache.shape
+    slots = slots.reshape(-1).to(torch.int64).contiguous()
+    check(_lib().nsg_kv_clear_slots(slots.data_ptr(), slots.numel(), k_cache.data_ptr(),
+                                    v_cache.data_ptr(), L, N * P * Hkv * D, Hkv, D, N * P,
+                                    _stream_ptr(k_cache.device)), "nsg_kv_clear_slots")
+
+
+def philox_uniform(seed: int, stream_id: int, offset: int, n: int, device) -> torch.Tensor:
+    """n float32 uniforms of Philox4x32-10 stream ``stream_id`` (see nsg_spec.h)."""
+    out = torch.empty(n, dtype=torch.float32, device=device)
+    _require_gpu(out, "out")
+    check(_lib().nsg_philox_uniform(seed, stream_id, offset, n, out.data_ptr(),
+                                    _stream_ptr(out.device)), "nsg_philox_uniform")
+    return out

@@ -151,6 +151,8 @@ def spec_accept(target_logits, draft_logits, draft_tokens, uniforms, temperature
     emitted = np.full((B, k + 1), -1, np.int64)
     rb = np.full((B, max(k, 1)), -1, np.int64)[:, :k]
     margin = np.full(B, np.inf)
+    if uniforms is None:  # greedy needs none
+        uniforms = np.zeros((B, k + 1), np.float32)
     for b in range(B):
         dl = None if draft_logits is None else np.asarray(draft_logits[b])
         out, m = accept_request(target_logits[b], dl, np.asarray(draft_tokens[b]),

@@ -1,0 +1,146 @@
+"""GPU parity of the verify-attention kernel (C ABI via the host wrapper)
+against the float64 oracle on identical seeded inputs.
+
+Bounds: max |gpu - oracle| <= 2e-2 (the stated bf16 bound) and, per element,
+the tighter |gpu - oracle| <= 2e-3 + 2^-8 |oracle| (bf16 output rounding is at
+most 2^-9 relative), which the kernel must also meet: |out| is only ~0.03 at
+the verify shapes, so 2e-2 alone would not catch a wrong page or mask.
+"""
+import numpy as np
+import pytest
+import torch
+
+from nanosglang_amd import workloads
+from oracle.verify_attention import verify_attention
+
+pytestmark = pytest.mark.gpu
+TOL_SPEC, TOL_TIGHT = 2e-2, 2e-3
+
+
+def _dev(x, dtype=torch.bfloat16):
+    return torch.from_numpy(np.ascontiguousarray(x)).to("cuda").to(dtype)
+
+
+def _gpu_attention(c, Hq, Hkv, D, causal=True, num_cus=256):
+    from nanosglang_amd.kernels import BatchPrefillWithPagedKVCacheWrapper
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    w = BatchPrefillWithPagedKVCacheWrapper(ws, "NHD", num_cus=num_cus)
+    w.plan(torch.from_numpy(c["qo_indptr"]), torch.from_numpy(c["kv_indptr"]),
+           torch.from_numpy(c["kv_indices"]), torch.from_numpy(c["kv_last_page_len"]),
+           Hq, Hkv, D, c["page_size"], causal=causal)
+    out = w.run(_dev(c["q"]), (_dev(c["k"]), _dev(c["v"])))
+    torch.cuda.synchronize()
+    flags = w.check_flags()
+    return out.float().cpu().numpy(), flags, w.plan_info
+
+
+def _oracle(c, causal=True):
+    return verify_attention(c["q"], c["k"], c["v"], c["qo_indptr"], c["kv_indptr"],
+                            c["kv_indices"], c["kv_last_page_len"], c["sm_scale"], causal)
+
+
+def _check(c, Hq, Hkv, D, causal=True, **kw):
+    print(f"case: B={len(c['q_lens'])} q_lens={sorted(set(c['q_lens'].tolist()))[:4]} "
+          f"Hq={Hq} Hkv={Hkv} D={D} causal={causal}", flush=True)
+    got, flags, plan = _gpu_attention(c, Hq, Hkv, D, causal, **kw)
+    ref = _oracle(c, causal)
+    err = np.abs(got - ref).max()
+    print(f"  max abs err {err:.3e}  |ref| max {np.abs(ref).max():.3e}  "
+          f"work={plan.num_work} splits<={plan.max_splits} rt={plan.row_tiles}", flush=True)
+    assert flags == 0
+    assert np.isfinite(got).all()
+    assert err <= TOL_SPEC
+    assert (np.abs(got - ref) <= TOL_TIGHT + 2.0 ** -8 * np.abs(ref)).all()
+    return plan
+
+
+def test_verify_c2_shape_small_pool():
+    c = workloads.verify_attention_batch(batch=4, num_pages=200, seed=1)
+    _check(c, 14, 2, 64)
+
+
+def test_verify_c2_full():
+    c = workloads.verify_attention_batch(seed=0)   # 32 x 5 queries, 14/2 heads, D=64
+    plan = _check(c, 14, 2, 64)
+    assert plan.max_splits > 1   # exercises the cross-split merge
+
+
+def test_verify_c2_single_split():
+    c = workloads.verify_attention_batch(batch=8, num_pages=400, seed=2)
+    _check(c, 14, 2, 64, num_cus=1)
+
+
+def test_verify_large_shape_d128():
+    c = workloads.verify_attention_batch(batch=6, q_len=9, num_qo_heads=32, num_kv_heads=8,
+                                         head_dim=128, min_len=2048, max_len=4096,
+                                         num_pages=1600, seed=3)
+    _check(c, 32, 8, 128)
+
+
+def test_decode_q1():
+    c = workloads.verify_attention_batch(batch=16, q_len=1, num_pages=800, seed=4)
+    _check(c, 14, 2, 64)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_ragged_prefill(causal):
+    kv = [17, 300, 64, 129, 512]
+    ql = [17, 120, 1, 5, 300]
+    c = workloads.verify_attention_batch(batch=5, kv_lens=kv, q_lens=ql, num_pages=120, seed=5)
+    _check(c, 14, 2, 64, causal=causal)
+
+
+def test_partial_and_full_pages_and_tiny():
+    kv = [5, 16, 32, 33, 1, 6]
+    ql = [5, 5, 5, 5, 1, 6]
+    c = workloads.verify_attention_batch(batch=6, kv_lens=kv, q_lens=ql, num_pages=40, seed=6)
+    _check(c, 14, 2, 64)
+
+
+@pytest.mark.parametrize("page_size", [8, 32, 64])
+def test_other_page_sizes(page_size):
+    c = workloads.verify_attention_batch(batch=5, page_size=page_size,
+                                         num_pages=40000 // page_size, seed=7)
+    _check(c, 14, 2, 64)
+
+
+def test_mha_and_group8():
+    c = workloads.verify_attention_batch(batch=3, q_len=5, num_qo_heads=4, num_kv_heads=4,
+                                         num_pages=150, seed=8)
+    _check(c, 4, 4, 64)
+    c = workloads.verify_attention_batch(batch=3, q_len=9, num_qo_heads=16, num_kv_heads=2,
+                                         head_dim=128, num_pages=150, seed=9)
+    _check(c, 16, 2, 128)
+
+
+def test_page_permutation_gives_identical_output():
+    c = workloads.verify_attention_batch(batch=4, num_pages=300, seed=10)
+    a, _, _ = _gpu_attention(c, 14, 2, 64)
+    perm = np.random.default_rng(1).permutation(300)
+    k2 = np.empty_like(c["k"]); v2 = np.empty_like(c["v"])
+    k2[perm] = c["k"]; v2[perm] = c["v"]
+    c2 = dict(c, k=k2, v=v2, kv_indices=perm[c["kv_indices"]].astype(np.int32))
+    b, _, _ = _gpu_attention(c2, 14, 2, 64)
+    assert np.array_equal(a, b)
+
+
+def test_out_of_range_page_is_flagged_not_read():
+    c = workloads.verify_attention_batch(batch=2, num_pages=100, seed=11)
+    c["kv_indices"] = c["kv_indices"].copy()
+    c["kv_indices"][3] = 100          # one past the pool: must read as zeros
+    got, flags, _ = _gpu_attention(c, 14, 2, 64)
+    assert flags & 1
+    assert np.isfinite(got).all()
+
+
+def test_bad_arguments_raise():
+    from nanosglang_amd.kernels import BatchPrefillWithPagedKVCacheWrapper
+    from nanosglang_amd._native import NativeError
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    w = BatchPrefillWithPagedKVCacheWrapper(ws)
+    with pytest.raises(NativeError):
+        w.plan([0, 5], [0, 1], [0], [3], 14, 2, 64, 16)      # L=3 < q_len=5 (causal)
+    with pytest.raises(NativeError):
+        w.plan([0, 1], [0, 1], [0], [3], 14, 2, 96, 16)      # head_dim 96
+    with pytest.raises(NativeError):
+        w.plan([0, 1], [0, 1], [0], [3], 14, 3, 64, 16)      # 14 % 3

@@ -133,3 +133,9 @@ def test_batched_matches_per_request():
         assert res["num_emitted"][b] == len(out)
         assert res["emitted"][b, :len(out)].tolist() == out
         assert (res["emitted"][b, len(out):] == -1).all()
+
+
+def test_greedy_batched_needs_no_uniforms():
+    t = np.zeros((2, 3, 5)); t[:, :, 1] = 1
+    res = spec_accept(t, None, np.array([[1, 1], [1, 2]]), None, 0.0)
+    assert res["num_emitted"].tolist() == [3, 2]

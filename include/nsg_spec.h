@@ -42,7 +42,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 1
+#define NSG_ABI_VERSION 2
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -59,6 +59,7 @@ int32_t nsg_abi_version(void);
 
 typedef struct {
   int32_t num_work;        /* work items: (request, query tile, KV split)        */
+  int32_t num_merge;       /* query tiles whose KV splits need a merge pass      */
   int32_t num_groups;      /* (request, query tile) pairs                        */
   int32_t row_tiles;       /* 16-row MFMA tiles per work item, 1..4              */
   int32_t q_tile_tokens;   /* query tokens per query tile                        */
@@ -71,8 +72,8 @@ typedef struct {
 
 /* Host-side planner (replaces BatchPrefillWithPagedKVCacheWrapper.plan,
  * engine.py:451-462).  Reads HOST copies of the CSR metadata and writes the
- * work list (num_work * NSG_ATTN_WORK_INTS int32) into work_h, which the
- * caller copies to device memory for nsg_attn_run.  num_cus sizes the KV
+ * work list ((num_work + num_merge) * NSG_ATTN_WORK_INTS int32) into work_h,
+ * which the caller copies to device memory for nsg_attn_run.  num_cus sizes the KV
  * split (256 on MI355X).  head_dim must be 64 or 128; num_qo_heads a multiple
  * of num_kv_heads with a group of at most 64; page_size a power of two. */
 int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
@@ -81,8 +82,8 @@ int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
                       int32_t page_size, int32_t causal, int32_t num_cus,
                       int32_t* work_h, int32_t work_capacity, nsg_attn_plan_t* plan);
 
-/* Device workspace must be zero-filled once before its first use (the kernels
- * leave their counters at zero on exit).  Returns the number of bytes. */
+/* Bytes of device workspace nsg_attn_run needs for this plan (split partials
+ * and an error-flag word, which should start at zero). */
 int64_t nsg_attn_workspace_bytes(const nsg_attn_plan_t* plan);
 
 /* Runs one layer (replaces wrapper.run, causal_lm.py:340).

@@ -13,18 +13,22 @@
 //     (pd == 0 accepts); on rejection sample max(0, pt - pd) (falls back to pt
 //     if that sums to 0) by inverse CDF with u_k; else the bonus from pt_k.
 //
-// Two launches, both bandwidth-bound streaming passes:
-//   stats_kernel  grid (chunks, rows): every target row (and draft row when
+// Launches (no workgroup waits on another inside a launch: on gfx950 that
+// handshake needs agent-scope fences, which write back and invalidate the
+// XCD's L2):
+//   stats_kernel   grid (chunks, rows): every target row (and draft row when
 //     stochastic) is cut into chunks; a workgroup reduces its chunk to
-//     (max, sum exp2) -- or (max, first argmax) when greedy -- with 16-byte
-//     loads and wave-shuffle reductions.  The last workgroup of a request
-//     (atomic counter) combines the chunk stats, runs the k ratio tests and
-//     writes the accepted prefix, the decision and the rollback slots.
-//   sample_kernel grid (chunks, B), stochastic only: chunk sums of the
-//     residual (or bonus) weights over the one decided row pair; the last
-//     workgroup of a request picks the chunk by a sequential prefix and the
-//     token by a block scan over contiguous per-thread runs, so the search
-//     re-reads one chunk only.  These rows were just streamed by stats_kernel.
+//     (max, sum 2^x) -- or (max, first argmax) when greedy -- with 16-byte
+//     loads and wave-shuffle reductions.  This pass streams every logit once.
+//   greedy: finalize_kernel, one wave per request: combine the argmax chunks,
+//     compare with the drafts, write tokens and rollback slots.
+//   stochastic: sum_kernel grid (chunks, B): each workgroup recombines the
+//     (tiny) chunk stats of its request, runs the k ratio tests, and sums the
+//     residual (or bonus) weights of its chunk of the one decided row pair;
+//     select_kernel, one workgroup per request: picks the chunk by a
+//     sequential prefix and the token by a block scan over contiguous
+//     per-thread runs, re-reading one chunk only.  The decided rows were just
+//     streamed by stats_kernel.
 #include <cfloat>
 #include <climits>
 
@@ -39,7 +43,6 @@ constexpr int kMaxBatch = 1 << 14;
 constexpr int kMaxChunks = 64;
 constexpr int kTargetWgs = 2048;
 constexpr int64_t kFlagBytes = 256;
-constexpr int64_t kCounterBytes = 2LL * kMaxBatch * 4;
 constexpr float kLog2e = 1.4426950408889634f;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -64,8 +67,6 @@ struct AccParams {
   int nch, cs;    // stats chunks / chunk size
   int nch2, cs2;  // sample chunks / chunk size
   float2* stats;  // [rows][nch]
-  int* cnt_a;     // [kMaxBatch]
-  int* cnt_b;     // [kMaxBatch]
   float* dec;     // [B][8]
   float* psum;    // [B][nch2]
   int* flags;
@@ -186,95 +187,10 @@ __device__ void write_rollback(const AccParams& p, int b, int n) {
   }
 }
 
-// The decision for request b, run by one wave of the last stats workgroup.
-template <typename T>
-__device__ void decide(const AccParams& p, int b) {
-  const int lane = threadIdx.x & 63;
-  const int k = p.k;
-  int64_t* em = p.emitted + (int64_t)b * (k + 1);
-  if (p.greedy) {
-    int n = k + 1;
-    for (int i = 0; i <= k; ++i) {
-      const int r = b * (k + 1) + i;
-      float v = -INFINITY;
-      int ix = INT_MAX;
-      for (int c = lane; c < p.nch; c += 64) {
-        const float2 st = p.stats[(int64_t)r * p.nch + c];
-        am_merge(v, ix, st.x, __float_as_int(st.y));
-      }
-      wave_am(v, ix);
-      if (lane == 0) {
-        if (i < k && p.dtok[(int64_t)b * k + i] == (int64_t)ix) {
-          em[i] = ix;
-        } else {
-          em[i] = ix;
-          n = i + 1;
-        }
-      }
-      n = __shfl(n, 0, 64);
-      if (n == i + 1) break;
-    }
-    if (lane == 0) {
-      for (int i = n; i <= k; ++i) em[i] = -1;
-      p.n_out[b] = n;
-      write_rollback(p, b, n);
-    }
-    return;
-  }
-  // stochastic: normalisers of target rows 0..k and draft rows 0..k-1
-  __shared__ float sM[2 * kMaxK + 1], sZ[2 * kMaxK + 1];
-  for (int i = 0; i < 2 * k + 1; ++i) {
-    const int r = i <= k ? b * (k + 1) + i : p.B * (k + 1) + b * k + (i - k - 1);
-    float m = -INFINITY, s = 0.f;
-    for (int c = lane; c < p.nch; c += 64) {
-      const float2 st = p.stats[(int64_t)r * p.nch + c];
-      ms_merge(m, s, st.x, st.y);
-    }
-    wave_ms(m, s);
-    if (lane == 0) {
-      sM[i] = m;
-      sZ[i] = s;
-    }
-  }
-  if (lane != 0) return;
-  int j = k;  // first rejected position, k = none
-  for (int i = 0; i < k; ++i) {
-    const int64_t x = p.dtok[(int64_t)b * k + i];
-    bool acc;
-    if (x < 0 || x >= p.V) {
-      atomicOr(p.flags, 4);
-      acc = false;
-    } else {
-      const float lt = Logit<T>::at(p.tl, trow(p, b, i) + x) * p.c;
-      const float ld = Logit<T>::at(p.dl, drow(p, b, i) + x) * p.c;
-      const float pt = exp2f(lt - sM[i]) / sZ[i];
-      const float pd = exp2f(ld - sM[k + 1 + i]) / sZ[k + 1 + i];
-      acc = pd > 0.f ? (p.u[(int64_t)b * (k + 1) + i] < fminf(1.f, pt / pd)) : true;
-    }
-    if (acc) {
-      em[i] = x;
-    } else {
-      j = i;
-      break;
-    }
-  }
-  for (int i = j; i <= k; ++i) em[i] = -1;
-  float* d = p.dec + (int64_t)b * 8;
-  d[0] = __int_as_float(j);
-  d[1] = __int_as_float(j < k ? 0 : 1);  // 0 = residual of row j, 1 = target row j alone
-  d[2] = sM[j];
-  d[3] = 1.f / sZ[j];
-  d[4] = j < k ? sM[k + 1 + j] : 0.f;
-  d[5] = j < k ? 1.f / sZ[k + 1 + j] : 0.f;
-  p.n_out[b] = j + 1;
-  write_rollback(p, b, j + 1);
-}
-
 template <typename T, bool GREEDY>
 __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
   __shared__ float sm_a[kThreads / 64];
   __shared__ float sm_b[kThreads / 64];
-  __shared__ int s_last;
   const int r = blockIdx.y;
   const int chunk = blockIdx.x;
   int b, i;
@@ -303,25 +219,37 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
     }
   };
   int v = v0 + tid * 8;
+  auto take8 = [&](const float* x, int vv) {
+    if constexpr (GREEDY) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) am_merge(bv, bi, x[e], vv + e);
+    } else {
+      float mx = x[0] * p.c;
+#pragma unroll
+      for (int e = 1; e < 8; ++e) mx = fmaxf(mx, x[e] * p.c);
+      if (mx > m) {
+        s = s * exp2f(m - mx);
+        m = mx;
+      }
+      const float mm = m == -INFINITY ? 0.f : m;  // all -inf so far: adds 0
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += exp2f(x[e] * p.c - mm);
+    }
+  };
   if (vec) {
-    for (; v + 8 <= v1; v += kThreads * 8) {
+    constexpr int U = 4;  // independent 16-byte loads in flight per thread
+    constexpr int STRIDE = kThreads * 8;
+    for (; v + (U - 1) * STRIDE + 8 <= v1; v += U * STRIDE) {
+      float x[U][8];
+#pragma unroll
+      for (int u = 0; u < U; ++u) Logit<T>::load8(base, roff + v + u * STRIDE, x[u]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) take8(x[u], v + u * STRIDE);
+    }
+    for (; v + 8 <= v1; v += STRIDE) {
       float x[8];
       Logit<T>::load8(base, roff + v, x);
-      if constexpr (GREEDY) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) am_merge(bv, bi, x[e], v + e);
-      } else {
-        float mx = x[0] * p.c;
-#pragma unroll
-        for (int e = 1; e < 8; ++e) mx = fmaxf(mx, x[e] * p.c);
-        if (mx > m) {
-          s = s * exp2f(m - mx);
-          m = mx;
-        }
-        const float mm = m == -INFINITY ? 0.f : m;  // all -inf so far: adds 0
-#pragma unroll
-        for (int e = 0; e < 8; ++e) s += exp2f(x[e] * p.c - mm);
-      }
+      take8(x, v);
     }
   }
   // tail (and unaligned rows): scalar, still in increasing index per thread
@@ -358,17 +286,108 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
     }
     p.stats[(int64_t)r * p.nch + chunk] = make_float2(a, c2);
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const int per_req = (p.k + 1 + (GREEDY ? 0 : p.k)) * p.nch;
-    s_last = atomicAdd(&p.cnt_a[b], 1) == per_req - 1;
+}
+
+// Greedy: one wave per request combines the argmax chunks of its k+1 target
+// rows, compares them with the drafts and writes every output.
+__global__ __launch_bounds__(64) void greedy_finalize_kernel(AccParams p) {
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int k = p.k;
+  int64_t* em = p.emitted + (int64_t)b * (k + 1);
+  int n = k + 1;
+  for (int i = 0; i <= k; ++i) {
+    const int r = b * (k + 1) + i;
+    float v = -INFINITY;
+    int ix = INT_MAX;
+    for (int c = lane; c < p.nch; c += 64) {
+      const float2 st = p.stats[(int64_t)r * p.nch + c];
+      am_merge(v, ix, st.x, __float_as_int(st.y));
+    }
+    wave_am(v, ix);
+    const bool match = i < k && p.dtok[(int64_t)b * k + i] == (int64_t)ix;
+    if (lane == 0) em[i] = ix;
+    if (!match) {
+      n = i + 1;
+      break;
+    }
   }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  if (wave == 0) decide<T>(p, b);
-  if (tid == 0) p.cnt_a[b] = 0;
+  if (lane == 0) {
+    for (int i = n; i <= k; ++i) em[i] = -1;
+    p.n_out[b] = n;
+    write_rollback(p, b, n);
+  }
+}
+
+struct Decision {
+  int j;      // first rejected position; k = all accepted
+  int mode;   // 0 = residual of row j, 1 = target row j alone (bonus)
+  float Mt, iZt, Md, iZd;
+};
+
+// Stochastic decision of request b, computed by one wave (lane 0 returns it;
+// other lanes return garbage).  With `write`, lane 0 also writes the
+// accepted prefix, num_emitted and the rollback slots.
+template <typename T>
+__device__ Decision decide(const AccParams& p, int b, bool write) {
+  __shared__ float sM[2 * kMaxK + 1], sZ[2 * kMaxK + 1];
+  const int lane = threadIdx.x & 63;
+  const int k = p.k;
+  for (int i = 0; i < 2 * k + 1; ++i) {
+    const int r = i <= k ? b * (k + 1) + i : p.B * (k + 1) + b * k + (i - k - 1);
+    float m = -INFINITY, s = 0.f;
+    for (int c = lane; c < p.nch; c += 64) {
+      const float2 st = p.stats[(int64_t)r * p.nch + c];
+      ms_merge(m, s, st.x, st.y);
+    }
+    wave_ms(m, s);
+    if (lane == 0) {
+      sM[i] = m;
+      sZ[i] = s;
+    }
+  }
+  Decision d = {k, 1, 0.f, 0.f, 0.f, 0.f};
+  if (lane != 0) return d;
+  int64_t* em = p.emitted + (int64_t)b * (k + 1);
+  int j = k;
+  for (int i = 0; i < k; ++i) {
+    const int64_t x = p.dtok[(int64_t)b * k + i];
+    bool acc;
+    if (x < 0 || x >= p.V) {
+      if (write) atomicOr(p.flags, 4);
+      acc = false;
+    } else {
+      const float lt = Logit<T>::at(p.tl, trow(p, b, i) + x) * p.c;
+      const float ld = Logit<T>::at(p.dl, drow(p, b, i) + x) * p.c;
+      const float pt = exp2f(lt - sM[i]) / sZ[i];
+      const float pd = exp2f(ld - sM[k + 1 + i]) / sZ[k + 1 + i];
+      acc = pd > 0.f ? (p.u[(int64_t)b * (k + 1) + i] < fminf(1.f, pt / pd)) : true;
+    }
+    if (!acc) {
+      j = i;
+      break;
+    }
+    if (write) em[i] = x;
+  }
+  d.j = j;
+  d.mode = j < k ? 0 : 1;
+  d.Mt = sM[j];
+  d.iZt = 1.f / sZ[j];
+  d.Md = j < k ? sM[k + 1 + j] : 0.f;
+  d.iZd = j < k ? 1.f / sZ[k + 1 + j] : 0.f;
+  if (write) {
+    for (int i = j; i <= k; ++i) em[i] = -1;
+    p.n_out[b] = j + 1;
+    write_rollback(p, b, j + 1);
+    float* dd = p.dec + (int64_t)b * 8;
+    dd[0] = __int_as_float(d.j);
+    dd[1] = __int_as_float(d.mode);
+    dd[2] = d.Mt;
+    dd[3] = d.iZt;
+    dd[4] = d.Md;
+    dd[5] = d.iZd;
+  }
+  return d;
 }
 
 // Weight of vocabulary entry v for the decided row pair.
@@ -397,26 +416,41 @@ __device__ float block_incl_scan(float x, float* sh) {
   return pre + x;
 }
 
+// Chunk sums of the decided weights; chunk 0 also publishes the decision.
 template <typename T>
-__global__ __launch_bounds__(kThreads) void sample_kernel(AccParams p) {
+__global__ __launch_bounds__(kThreads) void sum_kernel(AccParams p) {
   __shared__ float sh[kThreads / 64];
-  __shared__ int s_last, s_tok, s_chunk, s_full;
-  __shared__ float s_rem;
+  __shared__ Decision s_dec;
   const int b = blockIdx.y;
   const int chunk = blockIdx.x;
   const int tid = threadIdx.x;
-  const float* d = p.dec + (int64_t)b * 8;
-  const int j = __float_as_int(d[0]);
-  int mode = __float_as_int(d[1]);
-  const float Mt = d[2], iZt = d[3], Md = d[4], iZd = d[5];
-  const int64_t to = trow(p, b, j);
-  const int64_t dof = mode == 0 ? drow(p, b, j) : 0;
-
-  // ---- chunk sum of the weights (coalesced, any order) ----
+  if (tid < 64) {
+    const Decision d = decide<T>(p, b, chunk == 0);
+    if (tid == 0) s_dec = d;
+  }
+  __syncthreads();
+  const Decision d = s_dec;
+  const int64_t to = trow(p, b, d.j);
+  const int64_t dof = d.mode == 0 ? drow(p, b, d.j) : 0;
   const int v0 = chunk * p.cs2;
   const int v1 = min(p.V, v0 + p.cs2);
   float acc = 0.f;
-  for (int v = v0 + tid; v < v1; v += kThreads) acc += weight<T>(p, to, dof, mode, Mt, iZt, Md, iZd, v);
+  int v = v0 + tid * 8;
+  if (((to | dof) % Logit<T>::kAlign) == 0) {
+    for (; v + 8 <= v1; v += kThreads * 8) {
+      float xt[8], xd[8];
+      Logit<T>::load8(p.tl, to + v, xt);
+      if (d.mode == 0) Logit<T>::load8(p.dl, dof + v, xd);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float pt = exp2f(xt[e] * p.c - d.Mt) * d.iZt;
+        acc += d.mode == 0 ? fmaxf(0.f, pt - exp2f(xd[e] * p.c - d.Md) * d.iZd) : pt;
+      }
+    }
+  }
+  for (; v < v1; v += kThreads * 8)
+    for (int e = 0; e < 8 && v + e < v1; ++e)
+      acc += weight<T>(p, to, dof, d.mode, d.Mt, d.iZt, d.Md, d.iZd, v + e);
   acc = wave_sum(acc);
   if ((tid & 63) == 0) sh[tid >> 6] = acc;
   __syncthreads();
@@ -425,21 +459,31 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(AccParams p) {
     for (int w = 0; w < kThreads / 64; ++w) t += sh[w];
     p.psum[(int64_t)b * p.nch2 + chunk] = t;
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_last = atomicAdd(&p.cnt_b[b], 1) == p.nch2 - 1;
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+}
 
-  // ---- last workgroup: pick the chunk, then the token ----
+// One workgroup per request: chunk by a sequential prefix, token by a block
+// scan over contiguous runs of that chunk.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void select_kernel(AccParams p) {
+  __shared__ float sh[kThreads / 64];
+  __shared__ int s_tok, s_chunk, s_full;
+  __shared__ float s_rem;
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const float* dd = p.dec + (int64_t)b * 8;
+  const int j = __float_as_int(dd[0]);
+  int mode = __float_as_int(dd[1]);
+  const float Mt = dd[2], iZt = dd[3], Md = dd[4], iZd = dd[5];
+  const int64_t to = trow(p, b, j);
+  const int64_t dof = mode == 0 ? drow(p, b, j) : 0;
+  const float u = p.u[(int64_t)b * (p.k + 1) + p.k];
   if (tid == 0) {
     const float* ps = p.psum + (int64_t)b * p.nch2;
     float tot = 0.f;
     for (int c = 0; c < p.nch2; ++c) tot += ps[c];
     s_full = 0;
     if (tot > 0.f) {
-      const float target = p.u[(int64_t)b * (p.k + 1) + p.k] * tot;
+      const float target = u * tot;
       float pre = 0.f;
       int cs = -1, lastnz = -1;
       for (int c = 0; c < p.nch2; ++c) {
@@ -460,6 +504,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(AccParams p) {
       // vocabulary (mirrors speculative.py:163-169)
       s_full = 1;
     }
+    s_tok = -1;
   }
   __syncthreads();
   int a, e;
@@ -471,22 +516,17 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(AccParams p) {
     a = s_chunk * p.cs2;
     e = min(p.V, a + p.cs2);
   }
-  // per-thread contiguous runs, sequential sums, block scan (fixed order)
   const int R = (e - a + kThreads - 1) / kThreads;
   const int ra = min(e, a + tid * R), rb = min(e, ra + R);
   float run = 0.f;
   for (int v = ra; v < rb; ++v) run += weight<T>(p, to, dof, mode, Mt, iZt, Md, iZd, v);
   const float incl = block_incl_scan(run, sh);
   const float excl = incl - run;
-  if (s_full && tid == kThreads - 1) {
-    s_rem = p.u[(int64_t)b * (p.k + 1) + p.k] * incl;
-  }
-  if (tid == 0) s_tok = -1;
+  if (s_full && tid == kThreads - 1) s_rem = u * incl;
   __syncthreads();
   const float rem = s_rem;
   if (run > 0.f && incl > rem && !(excl > rem)) {
-    // recompute the prefix in the same order as `run`
-    float cum = 0.f;
+    float cum = 0.f;  // same order as `run`, so excl + cum reaches incl
     for (int v = ra; v < rb; ++v) {
       cum += weight<T>(p, to, dof, mode, Mt, iZt, Md, iZd, v);
       if (excl + cum > rem) {
@@ -508,10 +548,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(AccParams p) {
     atomicMax(&s_tok, last);
     __syncthreads();
   }
-  if (tid == 0) {
-    p.emitted[(int64_t)b * (p.k + 1) + j] = s_tok;
-    p.cnt_b[b] = 0;
-  }
+  if (tid == 0) p.emitted[(int64_t)b * (p.k + 1) + j] = s_tok;
 }
 
 struct Layout {
@@ -530,9 +567,8 @@ Layout layout(int B, int k, int V, bool greedy) {
   L.cs2 = ((V + L.nch2 - 1) / L.nch2 + 7) / 8 * 8;
   L.nch2 = (V + L.cs2 - 1) / L.cs2;
   auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
-  // stats sized for the stochastic row count so one workspace serves both modes
-  const int rows_max = B * (2 * k + 1);
-  L.stats_off = kFlagBytes + kCounterBytes;
+  const int rows_max = B * (2 * k + 1);  // one workspace serves both modes
+  L.stats_off = kFlagBytes;
   L.dec_off = L.stats_off + al((int64_t)rows_max * kMaxChunks * 8);
   L.psum_off = L.dec_off + al((int64_t)B * 8 * 4);
   L.total = L.psum_off + al((int64_t)B * kMaxChunks * 4);
@@ -544,13 +580,19 @@ int32_t launch_accept(const AccParams& p, int rows, hipStream_t s) {
   dim3 g1(p.nch, rows);
   if (p.greedy) {
     hipLaunchKernelGGL((stats_kernel<T, true>), g1, dim3(kThreads), 0, s, p);
-    return launch_status("stats_kernel");
+    int32_t rc = launch_status("stats_kernel");
+    if (rc) return rc;
+    hipLaunchKernelGGL(greedy_finalize_kernel, dim3(p.B), dim3(64), 0, s, p);
+    return launch_status("greedy_finalize_kernel");
   }
   hipLaunchKernelGGL((stats_kernel<T, false>), g1, dim3(kThreads), 0, s, p);
   int32_t rc = launch_status("stats_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL((sample_kernel<T>), dim3(p.nch2, p.B), dim3(kThreads), 0, s, p);
-  return launch_status("sample_kernel");
+  hipLaunchKernelGGL((sum_kernel<T>), dim3(p.nch2, p.B), dim3(kThreads), 0, s, p);
+  rc = launch_status("sum_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL((select_kernel<T>), dim3(p.B), dim3(kThreads), 0, s, p);
+  return launch_status("select_kernel");
 }
 
 }  // namespace
@@ -633,8 +675,6 @@ extern "C" int32_t nsg_spec_accept(const void* target_logits, int64_t target_req
   p.cs2 = L.cs2;
   char* ws = static_cast<char*>(workspace);
   p.flags = reinterpret_cast<int*>(ws);
-  p.cnt_a = reinterpret_cast<int*>(ws + kFlagBytes);
-  p.cnt_b = p.cnt_a + kMaxBatch;
   p.stats = reinterpret_cast<float2*>(ws + L.stats_off);
   p.dec = reinterpret_cast<float*>(ws + L.dec_off);
   p.psum = reinterpret_cast<float*>(ws + L.psum_off);

@@ -12,23 +12,23 @@
 //   one workgroup = (request, query tile, KV split) x one KV head.
 //   A query tile holds up to 64 query rows = q_tile_tokens x GQA group,
 //   row rho -> (token rho / G, head-in-group rho % G), padded to 16-row MFMA
-//   tiles.  Long KV ranges are split; the last workgroup of a split group to
-//   finish merges the partial (m, l, O) rows (atomic counter, agent-scope
-//   fences), so one launch produces the final output.
+//   tiles.  Long KV ranges are split; split workgroups write partial
+//   (O, m, l) rows and a second, small launch merges them.  No workgroup
+//   waits on another inside a launch: on gfx950 a cross-workgroup handshake
+//   needs agent-scope fences, which write back and invalidate the XCD's L2.
 //
-// Inside a workgroup the 4 waves take 32-token KV steps round-robin; each
-// wave keeps its own online-softmax state and the waves merge through LDS.
-// Per 32-token step a wave:
-//   - loads K rows straight into MFMA operands: lane (token = lane%16,
-//     d-group = lane/16) reads 16 contiguous bytes of one token's head row;
-//   - loads V rows (16-byte coalesced loads) and stages them in a per-wave
-//     LDS tile [32 tokens][D + 8] bf16;
-//   - computes S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (M = tokens,
-//     N = query rows, K = head dim), so every lane holds 4 tokens of ONE query
-//     row and the row max / sum need only two cross-lane steps;
-//   - converts P^T to bf16 in registers, which is already the B operand of
+// Inside a workgroup wave w owns query rows [16w, 16w+16) of the tile.  The
+// workgroup walks its KV range in 32-token steps; per step:
+//   - all threads load the NEXT step's K and V rows (16-byte coalesced loads
+//     of NHD page rows) into registers, overlapping this step's math;
+//   - each wave computes S^T = K Q^T with v_mfma_f32_16x16x32_bf16
+//     (M = 16 tokens, N = 16 query rows, K = head dim; K fragments read from
+//     LDS with ds_read_b128), so each lane holds 4 tokens of ONE query row and
+//     the row max / sum need two cross-lane steps;
+//   - P^T, converted to bf16 in registers, is already the B operand of
 //     O^T += V^T P^T (M = head dim, N = query rows, K = 32 tokens); V^T comes
-//     from the LDS tile with the same token order.
+//     from the LDS tile in the same token order;
+//   - the prefetched registers go to the other LDS buffer; one barrier.
 #include <algorithm>
 #include <cstdarg>
 #include <vector>
@@ -38,14 +38,12 @@
 namespace nsg {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
+constexpr int kThreads = 256;         // merge kernel
+constexpr int kMinSplitSteps = 4;     // 32-token steps per KV split, at least
 constexpr int kTokIt = 32;           // KV tokens per wave step
 constexpr float kMaskVal = -1.0e30f; // finite "minus infinity" (no inf - inf)
-constexpr int64_t kHeaderBytes = 256;          // flags word + padding
-constexpr int64_t kMaxCounters = 1 << 16;      // (group, kv head) merge counters
-constexpr int64_t kCounterBytes = kMaxCounters * 4;
-constexpr int kTargetWgPerCu = 4;
+constexpr int64_t kHeaderBytes = 256;  // flags word + padding
+constexpr int kTargetWgPerCu = 2;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -64,7 +62,6 @@ struct AttnParams {
   int Hq, Hkv, G, log2P, num_pages, causal;
   float scale_log2;
   int* flags;
-  int* counters;
   float* partials;
 };
 
@@ -73,28 +70,39 @@ __device__ __forceinline__ bf16x8 load_bf16x8(const bf16* p) {
   return __builtin_bit_cast(bf16x8, v);
 }
 
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16 pair (v_cvt_pk_bf16_f32, round to nearest even).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(floatx2{lo, hi}, bf16x2));
+}
+
+// One workgroup = one work item x one KV head; wave w owns query rows
+// [16w, 16w + 16) of the item's query tile.  The workgroup walks the item's
+// KV range in 32-token steps: all threads load the next step's K and V rows
+// into registers while the waves compute the current step out of LDS, then
+// the registers go to the other LDS buffer (one barrier per step).
 template <int D, int RT>
-__global__ __launch_bounds__(kThreads) void verify_attn_kernel(AttnParams p) {
-  constexpr int KC = D / 32;   // K-dim chunks of QK^T
-  constexpr int DT = D / 16;   // d tiles of PV
+__global__ __launch_bounds__(RT * 64) void verify_attn_kernel(AttnParams p) {
+  constexpr int NT = RT * 64;
+  constexpr int KC = D / 32;              // K-dim chunks of QK^T
+  constexpr int DT = D / 16;              // d tiles of PV
   constexpr int ROWS = RT * 16;
-  constexpr int VROW = D + 8;  // padded LDS row (bf16): 16-byte aligned, conflict-free reads
-  constexpr int VCH = D / 8;   // 16-byte chunks per V row
-  constexpr int NV = kTokIt * VCH / 64;
-  constexpr int OROW = D + 4;
-  constexpr int PSTRIDE = D + 4;  // partial row: O[D], m, l, 2 pad (16-byte aligned rows)
-  constexpr int SMEM_V = kWaves * kTokIt * VROW * 2;
-  constexpr int SMEM_M = kWaves * 16 * OROW * 4 + 2 * kWaves * 16 * 4;
-  constexpr int SMEM = SMEM_V > SMEM_M ? SMEM_V : SMEM_M;
-  __shared__ __attribute__((aligned(16))) char smem[SMEM];
-  __shared__ int s_last;
+  constexpr int KROW = D + 8;             // LDS row stride (bf16): 16-byte aligned, spreads banks
+  constexpr int VCH = D / 8;              // 16-byte chunks per token row
+  constexpr int TILE_CH = kTokIt * VCH;   // chunks per K (or V) tile
+  constexpr int NLD = (2 * TILE_CH + NT - 1) / NT;  // chunks per thread per step
+  constexpr int TILE = kTokIt * KROW;
+  constexpr int PSTRIDE = D + 4;          // partial row: O[D], m, l, 2 pad
+  __shared__ __attribute__((aligned(16))) bf16 lds[2][2][TILE];
 
   const int wi = blockIdx.x;
   if (wi >= p.num_work) return;
   const int h = blockIdx.y;
   const int* wk = p.work + (size_t)wi * NSG_ATTN_WORK_INTS;
   const int b = wk[0], qb = wk[1], qn = wk[2], kvb = wk[3], kve = wk[4];
-  const int split = wk[5], nsplit = wk[6], group = wk[7];
+  const int nsplit = wk[6];
   const int P = 1 << p.log2P;
   const int G = p.G;
   const int q0 = p.qo_indptr[b];
@@ -103,265 +111,230 @@ __global__ __launch_bounds__(kThreads) void verify_attn_kernel(AttnParams p) {
   const int npg = p.kv_indptr[b + 1] - pb;
   const int L = npg > 0 ? (npg - 1) * P + p.kv_last[b] : 0;
   const int nrows = qn * G;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int r16 = lane & 15;
   const int g4 = lane >> 4;
 
-  // Query fragments (B operand of S^T = K Q^T) and per-row causal limits.
-  bf16x8 qf[RT][KC];
-  int lim[RT];
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const int row = rt * 16 + r16;
-    const bool ok = row < nrows;
-    const int tau = row / G;
-    const int gam = row - tau * G;
-    lim[rt] = ok ? (p.causal ? L - ql + qb + tau : L - 1) : -1;
+  // This lane's query row (B operand of S^T = K Q^T) and causal limit.
+  const int row = wave * 16 + r16;
+  const bool row_ok = row < nrows;
+  const int tau = row / G;
+  const int gam = row - tau * G;
+  const int lim = row_ok ? (p.causal ? L - ql + qb + tau : L - 1) : -1;
+  bf16x8 qf[KC];
+  {
     const bf16* qrow = p.q + ((size_t)(q0 + qb + tau) * p.Hq + h * G + gam) * D;
 #pragma unroll
-    for (int c = 0; c < KC; ++c) {
-      if (ok) {
-        qf[rt][c] = load_bf16x8(qrow + 32 * c + 8 * g4);
-      } else {
-        qf[rt][c] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
-      }
-    }
+    for (int c = 0; c < KC; ++c)
+      qf[c] = row_ok ? load_bf16x8(qrow + 32 * c + 8 * g4)
+                     : __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
   }
 
-  floatx4 oacc[RT][DT];
-  float m_run[RT], l_run[RT];
+  floatx4 oacc[DT];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    m_run[rt] = kMaskVal;
-    l_run[rt] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) oacc[rt][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-  }
+  for (int dt = 0; dt < DT; ++dt) oacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kMaskVal, l_run = 0.f;
 
-  bf16* vt = reinterpret_cast<bf16*>(smem) + wave * kTokIt * VROW;
   const size_t head_off = (size_t)h * D;
   const size_t tok_stride = (size_t)p.Hkv * D;
   const int n_it = (kve - kvb + kTokIt - 1) / kTokIt;
 
-  for (int it = wave; it < n_it; it += kWaves) {
+  // Page ids are fetched one step ahead of the K/V rows so that no data load
+  // waits on an index load (vmcnt retires in order).
+  int pg[NLD], pgn[NLD];  // page ids of the step being loaded / of the one after
+  u32x4 pre[NLD];
+  bool bad_page = false;
+  // Loads are unconditional: invalid lanes read a valid dummy address and the
+  // value is replaced by zero only where it is consumed (selecting right
+  // after the load would make the compiler wait for it there).
+  auto chunk_ok = [&](int i, int t0) {
+    const int e = tid + i * NT;
+    const int which = e >= TILE_CH;
+    const int t = (e - which * TILE_CH) / VCH;
+    return e < 2 * TILE_CH && t0 + t < kve;
+  };
+  auto fetch_pages = [&](int it) {
     const int t0 = kvb + it * kTokIt;
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int e = tid + i * NT;
+      const int which = e >= TILE_CH;
+      const int t = (e - which * TILE_CH) / VCH;
+      const int j = t0 + t;
+      pgn[i] = p.kv_indices[pb + (chunk_ok(i, t0) ? (j >> p.log2P) : 0)];
+    }
+  };
+  unsigned okbits = 0;  // bit i: chunk i of the prefetched step holds real data
+  auto load_step = [&](int it) {
+    const int t0 = kvb + it * kTokIt;
+    okbits = 0;
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int e = tid + i * NT;
+      const int which = e >= TILE_CH;
+      const int r = e - which * TILE_CH;
+      const int t = r / VCH;
+      const int ch = r - t * VCH;
+      const int j = t0 + t;
+      const int page = pg[i];
+      const bool in_req = chunk_ok(i, t0);
+      bad_page |= in_req && (unsigned)page >= (unsigned)p.num_pages;
+      const bool ok = in_req && (unsigned)page < (unsigned)p.num_pages;
+      okbits |= (unsigned)ok << i;
+      const size_t off =
+          ok ? ((size_t)page * P + (j & (P - 1))) * tok_stride + head_off + ch * 8 : 0;
+      pre[i] = *reinterpret_cast<const u32x4*>((which ? p.vc : p.kc) + off);
+    }
+  };
+  auto store_step = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int e = tid + i * NT;
+      if (e < 2 * TILE_CH) {
+        const int which = e >= TILE_CH;
+        const int r = e - which * TILE_CH;
+        const int t = r / VCH;
+        const int ch = r - t * VCH;
+        *reinterpret_cast<u32x4*>(&lds[buf][which][t * KROW + ch * 8]) =
+            (okbits >> i) & 1u ? pre[i] : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  };
 
-    // ---- K rows straight into MFMA A operands ----
-    bf16x8 kf[2][KC];
+  auto next_pages = [&]() {
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) pg[i] = pgn[i];
+  };
+  if (n_it > 0) {
+    fetch_pages(0);
+    next_pages();
+    load_step(0);
+    store_step(0);
+    fetch_pages(1);
+  }
+  __syncthreads();
+  for (int it = 0; it < n_it; ++it) {
+    const int buf = it & 1;
+    const int t0 = kvb + it * kTokIt;
+    // Straight-line prefetch: past the last step chunk_ok() is false, so these
+    // read page 0 of the request's table and no real K/V rows.
+    next_pages();
+    fetch_pages(it + 2);                     // index loads first, then the rows,
+    load_step(it + 1);                       // in flight during this step's math
+
+    // ---- S^T = K Q^T: lane holds tokens 16s + 4*g4 + i of query row r16 ----
+    const bf16* Kt = lds[buf][0];
+    floatx4 sacc[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const int j = t0 + 16 * s + r16;
-      int page = -1;
-      if (j < kve) {
-        page = p.kv_indices[pb + (j >> p.log2P)];
-        if ((unsigned)page >= (unsigned)p.num_pages) {
-          atomicOr(p.flags, 1);
-          page = -1;
-        }
-      }
-      const bf16* kp = p.kc + ((size_t)max(page, 0) * P + (j & (P - 1))) * tok_stride + head_off;
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < KC; ++c) {
-        if (page >= 0) {
-          kf[s][c] = load_bf16x8(kp + 32 * c + 8 * g4);
-        } else {
-          kf[s][c] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
-        }
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&Kt[(16 * s + r16) * KROW + 32 * c + 8 * g4]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[c], acc, 0, 0, 0);
       }
-    }
-    // ---- V rows: coalesced 16-byte loads ----
-    u32x4 vr[NV];
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int e = lane + 64 * i;
-      const int t = e / VCH;
-      const int ch = e - t * VCH;
-      const int j = t0 + t;
-      int page = -1;
-      if (j < kve) {
-        page = p.kv_indices[pb + (j >> p.log2P)];
-        if ((unsigned)page >= (unsigned)p.num_pages) page = -1;
-      }
-      if (page >= 0) {
-        vr[i] = *reinterpret_cast<const u32x4*>(
-            p.vc + ((size_t)page * P + (j & (P - 1))) * tok_stride + head_off + ch * 8);
-      } else {
-        vr[i] = u32x4{0u, 0u, 0u, 0u};
-      }
+      sacc[s] = acc;
     }
 
-    // ---- S^T = K Q^T ----
-    floatx4 sacc[RT][2];
+    // ---- online softmax (base 2) ----
+    float sv[8];
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
+    for (int s = 0; s < 2; ++s) {
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < KC; ++c)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[s][c], qf[rt][c], acc, 0, 0, 0);
-        sacc[rt][s] = acc;
+      for (int i = 0; i < 4; ++i) {
+        const int j = t0 + 16 * s + 4 * g4 + i;
+        sv[4 * s + i] = (j <= lim && j < kve) ? sacc[s][i] * p.scale_log2 : kMaskVal;
       }
     }
-
-    // ---- stage V in this wave's LDS tile ----
+    float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                     fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mnew = fmaxf(m_run, mx);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);
+    m_run = mnew;
+    float pv[8];
+    float ps = 0.f;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int e = lane + 64 * i;
-      const int t = e / VCH;
-      const int ch = e - t * VCH;
-      *reinterpret_cast<u32x4*>(vt + t * VROW + ch * 8) = vr[i];
+    for (int x = 0; x < 8; ++x) {
+      pv[x] = __builtin_amdgcn_exp2f(sv[x] - mnew);
+      ps += pv[x];
     }
+    l_run = l_run * alpha + ps;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+    const bf16x8 pf = __builtin_bit_cast(
+        bf16x8, u32x4{cvt_pk_bf16(pv[0], pv[1]), cvt_pk_bf16(pv[2], pv[3]),
+                      cvt_pk_bf16(pv[4], pv[5]), cvt_pk_bf16(pv[6], pv[7])});
 
-    // ---- online softmax; P^T packed as the B operand of the PV MFMA ----
-    bf16x8 pf[RT];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      float sv[8];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int j = t0 + 16 * s + 4 * g4 + i;
-          sv[4 * s + i] = (j <= lim[rt] && j < kve) ? sacc[rt][s][i] * p.scale_log2 : kMaskVal;
-        }
-      }
-      float mx = sv[0];
-#pragma unroll
-      for (int x = 1; x < 8; ++x) mx = fmaxf(mx, sv[x]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(m_run[rt], mx);
-      const float alpha = exp2f(m_run[rt] - mnew);
-      m_run[rt] = mnew;
-      float pv[8];
-      float ps = 0.f;
-#pragma unroll
-      for (int x = 0; x < 8; ++x) {
-        pv[x] = exp2f(sv[x] - mnew);
-        ps += pv[x];
-      }
-      l_run[rt] = l_run[rt] * alpha + ps;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) oacc[rt][dt] *= alpha;
-      u32x4 pk = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]),
-                  pack_bf16x2(pv[4], pv[5]), pack_bf16x2(pv[6], pv[7])};
-      pf[rt] = __builtin_bit_cast(bf16x8, pk);
-    }
-
-    __builtin_amdgcn_wave_barrier();
     // ---- O^T += V^T P^T; element e of lane group g4 is token
     //      4*g4 + e (e < 4) or 16 + 4*g4 + (e - 4), matching pf ----
-    const uint16_t* vt16 = reinterpret_cast<const uint16_t*>(vt);
+    const uint16_t* Vt = reinterpret_cast<const uint16_t*>(lds[buf][1]);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       const int col = dt * 16 + r16;
       uint32_t w[4];
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
-        const int ea = 2 * e2, eb = 2 * e2 + 1;
-        const int ta = ea < 4 ? 4 * g4 + ea : 16 + 4 * g4 + ea - 4;
-        const int tb = eb < 4 ? 4 * g4 + eb : 16 + 4 * g4 + eb - 4;
-        w[e2] = (uint32_t)vt16[ta * VROW + col] | ((uint32_t)vt16[tb * VROW + col] << 16);
+        const int ta = e2 < 2 ? 4 * g4 + 2 * e2 : 16 + 4 * g4 + 2 * e2 - 4;
+        w[e2] = (uint32_t)Vt[ta * KROW + col] | ((uint32_t)Vt[(ta + 1) * KROW + col] << 16);
       }
       const bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
-        oacc[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[rt], oacc[rt][dt], 0, 0, 0);
+      oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, oacc[dt], 0, 0, 0);
     }
-    __builtin_amdgcn_wave_barrier();
+
+    store_step(buf ^ 1);
+    __syncthreads();
   }
 
-  // ---- row sums across the 4 lane groups that share a query row ----
-  float l_tot[RT];
+  if (bad_page) atomicOr(p.flags, 1);
+  // ---- finish: the 4 lane groups sharing query row r16 hold partial sums ----
+  float l = l_run;
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  if (!row_ok) return;
+  if (nsplit == 1) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    bf16* orow = p.out + ((size_t)(q0 + qb + tau) * p.Hq + h * G + gam) * D + 4 * g4;
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    float l = l_run[rt];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
-    l_tot[rt] = l;
-  }
-
-  // ---- merge the 4 waves through LDS, one 16-row tile at a time ----
-  __syncthreads();
-  float* mo = reinterpret_cast<float*>(smem);          // [kWaves][16][OROW]
-  float* mm = mo + kWaves * 16 * OROW;                  // [kWaves][16]
-  float* ml = mm + kWaves * 16;                         // [kWaves][16]
-  constexpr int CPT = D / 16;                           // columns per thread
-  const int mrow = threadIdx.x >> 4;
-  const int c0 = (threadIdx.x & 15) * CPT;
-  const size_t part_base = ((size_t)wi * p.Hkv + h) * ROWS * PSTRIDE;
+    for (int dt = 0; dt < DT; ++dt) {
+      const floatx4 o = oacc[dt];
+      *reinterpret_cast<u32x2*>(orow + dt * 16) =
+          u32x2{cvt_pk_bf16(o[0] * inv, o[1] * inv), cvt_pk_bf16(o[2] * inv, o[3] * inv)};
+    }
+  } else {
+    float* prow = p.partials + ((size_t)wi * p.Hkv + h) * ROWS * PSTRIDE + (size_t)row * PSTRIDE;
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-      *reinterpret_cast<floatx4*>(&mo[(wave * 16 + r16) * OROW + dt * 16 + 4 * g4]) = oacc[rt][dt];
+    for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<floatx4*>(prow + dt * 16 + 4 * g4) = oacc[dt];
     if (g4 == 0) {
-      mm[wave * 16 + r16] = m_run[rt];
-      ml[wave * 16 + r16] = l_tot[rt];
+      prow[D] = m_run;
+      prow[D + 1] = l;
     }
-    __syncthreads();
-    const int grow = rt * 16 + mrow;
-    if (grow < nrows) {
-      float M = mm[mrow];
-#pragma unroll
-      for (int w = 1; w < kWaves; ++w) M = fmaxf(M, mm[w * 16 + mrow]);
-      float wt[kWaves];
-      float lsum = 0.f;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        wt[w] = exp2f(mm[w * 16 + mrow] - M);
-        lsum += wt[w] * ml[w * 16 + mrow];
-      }
-      float o[CPT];
-#pragma unroll
-      for (int c = 0; c < CPT; ++c) {
-        float acc = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) acc += wt[w] * mo[(w * 16 + mrow) * OROW + c0 + c];
-        o[c] = acc;
-      }
-      if (nsplit == 1) {
-        const int tau = grow / G;
-        const int gam = grow - tau * G;
-        bf16* orow = p.out + ((size_t)(q0 + qb + tau) * p.Hq + h * G + gam) * D + c0;
-        const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-        uint32_t pk[CPT / 2];
-#pragma unroll
-        for (int c = 0; c < CPT / 2; ++c) pk[c] = pack_bf16x2(o[2 * c] * inv, o[2 * c + 1] * inv);
-        if constexpr (CPT == 8) {
-          *reinterpret_cast<u32x4*>(orow) = u32x4{pk[0], pk[1], pk[2], pk[3]};
-        } else {
-          *reinterpret_cast<u32x2*>(orow) = u32x2{pk[0], pk[1]};
-        }
-      } else {
-        float* prow = p.partials + part_base + (size_t)grow * PSTRIDE;
-#pragma unroll
-        for (int c = 0; c < CPT; c += 4)
-          *reinterpret_cast<floatx4*>(prow + c0 + c) = floatx4{o[c], o[c + 1], o[c + 2], o[c + 3]};
-        if (c0 == 0) {
-          prow[D] = M;
-          prow[D + 1] = lsum;
-        }
-      }
-    }
-    __syncthreads();
   }
-  if (nsplit == 1) return;
+}
 
-  // ---- cross-split merge by the last workgroup of the group ----
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = atomicAdd(&p.counters[(size_t)group * p.Hkv + h], 1);
-    s_last = (prev == nsplit - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  const int wi0 = wi - split;
-  for (int grow = mrow; grow < nrows; grow += kThreads / 16) {
+// Merge of the split partials of one (request, query tile) group x KV head.
+// A separate launch: partials written by workgroups on other XCDs become
+// visible at the kernel boundary, so no in-kernel cross-workgroup fence (an
+// L2 write-back + invalidate on gfx950) is needed.
+template <int D, int RT>
+__global__ __launch_bounds__(kThreads) void verify_merge_kernel(AttnParams p, const int* merge,
+                                                               int num_merge) {
+  constexpr int ROWS = RT * 16;
+  constexpr int PSTRIDE = D + 4;
+  constexpr int CPT = D / 16;
+  const int mi = blockIdx.x;
+  if (mi >= num_merge) return;
+  const int h = blockIdx.y;
+  const int* mw = merge + (size_t)mi * NSG_ATTN_WORK_INTS;
+  const int b = mw[0], qb = mw[1], qn = mw[2], wi0 = mw[3], nsplit = mw[4];
+  const int G = p.G;
+  const int q0 = p.qo_indptr[b];
+  const int nrows = qn * G;
+  const int c0 = (threadIdx.x & 15) * CPT;
+  for (int grow = threadIdx.x >> 4; grow < nrows; grow += kThreads / 16) {
     float M = kMaskVal;
     for (int s = 0; s < nsplit; ++s) {
       const float* prow = p.partials + ((size_t)(wi0 + s) * p.Hkv + h) * ROWS * PSTRIDE +
@@ -399,21 +372,30 @@ __global__ __launch_bounds__(kThreads) void verify_attn_kernel(AttnParams p) {
       *reinterpret_cast<u32x2*>(orow) = u32x2{pk[0], pk[1]};
     }
   }
-  if (threadIdx.x == 0) p.counters[(size_t)group * p.Hkv + h] = 0;
+}
+
+template <int D, int RT>
+int32_t launch_rt(const nsg_attn_plan_t* plan, const AttnParams& prm, const int* merge,
+                  hipStream_t stream) {
+  hipLaunchKernelGGL((verify_attn_kernel<D, RT>), dim3(plan->num_work, plan->num_kv_heads),
+                     dim3(RT * 64), 0, stream, prm);
+  int32_t rc = launch_status("verify_attn_kernel");
+  if (rc || plan->num_merge == 0) return rc;
+  hipLaunchKernelGGL((verify_merge_kernel<D, RT>), dim3(plan->num_merge, plan->num_kv_heads),
+                     dim3(kThreads), 0, stream, prm, merge, plan->num_merge);
+  return launch_status("verify_merge_kernel");
 }
 
 template <int D>
-int32_t launch_d(const nsg_attn_plan_t* plan, const AttnParams& prm, hipStream_t stream) {
-  dim3 grid(plan->num_work, plan->num_kv_heads);
-  dim3 block(kThreads);
+int32_t launch_d(const nsg_attn_plan_t* plan, const AttnParams& prm, const int* merge,
+                 hipStream_t stream) {
   switch (plan->row_tiles) {
-    case 1: hipLaunchKernelGGL((verify_attn_kernel<D, 1>), grid, block, 0, stream, prm); break;
-    case 2: hipLaunchKernelGGL((verify_attn_kernel<D, 2>), grid, block, 0, stream, prm); break;
-    case 3: hipLaunchKernelGGL((verify_attn_kernel<D, 3>), grid, block, 0, stream, prm); break;
-    case 4: hipLaunchKernelGGL((verify_attn_kernel<D, 4>), grid, block, 0, stream, prm); break;
+    case 1: return launch_rt<D, 1>(plan, prm, merge, stream);
+    case 2: return launch_rt<D, 2>(plan, prm, merge, stream);
+    case 3: return launch_rt<D, 3>(plan, prm, merge, stream);
+    case 4: return launch_rt<D, 4>(plan, prm, merge, stream);
     default: set_error("row_tiles %d out of range", plan->row_tiles); return NSG_ERR_ARG;
   }
-  return launch_status("verify_attn_kernel");
 }
 
 int ilog2_exact(int v) {
@@ -488,24 +470,42 @@ extern "C" int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_i
       total_it += (kv_end + kTokIt - 1) / kTokIt;
     }
   }
-  NSG_CHECK_ARG((long long)groups.size() * num_kv_heads <= kMaxCounters,
-                "%zu query tiles x %d kv heads exceed the %lld merge counters", groups.size(),
-                num_kv_heads, (long long)kMaxCounters);
   const long long target_items = std::max(1, num_cus * kTargetWgPerCu / num_kv_heads);
-  long long chunk_it = std::max<long long>(kWaves, (total_it + target_items - 1) / target_items);
-  chunk_it = (chunk_it + kWaves - 1) / kWaves * kWaves;
+  // a split is at least kMinSplitSteps steps: its partial rows cost about as
+  // much traffic as one step of K and V
+  const long long chunk_it =
+      std::max<long long>(kMinSplitSteps, (total_it + target_items - 1) / target_items);
 
-  int n = 0, max_splits = 0;
+  int n = 0, max_splits = 0, n_merge = 0;
+  std::vector<int> split_counts(groups.size());
+  for (size_t gi = 0; gi < groups.size(); ++gi) {
+    const long long its = (groups[gi].kv_end + kTokIt - 1) / kTokIt;
+    split_counts[gi] = (int)std::max<long long>(1, (its + chunk_it - 1) / chunk_it);
+    n += split_counts[gi];
+    n_merge += split_counts[gi] > 1;
+  }
+  if (!work_h || n + n_merge > work_capacity) {
+    set_error("work list needs %d items, buffer holds %d", n + n_merge, work_capacity);
+    return NSG_ERR_WORKSPACE;
+  }
+  const int n_work = n;
+  n = 0;
+  int m = 0;
   for (size_t gi = 0; gi < groups.size(); ++gi) {
     const Group& g = groups[gi];
-    const long long its = (g.kv_end + kTokIt - 1) / kTokIt;
-    const int ns = (int)std::max<long long>(1, (its + chunk_it - 1) / chunk_it);
+    const int ns = split_counts[gi];
     max_splits = std::max(max_splits, ns);
+    if (ns > 1) {  // merge item: (b, qb, qn, first work item, splits)
+      int32_t* w = work_h + (size_t)(n_work + m) * NSG_ATTN_WORK_INTS;
+      w[0] = g.b;
+      w[1] = g.qb;
+      w[2] = g.qn;
+      w[3] = n;
+      w[4] = ns;
+      w[5] = w[6] = w[7] = 0;
+      ++m;
+    }
     for (int s = 0; s < ns; ++s) {
-      if (n >= work_capacity || !work_h) {
-        set_error("work list needs more than %d items", work_capacity);
-        return NSG_ERR_WORKSPACE;
-      }
       int32_t* w = work_h + (size_t)n * NSG_ATTN_WORK_INTS;
       w[0] = g.b;
       w[1] = g.qb;
@@ -519,6 +519,7 @@ extern "C" int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_i
     }
   }
   plan->num_work = n;
+  plan->num_merge = m;
   plan->num_groups = (int)groups.size();
   plan->row_tiles = RT;
   plan->q_tile_tokens = T;
@@ -527,7 +528,7 @@ extern "C" int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_i
   plan->num_qo_heads = num_qo_heads;
   plan->num_kv_heads = num_kv_heads;
   plan->workspace_bytes =
-      kHeaderBytes + kCounterBytes + (int64_t)n * num_kv_heads * RT * 16 * (head_dim + 4) * 4;
+      kHeaderBytes + (int64_t)n * num_kv_heads * RT * 16 * (head_dim + 4) * 4;
   clear_error();
   return NSG_OK;
 }
@@ -575,11 +576,11 @@ extern "C" int32_t nsg_attn_run(const nsg_attn_plan_t* plan, const int32_t* work
   prm.scale_log2 = sm_scale * 1.4426950408889634f;
   char* ws = static_cast<char*>(workspace);
   prm.flags = reinterpret_cast<int*>(ws);
-  prm.counters = reinterpret_cast<int*>(ws + kHeaderBytes);
-  prm.partials = reinterpret_cast<float*>(ws + kHeaderBytes + kCounterBytes);
+  prm.partials = reinterpret_cast<float*>(ws + kHeaderBytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (plan->head_dim == 64) return launch_d<64>(plan, prm, s);
-  if (plan->head_dim == 128) return launch_d<128>(plan, prm, s);
+  const int* merge = work_d + (size_t)plan->num_work * NSG_ATTN_WORK_INTS;
+  if (plan->head_dim == 64) return launch_d<64>(plan, prm, merge, s);
+  if (plan->head_dim == 128) return launch_d<128>(plan, prm, merge, s);
   set_error("head_dim %d not supported", plan->head_dim);
   return NSG_ERR_UNSUPPORTED;
 }

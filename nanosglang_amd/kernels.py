@@ -110,7 +110,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
             ql = int(qo_h[b + 1] - qo_h[b])
             npg = int(kvp_h[b + 1] - kvp_h[b])
             L = (npg - 1) * page_size + int(last_h[b]) if npg else 0
-            bound += math.ceil(ql / T) * max(1, math.ceil(L / 32))
+            bound += math.ceil(ql / T) * (1 + max(1, math.ceil(L / 32)))
         if bound > self._work_cap:
             self._work_cap = max(bound, 2 * self._work_cap, 64)
             self._work_h = np.zeros(self._work_cap * NSG_ATTN_WORK_INTS, np.int32)
@@ -126,7 +126,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
             raise RuntimeError(
                 f"attention workspace too small: plan needs {pl.workspace_bytes} bytes, "
                 f"buffer has {self._ws.numel() * self._ws.element_size()}")
-        n = pl.num_work * NSG_ATTN_WORK_INTS
+        n = (pl.num_work + pl.num_merge) * NSG_ATTN_WORK_INTS
         if n:
             self._work_d[:n].copy_(torch.from_numpy(self._work_h[:n]), non_blocking=False)
         self._plan = pl

@@ -1,0 +1,250 @@
+"""Benchmark of the speculative-decoding verify step on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
+
+Prints ONE JSON line.  ``value`` is end-to-end speculative-decoding
+throughput (emitted tokens / wall time, prefill included) of the workload
+"0.5B-shape spec decode": a random-init Qwen2.5-0.5B-shape target (24 layers,
+hidden 896, 14 q / 2 kv heads, head dim 64, FFN 4864, vocab 151936, RoPE
+theta 1e6, bf16), a draft made of its first 4 layers with the shared
+embedding / norm / lm_head, k = 4, greedy verification, 32 requests admitted
+together with prompts of uniform-random ids and lengths U[100, 512], outputs
+of U[64, 128] tokens (EOS ignored), paged KV of 8000 blocks x 16 tokens.
+One step = one full pass of that workload.
+
+``roofline`` is the verify-attention kernel at the verify shape of that
+workload (batch 32, 5 query tokens, 14/2 heads, D 64, page 16, KV lengths
+U[100, 640], pages scattered over an 8000-block pool): algorithmic bytes per
+launch / mean launch time from HIP events on the launch stream, with 16 pool
+copies (~1 GB) rotated so no launch is served from the 256 MB Infinity Cache.
+``kernels`` adds the acceptance kernels (batch 64, k 4, vocab 151936, T 0.8,
+three rotated buffer sets) and the large verify shape (Llama-3-8B heads,
+k 8, batch 64, KV U[2048, 8192]).  ``cpu_baseline`` times the oracle's fp32
+PyTorch CPU speculative loop (batch 1, the reference's own algorithm) on a
+bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def c4_workload(seed=0, n=32, vocab=151936):
+    rng = np.random.default_rng(seed)
+    plens = rng.integers(100, 513, n)
+    prompts = [rng.integers(0, vocab, int(L)).tolist() for L in plens]
+    outs = rng.integers(64, 129, n).tolist()
+    return prompts, outs
+
+
+def event_time_us(torch, fn, n):
+    """Mean duration of fn(i) over n launches, each bracketed by its own pair
+    of HIP events on the current (launch) stream."""
+    pairs = []
+    for i in range(n):
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn(i)
+        e.record()
+        pairs.append((s, e))
+    torch.cuda.synchronize()
+    return float(np.mean([s.elapsed_time(e) for s, e in pairs])) * 1e3
+
+
+def bench_verify_attention(torch, w, dev, reps=160, pools=16, shape=None):
+    from nanosglang_amd import workloads
+    from nanosglang_amd.kernels import BatchPrefillWithPagedKVCacheWrapper
+    shape = shape or {}
+    c = workloads.verify_attention_batch(seed=0, **shape)
+    Hq, Hkv, D = c["q"].shape[1], c["k"].shape[2], c["k"].shape[3]
+    B = len(c["kv_lens"])
+    k0 = torch.from_numpy(c["k"]).to(dev).bfloat16()
+    v0 = torch.from_numpy(c["v"]).to(dev).bfloat16()
+    ks = [k0] + [k0.clone() for _ in range(pools - 1)]
+    vs = [v0] + [v0.clone() for _ in range(pools - 1)]
+    q = torch.from_numpy(c["q"]).to(dev).bfloat16()
+    ws = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    wr = BatchPrefillWithPagedKVCacheWrapper(ws)
+    wr.plan(c["qo_indptr"], c["kv_indptr"], c["kv_indices"], c["kv_last_page_len"], Hq, Hkv, D,
+            c["page_size"])
+    out = torch.empty_like(q)
+    for i in range(2 * pools):
+        wr.run(q, (ks[i % pools], vs[i % pools]), out=out)
+    t = event_time_us(torch, lambda i: wr.run(q, (ks[i % pools], vs[i % pools]), out=out), reps)
+    nbytes = workloads.algorithmic_bytes_verify_attention(
+        c["kv_lens"], c["qo_indptr"][-1], Hq, Hkv, D, B, c["kv_indptr"][-1])
+    pi = wr.plan_info
+    flops = 0
+    for b in range(B):
+        ql, L = int(c["q_lens"][b]), int(c["kv_lens"][b])
+        flops += 4 * Hq * D * sum(L - ql + r + 1 for r in range(ql))
+    del ks, vs
+    return {"us": t, "bytes": nbytes, "gbs": nbytes / t / 1e3, "flops": flops,
+            "work_items": pi.num_work, "merge_items": pi.num_merge, "pools_rotated": pools}
+
+
+def bench_acceptance(torch, dev, greedy, sets=3, reps=60, **kw):
+    from nanosglang_amd import workloads
+    from nanosglang_amd.kernels import philox_uniform, spec_accept
+    a = workloads.acceptance_batch(seed=0, **kw)
+    B, k1, V = a["target"].shape
+    k = k1 - 1
+    tl = torch.from_numpy(a["target"]).to(dev).bfloat16()
+    dl = torch.from_numpy(a["draft"]).to(dev).bfloat16()
+    dt = torch.from_numpy(a["draft_tokens"]).to(dev)
+    u = philox_uniform(123, 0, 0, B * k1, dev).view(B, k1)
+    bufs = [(tl, dl)] + [(tl.clone(), dl.clone()) for _ in range(sets - 1)]
+    T = 0.0 if greedy else a["temperature"]
+
+    def call(i):
+        t_, d_ = bufs[i % sets]
+        spec_accept(t_, None if greedy else d_, dt, None if greedy else u, T)
+
+    for i in range(2 * sets):
+        call(i)
+    t = event_time_us(torch, call, reps)
+    nbytes = workloads.algorithmic_bytes_acceptance(B, k, V, greedy)
+    return {"us": t, "bytes": nbytes, "gbs": nbytes / t / 1e3, "sets_rotated": sets}
+
+
+def cpu_baseline(prompts, outs, n_tokens=16):
+    """The oracle's fp32 PyTorch CPU speculative loop on request 0 of the
+    workload (prompt + n_tokens outputs), batch 1, k 4, 4-layer draft."""
+    import torch
+    sys.path.insert(0, ROOT)
+    from oracle.model import CPUCausalLM, CPUSpeculativeDecoder, ModelConfig, init_weights
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    cfg = ModelConfig()
+    w = init_weights(cfg, seed=0)
+    target = CPUCausalLM(cfg, w, max_pos=1024)
+    draft = CPUCausalLM(cfg, w, num_layers=4, max_pos=1024)
+    spec = CPUSpeculativeDecoder(draft, target, 4, temperature=0.0)
+    p = prompts[0]
+    spec.generate(p[:16], 2)                   # warm-up
+    t0 = time.perf_counter()
+    out = spec.generate(p, n_tokens)
+    dt = time.perf_counter() - t0
+    return {"value": len(out) / dt, "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"request 0 of the workload (prompt {len(p)} tokens) -> {n_tokens} output "
+                      f"tokens, batch 1, fp32, k=4, 4-layer draft, greedy, prefill included; "
+                      f"{dt:.1f} s", "seconds": dt,
+            "torch": torch.__version__}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-kernels", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the verify "
+              f"step runs on a single MI355X in this build.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    sys.path.insert(0, ROOT)
+    from nanosglang_amd.engine.spec_engine import SpecEngine
+    from nanosglang_amd.model.causal_lm import CausalLM, ModelConfig
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    prompts, outs = c4_workload()
+    log(f"workload: {len(prompts)} requests, prompt tokens {sum(map(len, prompts))}, "
+        f"output tokens {sum(outs)}")
+    model = CausalLM(ModelConfig(), device=dev, seed=0)
+    engine = SpecEngine(model, draft_layers=4, num_speculative=4, num_blocks=8000,
+                        block_size=16, temperature=0.0)
+    for w in range(args.warmup):
+        engine.generate(prompts, outs)
+        log(f"warmup {w}: {engine.stats}")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n_tok = 0
+    stats = []
+    for s in range(args.steps):
+        res = engine.generate(prompts, outs)
+        n_tok += sum(len(r) for r in res)
+        stats.append(dict(engine.stats))
+        log(f"step {s}: {engine.stats}")
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    value = n_tok / elapsed
+
+    result = {
+        "metric": "spec-decode tok/s (0.5B-shape, k=4, bs=32); verify-attn & accept % HBM peak",
+        "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 2),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init weights, uniform-random prompt ids)",
+        "config": {"workload": "0.5B-shape spec decode: 24-layer target / 4-layer draft, k=4, "
+                               "32 requests, prompts U[100,512], outputs U[64,128], greedy, "
+                               "paged KV 8000x16",
+                   "batch": 32, "k": 4, "page_size": 16, "num_blocks": 8000},
+        "decode_tok_per_s": round(float(np.mean([s["decode_tok_per_s"] for s in stats])), 1),
+        "acceptance_rate": round(float(np.mean([s["acceptance_rate"] for s in stats])), 4),
+        "tokens_per_step": round(float(np.mean([s["tokens_per_step"] for s in stats])), 3),
+        "prefill_s": round(float(np.mean([s["prefill_s"] for s in stats])), 4),
+    }
+    del engine, model
+    torch.cuda.empty_cache()
+
+    if not args.skip_kernels:
+        va = bench_verify_attention(torch, None, dev)
+        log(f"verify attention (verify shape): {va}")
+        result["roofline"] = {
+            "bound": "hbm", "achieved": round(va["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(va["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "verify attention (verify_attn_kernel + verify_merge_kernel), batch 32, "
+                      "5 query tokens, 14/2 heads, D 64",
+            "us_per_launch": round(va["us"], 2), "algorithmic_bytes": va["bytes"]}
+        acc_s = bench_acceptance(torch, dev, greedy=False)
+        log(f"acceptance stochastic: {acc_s}")
+        acc_g = bench_acceptance(torch, dev, greedy=True)
+        log(f"acceptance greedy: {acc_g}")
+        big = bench_verify_attention(torch, None, dev, reps=20, pools=1, shape=dict(
+            batch=64, q_len=9, num_qo_heads=32, num_kv_heads=8, head_dim=128, min_len=2048,
+            max_len=8192, num_pages=21000))
+        log(f"verify attention (large shape): {big}")
+
+        def k_entry(d):
+            e = {"us": round(d["us"], 2), "algorithmic_bytes": d["bytes"],
+                 "achieved_gbs": round(d["gbs"], 1), "frac_hbm": round(d["gbs"] / HBM_PEAK_GBS, 4)}
+            if "flops" in d:
+                e["tflops"] = round(d["flops"] / d["us"] / 1e6, 2)
+            return e
+
+        result["kernels"] = {
+            "verify_attention_verify_shape": k_entry(va),
+            "acceptance_stochastic_b64_k4_v151936": k_entry(acc_s),
+            "acceptance_greedy_b64_k4_v151936": k_entry(acc_g),
+            "verify_attention_large_shape": k_entry(big),
+        }
+
+    if not args.skip_cpu:
+        cb = cpu_baseline(prompts, outs)
+        log(f"cpu baseline: {cb}")
+        result["cpu_baseline"] = {k: cb[k] for k in ("value", "unit", "cores", "kind", "sample")}
+        result["cpu_baseline"]["value"] = round(cb["value"], 3)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -153,6 +153,23 @@ int32_t nsg_kv_write(const void* k, const void* v, int64_t src_token_stride,
                      void* v_cache, int32_t num_kv_heads, int32_t head_dim,
                      int64_t num_slots, nsg_stream_t stream);
 
+/* Fused RoPE + KV slot write for one layer.  qkv: num_tokens rows of the
+ * fused projection [q heads | k heads | v heads] x head_dim (bf16, rows
+ * qkv_token_stride elements apart); positions int64; cos/sin tables fp32
+ * [max_position, head_dim/2] (nano_sglang/model/causal_lm.py:157-164).
+ * q and k are rotated with the half-split rule and bf16 rounding of
+ * causal_lm.py:167-206; rotated q -> q_out [num_tokens, Hq, D]; rotated k and
+ * v -> flat slot slots[t] of the layer's pool (slot < 0 skips; slots may be
+ * NULL to skip the cache write).  Replaces apply_rope (causal_lm.py:300-301)
+ * plus the scatter at causal_lm.py:335-338.  Positions outside
+ * [0, max_position) or slots >= num_slots set bit 0 of *flags (if given). */
+int32_t nsg_rope_kv_write(const void* qkv, int64_t qkv_token_stride, const int64_t* positions,
+                          const float* cos_table, const float* sin_table,
+                          int32_t max_position, const int64_t* slots, int32_t num_tokens,
+                          int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                          void* q_out, void* k_cache, void* v_cache, int64_t num_slots,
+                          int32_t* flags, nsg_stream_t stream);
+
 /* Zero the K and V rows of `count` flat slots (negative slots are skipped)
  * in `num_layers` consecutive layer pools, layer_stride elements apart.
  * Used after nsg_spec_accept so rolled-back positions hold no stale data. */

@@ -69,6 +69,62 @@ __global__ void kv_clear_kernel(const int64_t* __restrict__ slots, int count,
   *reinterpret_cast<u32x4*>(vc + off) = u32x4{0u, 0u, 0u, 0u};
 }
 
+__device__ __forceinline__ float bf16r(float x) {  // round to bf16, back to float
+  return bf16_bits_to_float(float_to_bf16_bits(x));
+}
+
+// One workgroup per token.  Work item (head hh, pair i): q / k heads are
+// rotated with the half-split rule y[i] = x[i] c - x[i+D/2] s,
+// y[i+D/2] = x[i+D/2] c + x[i] s, every product and the sum rounded to bf16
+// and c, s rounded to bf16 first -- the arithmetic of bf16 tensors in
+// nano_sglang/model/causal_lm.py:181-206.  Rotated q goes to q_out; rotated k
+// and v go to the cache slot of the token (slot < 0 skips).
+__global__ void rope_kv_write_kernel(const uint16_t* __restrict__ qkv, int64_t qkv_stride,
+                                     const int64_t* __restrict__ positions,
+                                     const float* __restrict__ cos_t,
+                                     const float* __restrict__ sin_t, int max_pos,
+                                     const int64_t* __restrict__ slots, int Hq, int Hkv, int D,
+                                     uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
+                                     uint16_t* __restrict__ vc, int64_t num_slots,
+                                     int* __restrict__ flags) {
+  const int t = blockIdx.x;
+  const int half = D / 2;
+  const int64_t pos = positions[t];
+  const bool pos_ok = pos >= 0 && pos < max_pos;
+  const int64_t slot = slots ? slots[t] : -1;
+  const bool slot_ok = slot >= 0 && slot < num_slots;
+  if (threadIdx.x == 0 && (!pos_ok || slot >= num_slots) && flags) atomicOr(flags, 1);
+  const uint16_t* x = qkv + t * qkv_stride;
+  const int items = (Hq + 2 * Hkv) * half;
+  for (int it = threadIdx.x; it < items; it += blockDim.x) {
+    const int hh = it / half;
+    const int i = it - hh * half;
+    const float x1 = bf16_bits_to_float(x[hh * D + i]);
+    const float x2 = bf16_bits_to_float(x[hh * D + i + half]);
+    uint16_t y1, y2;
+    if (hh < Hq + Hkv) {
+      const float c = pos_ok ? bf16r(cos_t[pos * half + i]) : 0.f;
+      const float sn = pos_ok ? bf16r(sin_t[pos * half + i]) : 0.f;
+      y1 = float_to_bf16_bits(bf16r(x1 * c) + bf16r(-x2 * sn));
+      y2 = float_to_bf16_bits(bf16r(x2 * c) + bf16r(x1 * sn));
+    } else {
+      y1 = x[hh * D + i];
+      y2 = x[hh * D + i + half];
+    }
+    if (hh < Hq) {
+      uint16_t* qo = q_out + ((int64_t)t * Hq + hh) * D;
+      qo[i] = y1;
+      qo[i + half] = y2;
+    } else if (slot_ok) {
+      const bool is_k = hh < Hq + Hkv;
+      const int kh = is_k ? hh - Hq : hh - Hq - Hkv;
+      uint16_t* dst = (is_k ? kc : vc) + (slot * Hkv + kh) * D;
+      dst[i] = y1;
+      dst[i + half] = y2;
+    }
+  }
+}
+
 __device__ __forceinline__ void philox_round(uint32_t& c0, uint32_t& c1, uint32_t& c2,
                                              uint32_t& c3, uint32_t k0, uint32_t k1) {
   const uint64_t p0 = (uint64_t)0xD2511F53u * c0;
@@ -165,6 +221,35 @@ extern "C" int32_t nsg_kv_clear_slots(const int64_t* slots, int32_t count, void*
                      static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), num_layers,
                      layer_stride, row, num_slots);
   return launch_status("kv_clear_kernel");
+}
+
+extern "C" int32_t nsg_rope_kv_write(const void* qkv, int64_t qkv_token_stride,
+                                     const int64_t* positions, const float* cos_table,
+                                     const float* sin_table, int32_t max_position,
+                                     const int64_t* slots, int32_t num_tokens,
+                                     int32_t num_qo_heads, int32_t num_kv_heads,
+                                     int32_t head_dim, void* q_out, void* k_cache,
+                                     void* v_cache, int64_t num_slots, int32_t* flags,
+                                     nsg_stream_t stream) {
+  NSG_CHECK_ARG(num_tokens >= 0, "num_tokens %d < 0", num_tokens);
+  if (num_tokens == 0) {
+    clear_error();
+    return NSG_OK;
+  }
+  NSG_CHECK_ARG(qkv && positions && cos_table && sin_table && q_out, "null pointer argument");
+  NSG_CHECK_ARG(!slots || (k_cache && v_cache), "slots given without caches");
+  NSG_CHECK_ARG(head_dim > 0 && head_dim % 2 == 0, "head_dim %d must be even", head_dim);
+  NSG_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0, "head counts must be positive");
+  NSG_CHECK_ARG(qkv_token_stride >= (int64_t)(num_qo_heads + 2 * num_kv_heads) * head_dim,
+                "qkv_token_stride %lld too small", (long long)qkv_token_stride);
+  NSG_CHECK_ARG(max_position > 0, "max_position %d", max_position);
+  hipLaunchKernelGGL(rope_kv_write_kernel, dim3(num_tokens), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(qkv),
+                     qkv_token_stride, positions, cos_table, sin_table, max_position, slots,
+                     num_qo_heads, num_kv_heads, head_dim, static_cast<uint16_t*>(q_out),
+                     static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), num_slots,
+                     flags);
+  return launch_status("rope_kv_write_kernel");
 }
 
 extern "C" int32_t nsg_philox_uniform(uint64_t seed, uint32_t stream_id, uint64_t offset,

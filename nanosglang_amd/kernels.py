@@ -318,6 +318,35 @@ def kv_clear_slots(slots: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Te
                                     _stream_ptr(k_cache.device)), "nsg_kv_clear_slots")
 
 
+def rope_kv_write(qkv: torch.Tensor, num_qo_heads: int, num_kv_heads: int, head_dim: int,
+                  positions: torch.Tensor, cos_table: torch.Tensor, sin_table: torch.Tensor,
+                  slots: torch.Tensor | None, k_cache: torch.Tensor | None,
+                  v_cache: torch.Tensor | None, q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused RoPE of q, k plus the KV slot write (C ABI: nsg_rope_kv_write).
+
+    qkv: (T, (Hq + 2 Hkv) * D) bf16 rows of the fused projection (unit inner
+    stride); positions int64 (T,); cos/sin fp32 (max_pos, D/2); caches: one
+    layer's (N, P, Hkv, D) pool.  Returns rotated q (T, Hq, D)."""
+    _require_gpu(qkv, "qkv")
+    T = qkv.shape[0]
+    if qkv.dtype != torch.bfloat16 or qkv.stride(-1) != 1:
+        raise ValueError("qkv must be bfloat16 with unit inner stride")
+    if q_out is None:
+        q_out = torch.empty(T, num_qo_heads, head_dim, dtype=torch.bfloat16, device=qkv.device)
+    positions = positions.to(torch.int64).contiguous()
+    if slots is not None:
+        slots = slots.to(torch.int64).contiguous()
+        num_slots = k_cache.numel() // (num_kv_heads * head_dim)
+    else:
+        num_slots = 0
+    check(_lib().nsg_rope_kv_write(
+        qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), cos_table.data_ptr(),
+        sin_table.data_ptr(), cos_table.shape[0], _ptr(slots), T, num_qo_heads, num_kv_heads,
+        head_dim, q_out.data_ptr(), _ptr(k_cache), _ptr(v_cache), num_slots, None,
+        _stream_ptr(qkv.device)), "nsg_rope_kv_write")
+    return q_out
+
+
 def philox_uniform(seed: int, stream_id: int, offset: int, n: int, device) -> torch.Tensor:
     """n float32 uniforms of Philox4x32-10 stream ``stream_id`` (see nsg_spec.h)."""
     out = torch.empty(n, dtype=torch.float32, device=device)

@@ -1,0 +1,162 @@
+"""Qwen2 / Llama decoder on one MI355X for the speculative verify path.
+
+Mirrors nano_sglang/model/causal_lm.py where the verify path needs it:
+``ModelConfig`` (:77-101), pre-norm decoder layers with fused residual +
+RMSNorm (:474-532), SwiGLU MLP (:481-482), tied embedding / lm_head, and the
+packed forward ``forward_packed(input_ids, positions, kv_cache, attn_wrapper,
+write_indices, logit_indices)`` of the FlashInfer path (:585-646), where each
+layer writes its K/V into the paged pool and runs paged attention
+(:329-342).
+
+MI355X-side choices:
+* q/k/v are one fused GEMM (and gate/up another), via torch / hipBLASLt;
+* RoPE + KV-slot write is one HIP kernel (``kernels.rope_kv_write``) with
+  the reference's bf16 rounding order; attention is the HIP verify-attention
+  kernel behind ``BatchPrefillWithPagedKVCacheWrapper``;
+* RMSNorm uses the reference's fp32-variance formula (:142-145);
+* a draft made of the first ``n`` layers plus the shared embedding, final
+  norm and lm_head is ``forward_packed(..., num_layers=n)`` on the same
+  weights.
+
+Random init (no checkpoints offline): every linear and embedding weight
+~ N(0, 0.02), RMSNorm weights 1, q/k/v biases 0, drawn on the device from a
+seeded generator; or pass ``weights`` (the layout of a dict of fp32 tensors
+with keys embed / layers[q,k,v,o,gate,up,down,qb,kb,vb,ln1,ln2] / norm).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from .. import kernels
+
+
+@dataclass
+class ModelConfig:
+    """nano_sglang/model/causal_lm.py:77-101 (defaults: Qwen2.5-0.5B shape)."""
+    model_type: str = "qwen2"
+    vocab_size: int = 151936
+    hidden_size: int = 896
+    intermediate_size: int = 4864
+    num_hidden_layers: int = 24
+    num_attention_heads: int = 14
+    num_key_value_heads: int = 2
+    max_position_embeddings: int = 4096
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1e6
+    tie_word_embeddings: bool = True
+    attention_bias: bool = True
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_attention_heads
+
+
+def rope_tables(cfg: ModelConfig, device):
+    """causal_lm.py:157-164, computed in fp32 on the host then moved."""
+    D = cfg.head_dim
+    freqs = 1.0 / (cfg.rope_theta ** (torch.arange(0, D, 2).float() / D))
+    t = torch.arange(cfg.max_position_embeddings).float()
+    f = torch.outer(t, freqs)
+    return f.cos().contiguous().to(device), f.sin().contiguous().to(device)
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """causal_lm.py:142-145: fp32 variance, x * rsqrt, weight * x, cast back."""
+    dt = x.dtype
+    var = x.float().pow(2).mean(-1, keepdim=True)
+    return (weight * (x * torch.rsqrt(var + eps))).to(dt)
+
+
+class CausalLM:
+    def __init__(self, config: ModelConfig, device="cuda", dtype=torch.bfloat16, seed: int = 0,
+                 weights: dict | None = None):
+        self.config = c = config
+        self.device = torch.device(device)
+        self.dtype = dtype
+        H, D = c.hidden_size, c.head_dim
+        Hq, Hkv, I = c.num_attention_heads, c.num_key_value_heads, c.intermediate_size
+        if weights is None:
+            g = torch.Generator(device=self.device).manual_seed(seed)
+
+            def n(*shape):
+                return (torch.randn(*shape, generator=g, device=self.device,
+                                    dtype=torch.float32) * 0.02).to(dtype)
+
+            def z(*shape):
+                return torch.zeros(*shape, device=self.device, dtype=dtype)
+
+            def o(*shape):
+                return torch.ones(*shape, device=self.device, dtype=dtype)
+
+            self.embed = n(c.vocab_size, H)
+            self.layers = []
+            for _ in range(c.num_hidden_layers):
+                self.layers.append({
+                    "qkv": torch.cat([n(Hq * D, H), n(Hkv * D, H), n(Hkv * D, H)]),
+                    "qkv_b": z((Hq + 2 * Hkv) * D), "o": n(H, Hq * D),
+                    "gate_up": torch.cat([n(I, H), n(I, H)]), "down": n(H, I),
+                    "ln1": o(H), "ln2": o(H)})
+            self.norm = o(H)
+        else:
+            def d(t):
+                return t.to(self.device, dtype)
+
+            self.embed = d(weights["embed"])
+            self.layers = []
+            for L in weights["layers"]:
+                self.layers.append({
+                    "qkv": d(torch.cat([L["q"], L["k"], L["v"]])),
+                    "qkv_b": d(torch.cat([L["qb"], L["kb"], L["vb"]])), "o": d(L["o"]),
+                    "gate_up": d(torch.cat([L["gate"], L["up"]])), "down": d(L["down"]),
+                    "ln1": d(L["ln1"]), "ln2": d(L["ln2"])})
+            self.norm = d(weights["norm"])
+        self.lm_head = self.embed  # tie_word_embeddings
+        self.rope_cos, self.rope_sin = rope_tables(c, self.device)
+
+    @property
+    def num_layers(self) -> int:
+        return self.config.num_hidden_layers
+
+    @torch.inference_mode()
+    def forward_packed(self, input_ids: torch.Tensor, positions: torch.Tensor, kv_cache,
+                       attn_wrapper, write_indices: torch.Tensor,
+                       logit_indices: torch.Tensor | None = None,
+                       num_layers: int | None = None) -> torch.Tensor:
+        """Packed forward over ``T`` tokens of several requests.
+
+        kv_cache: (k_cache, v_cache) pools (L, N, P, Hkv, D); attn_wrapper: a
+        planned ``BatchPrefillWithPagedKVCacheWrapper``; write_indices: int64
+        flat slots (T,).  Returns logits (len(logit_indices) or T, V)."""
+        c = self.config
+        Hq, Hkv, D, I = (c.num_attention_heads, c.num_key_value_heads, c.head_dim,
+                         c.intermediate_size)
+        k_pool, v_pool = kv_cache
+        nl = self.num_layers if num_layers is None else num_layers
+        x = F.embedding(input_ids, self.embed)
+        residual = None
+        for li in range(nl):
+            L = self.layers[li]
+            if residual is None:
+                residual = x
+                h = rms_norm(x, L["ln1"], c.rms_norm_eps)
+            else:
+                residual = residual + x                          # causal_lm.py:505, 531
+                h = rms_norm(residual, L["ln1"], c.rms_norm_eps)
+            qkv = F.linear(h, L["qkv"], L["qkv_b"])
+            q = kernels.rope_kv_write(qkv, Hq, Hkv, D, positions, self.rope_cos, self.rope_sin,
+                                      write_indices, k_pool[li], v_pool[li])
+            attn = attn_wrapper.run(q, (k_pool[li], v_pool[li]))
+            x = F.linear(attn.view(-1, Hq * D), L["o"])
+            residual = residual + x                               # causal_lm.py:153
+            h = rms_norm(residual, L["ln2"], c.rms_norm_eps)
+            gu = F.linear(h, L["gate_up"])
+            x = F.linear(F.silu(gu[:, :I]) * gu[:, I:], L["down"])
+        x = residual + x
+        if logit_indices is not None:
+            x = x[logit_indices]
+        x = rms_norm(x, self.norm, c.rms_norm_eps)
+        return F.linear(x, self.lm_head)

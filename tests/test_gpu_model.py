@@ -1,0 +1,132 @@
+"""GPU parity of the model-side pieces of the verify path:
+* fused RoPE + KV write: bit-exact against the oracle's apply_rope evaluated
+  on bf16 tensors (the reference's rounding order) and the slot rule;
+* packed forward on the paged cache vs the CPU fp32 oracle forward
+  (bf16 tolerance) on a tiny random model;
+* the speculative engine: greedy output equals plain greedy decoding
+  (k = 0, one verify token per step) on the GPU -- the speculative-sampling
+  invariant; the first divergence from the CPU fp32 oracle is reported.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle.model import CPUCausalLM, CPUSpeculativeDecoder, ModelConfig as OCfg
+from oracle.model import apply_rope as oracle_rope, causal_mask, greedy_decode, init_weights
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(vocab_size=1000, hidden_size=256, intermediate_size=512, num_hidden_layers=4,
+            num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=1024)
+
+
+def test_rope_kv_write_bit_exact():
+    from nanosglang_amd.kernels import rope_kv_write
+    from nanosglang_amd.model.causal_lm import ModelConfig, rope_tables
+    cfg = ModelConfig(**TINY)
+    Hq, Hkv, D = 4, 2, 64
+    T = 37
+    g = torch.Generator().manual_seed(0)
+    qkv = torch.randn(T, (Hq + 2 * Hkv) * D, generator=g).bfloat16()
+    pos = torch.randint(0, 1024, (T,), generator=g)
+    cos, sin = rope_tables(cfg, "cpu")
+    slots = torch.randperm(50 * 16, generator=g)[:T]
+    kc = torch.zeros(50, 16, Hkv, D, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    q = rope_kv_write(qkv.cuda(), Hq, Hkv, D, pos.cuda(), cos.cuda(), sin.cuda(), slots.cuda(),
+                      kc, vc)
+    torch.cuda.synchronize()
+    x = qkv.view(T, Hq + 2 * Hkv, D).transpose(0, 1)[None]        # (1, heads, T, D) bf16
+    ref = oracle_rope(x, cos, sin, pos[None])[0].transpose(0, 1)   # bf16 arithmetic on CPU
+    assert torch.equal(q.cpu(), ref[:, :Hq])
+    flat_k = kc.view(-1, Hkv, D).cpu()
+    flat_v = vc.view(-1, Hkv, D).cpu()
+    assert torch.equal(flat_k[slots], ref[:, Hq:Hq + Hkv])
+    assert torch.equal(flat_v[slots], qkv.view(T, -1, D)[:, Hq + Hkv:])
+
+
+def _tiny_models(scale=8.0, dtype=torch.float32):
+    """Tiny random model; scale > 1 makes next-token choices non-trivial.  The
+    CPU oracle runs in ``dtype`` (bf16 reproduces the reference's GPU
+    arithmetic: bf16 weights, activations and cache, fp32 softmax)."""
+    from nanosglang_amd.model.causal_lm import CausalLM, ModelConfig
+    ocfg = OCfg(**TINY)
+    w = init_weights(ocfg, seed=3)
+    for L in w["layers"]:
+        for key in ("q", "k", "v", "o", "gate", "up", "down"):
+            L[key] *= scale
+    wc = w if dtype == torch.float32 else {
+        "embed": w["embed"].to(dtype), "norm": w["norm"].to(dtype),
+        "layers": [{k: v.to(dtype) for k, v in L.items()} for L in w["layers"]]}
+    return CPUCausalLM(ocfg, wc), CausalLM(ModelConfig(**TINY), weights=w)
+
+
+@pytest.mark.parametrize("scale,dtype,tol", [(1.0, torch.float32, 2e-2),
+                                             (3.0, torch.bfloat16, 5e-2)])
+def test_packed_forward_matches_cpu_oracle(scale, dtype, tol):
+    """bf16 GPU logits vs the oracle: at init scale against fp32 (relative
+    error 2e-2), with 3x weights against the oracle in bf16 (5e-2; the oracle's
+    own bf16-vs-fp32 gap there is 2.3e-2).  Argmax agreement >= 0.9: with 1000
+    random logits even the oracle's bf16 and fp32 runs agree on only ~0.96-0.98
+    of positions."""
+    from nanosglang_amd.engine.paged_kv_cache import BlockManager, PagedKVCache
+    from nanosglang_amd.kernels import BatchPrefillWithPagedKVCacheWrapper
+    cpu, gpu = _tiny_models(scale, dtype)
+    rng = np.random.default_rng(0)
+    prompts = [rng.integers(0, 1000, n).tolist() for n in (40, 7, 129)]
+    bm = BlockManager(64, 16, 4, 2, 64, torch.bfloat16, "cuda")
+    kv = PagedKVCache(bm)
+    tables = [kv.allocate_for_request(len(p)) for p in prompts]
+    lens = [len(p) for p in prompts]
+    qo = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    kvp = np.concatenate([[0], np.cumsum([t.num_blocks for t in tables])]).astype(np.int32)
+    idx = np.concatenate([t.block_indices for t in tables]).astype(np.int32)
+    last = np.asarray([(n % 16) or 16 for n in lens], np.int32)
+    w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(32 << 20, dtype=torch.uint8, device="cuda"))
+    w.plan(qo, kvp, idx, last, 4, 2, 64, 16, causal=True)
+    ids = torch.tensor(np.concatenate(prompts), device="cuda")
+    pos = torch.tensor(np.concatenate([np.arange(n) for n in lens]), device="cuda")
+    slots = torch.tensor(np.concatenate([kv.slots(t, 0, n) for t, n in zip(tables, lens)]),
+                         device="cuda")
+    got = gpu.forward_packed(ids, pos, (bm.k_cache, bm.v_cache), w, slots).float().cpu()
+    off = 0
+    for p in prompts:
+        S = len(p)
+        cache = [(a.to(dtype), b.to(dtype)) for a, b in cpu.new_cache(1, S)]
+        ref = cpu.forward(torch.tensor([p]), torch.arange(S)[None], cache, 0,
+                          causal_mask(S, S, dtype))[0].float()
+        g = got[off:off + S]
+        rel = ((g - ref).norm(dim=-1) / ref.norm(dim=-1)).max().item()
+        agree = (g.argmax(-1) == ref.argmax(-1)).float().mean().item()
+        print(f"  S={S} max rel err {rel:.3e} argmax agreement {agree:.3f}", flush=True)
+        assert rel < tol
+        assert agree >= 0.9
+        off += S
+
+
+def test_spec_engine_greedy_equals_plain_greedy_and_oracle():
+    from nanosglang_amd.engine.spec_engine import SpecEngine
+    cpu, gpu = _tiny_models()
+    rng = np.random.default_rng(1)
+    prompts = [rng.integers(0, 1000, n).tolist() for n in (20, 33, 5, 64)]
+    max_new = [24, 17, 30, 9]
+    spec = SpecEngine(gpu, draft_layers=2, num_speculative=4, num_blocks=64)
+    out_spec = spec.generate(prompts, max_new)
+    st = spec.stats
+    print(f"  spec: acceptance {st['acceptance_rate']:.2f} tokens/step {st['tokens_per_step']:.2f}",
+          flush=True)
+    plain = SpecEngine(gpu, draft_layers=2, num_speculative=0, num_blocks=64)
+    out_plain = plain.generate(prompts, max_new)
+    assert [len(o) for o in out_spec] == max_new
+    assert spec.bm.num_free_blocks == 64 and plain.bm.num_free_blocks == 64
+    same = sum(a == b for a, b in zip(out_spec, out_plain))
+    print(f"  spec == plain greedy for {same}/{len(prompts)} requests", flush=True)
+    assert same == len(prompts)
+    # CPU fp32 oracle on the same weights: reported, not asserted -- with 8x
+    # weights bf16 and fp32 logits disagree on ~9% of argmaxes even between
+    # the oracle's own bf16 and fp32 runs, so token streams part early.
+    draft = CPUCausalLM(cpu.cfg, cpu.w, num_layers=2)
+    for p, m, o in zip(prompts, max_new, out_spec):
+        ref = CPUSpeculativeDecoder(draft, cpu, 4).generate(p, m)
+        first = next((i for i, (a, b) in enumerate(zip(o, ref)) if a != b), len(o))
+        print(f"  prompt {len(p)}: first divergence from CPU oracle at {first}/{m}", flush=True)

@@ -15,8 +15,9 @@ One step = one full pass of that workload.
 ``roofline`` is the verify-attention kernel at the verify shape of that
 workload (batch 32, 5 query tokens, 14/2 heads, D 64, page 16, KV lengths
 U[100, 640], pages scattered over an 8000-block pool): algorithmic bytes per
-launch / mean launch time from HIP events on the launch stream, with 16 pool
-copies (~1 GB) rotated so no launch is served from the 256 MB Infinity Cache.
+launch / mean launch time, timed with HIP events around replays of a HIP
+graph of 160 launches on the launch stream, with 16 pool copies (~1 GB)
+rotated so no launch is served from the 256 MB Infinity Cache.
 ``kernels`` adds the acceptance kernels (batch 64, k 4, vocab 151936, T 0.8,
 three rotated buffer sets) and the large verify shape (Llama-3-8B heads,
 k 8, batch 64, KV U[2048, 8192]).  ``cpu_baseline`` times the oracle's fp32
@@ -50,19 +51,28 @@ def c4_workload(seed=0, n=32, vocab=151936):
     return prompts, outs
 
 
-def event_time_us(torch, fn, n):
-    """Mean duration of fn(i) over n launches, each bracketed by its own pair
-    of HIP events on the current (launch) stream."""
-    pairs = []
-    for i in range(n):
+def graph_time_us(torch, fn, n, reps=5):
+    """Mean per-launch time of fn(0..n-1) captured in one HIP graph: HIP
+    events on the replay stream bracket each replay (median of reps), so host
+    launch latency is excluded and the time is the GPU's, including the
+    dispatch gaps between the graph's kernels."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
         s = torch.cuda.Event(enable_timing=True)
         e = torch.cuda.Event(enable_timing=True)
         s.record()
-        fn(i)
+        g.replay()
         e.record()
-        pairs.append((s, e))
-    torch.cuda.synchronize()
-    return float(np.mean([s.elapsed_time(e) for s, e in pairs])) * 1e3
+        torch.cuda.synchronize()
+        ts.append(s.elapsed_time(e) * 1e3 / n)
+    del g
+    return float(np.median(ts))
 
 
 def bench_verify_attention(torch, w, dev, reps=160, pools=16, shape=None):
@@ -84,7 +94,7 @@ def bench_verify_attention(torch, w, dev, reps=160, pools=16, shape=None):
     out = torch.empty_like(q)
     for i in range(2 * pools):
         wr.run(q, (ks[i % pools], vs[i % pools]), out=out)
-    t = event_time_us(torch, lambda i: wr.run(q, (ks[i % pools], vs[i % pools]), out=out), reps)
+    t = graph_time_us(torch, lambda i: wr.run(q, (ks[i % pools], vs[i % pools]), out=out), reps)
     nbytes = workloads.algorithmic_bytes_verify_attention(
         c["kv_lens"], c["qo_indptr"][-1], Hq, Hkv, D, B, c["kv_indptr"][-1])
     pi = wr.plan_info
@@ -116,7 +126,7 @@ def bench_acceptance(torch, dev, greedy, sets=3, reps=60, **kw):
 
     for i in range(2 * sets):
         call(i)
-    t = event_time_us(torch, call, reps)
+    t = graph_time_us(torch, call, reps)
     nbytes = workloads.algorithmic_bytes_acceptance(B, k, V, greedy)
     return {"us": t, "bytes": nbytes, "gbs": nbytes / t / 1e3, "sets_rotated": sets}
 

@@ -178,6 +178,23 @@ int32_t nsg_kv_clear_slots(const int64_t* slots, int32_t count, void* k_cache, v
                            int32_t head_dim, int64_t num_slots, nsg_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Fused per-token layer ops of the draft / verify forwards.
+ * ---------------------------------------------------------------------- */
+
+/* RMSNorm of num_tokens rows of `hidden` bf16 values (hidden % 8 == 0,
+ * <= 8192): out = bf16(w * (x * rsqrt(mean(x^2) + eps))) in fp32
+ * (nano_sglang/model/causal_lm.py:139-145).  With residual != NULL it first
+ * does residual = bf16(residual + x) in place and normalises the sum
+ * (forward_fused_residual, causal_lm.py:147-154). */
+int32_t nsg_rmsnorm(const void* x, void* residual, const void* weight, void* out,
+                    int32_t num_tokens, int32_t hidden, float eps, nsg_stream_t stream);
+
+/* SwiGLU gate: gate_up rows hold [gate | up] (2 * intermediate bf16 each);
+ * out[t, j] = bf16(bf16(silu(gate)) * up) (causal_lm.py:481-482). */
+int32_t nsg_silu_mul(const void* gate_up, void* out, int64_t num_tokens,
+                     int32_t intermediate, nsg_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Philox4x32-10 uniforms: out[i] = u(seed, stream_id, offset + i) with
  * u = (word >> 8) * 2^-24 and word n of a stream = component n % 4 of
  * philox(ctr = [n/4 lo, n/4 hi, stream_id, 0], key = [seed lo, seed hi]).

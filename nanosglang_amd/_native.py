@@ -45,6 +45,8 @@ SIGNATURES = {
     "nsg_kv_clear_slots": (i32, [vp, i32, vp, vp, i32, i64, i32, i32, i64, vp]),
     "nsg_rope_kv_write": (i32, [vp, i64, vp, vp, vp, i32, vp, i32, i32, i32, i32, vp, vp, vp,
                                 i64, vp, vp]),
+    "nsg_rmsnorm": (i32, [vp, vp, vp, vp, i32, i32, f32, vp]),
+    "nsg_silu_mul": (i32, [vp, vp, i64, i32, vp]),
     "nsg_philox_uniform": (i32, [u64, u32, u64, i64, vp, vp]),
 }
 

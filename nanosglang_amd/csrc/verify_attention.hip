@@ -100,16 +100,14 @@ __global__ __launch_bounds__(RT * 64) void verify_attn_kernel(AttnParams p) {
   const int wi = blockIdx.x;
   if (wi >= p.num_work) return;
   const int h = blockIdx.y;
+  // Work item (host-precomputed, so the first loads need no index chase):
+  // [first query token, query tokens, KV limit of the tile's first row,
+  //  first page-table entry, KV begin, KV end, splits, -]
   const int* wk = p.work + (size_t)wi * NSG_ATTN_WORK_INTS;
-  const int b = wk[0], qb = wk[1], qn = wk[2], kvb = wk[3], kve = wk[4];
+  const int qs = wk[0], qn = wk[1], lim0 = wk[2], pb = wk[3], kvb = wk[4], kve = wk[5];
   const int nsplit = wk[6];
   const int P = 1 << p.log2P;
   const int G = p.G;
-  const int q0 = p.qo_indptr[b];
-  const int ql = p.qo_indptr[b + 1] - q0;
-  const int pb = p.kv_indptr[b];
-  const int npg = p.kv_indptr[b + 1] - pb;
-  const int L = npg > 0 ? (npg - 1) * P + p.kv_last[b] : 0;
   const int nrows = qn * G;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -122,10 +120,10 @@ __global__ __launch_bounds__(RT * 64) void verify_attn_kernel(AttnParams p) {
   const bool row_ok = row < nrows;
   const int tau = row / G;
   const int gam = row - tau * G;
-  const int lim = row_ok ? (p.causal ? L - ql + qb + tau : L - 1) : -1;
+  const int lim = row_ok ? lim0 + (p.causal ? tau : 0) : -1;
   bf16x8 qf[KC];
   {
-    const bf16* qrow = p.q + ((size_t)(q0 + qb + tau) * p.Hq + h * G + gam) * D;
+    const bf16* qrow = p.q + ((size_t)(qs + tau) * p.Hq + h * G + gam) * D;
 #pragma unroll
     for (int c = 0; c < KC; ++c)
       qf[c] = row_ok ? load_bf16x8(qrow + 32 * c + 8 * g4)
@@ -297,7 +295,7 @@ __global__ __launch_bounds__(RT * 64) void verify_attn_kernel(AttnParams p) {
   if (!row_ok) return;
   if (nsplit == 1) {
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    bf16* orow = p.out + ((size_t)(q0 + qb + tau) * p.Hq + h * G + gam) * D + 4 * g4;
+    bf16* orow = p.out + ((size_t)(qs + tau) * p.Hq + h * G + gam) * D + 4 * g4;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       const floatx4 o = oacc[dt];
@@ -318,59 +316,54 @@ __global__ __launch_bounds__(RT * 64) void verify_attn_kernel(AttnParams p) {
 // Merge of the split partials of one (request, query tile) group x KV head.
 // A separate launch: partials written by workgroups on other XCDs become
 // visible at the kernel boundary, so no in-kernel cross-workgroup fence (an
-// L2 write-back + invalidate on gfx950) is needed.
+// L2 write-back + invalidate on gfx950) is needed.  Each thread owns one
+// (row, 8-column) piece and streams the splits with independent loads.
 template <int D, int RT>
 __global__ __launch_bounds__(kThreads) void verify_merge_kernel(AttnParams p, const int* merge,
                                                                int num_merge) {
   constexpr int ROWS = RT * 16;
   constexpr int PSTRIDE = D + 4;
-  constexpr int CPT = D / 16;
+  constexpr int CH = D / 8;  // 8-column pieces per row
   const int mi = blockIdx.x;
   if (mi >= num_merge) return;
   const int h = blockIdx.y;
+  // merge item: [first query token, query tokens, first work item, splits, -...]
   const int* mw = merge + (size_t)mi * NSG_ATTN_WORK_INTS;
-  const int b = mw[0], qb = mw[1], qn = mw[2], wi0 = mw[3], nsplit = mw[4];
+  const int qs = mw[0], qn = mw[1], wi0 = mw[2], nsplit = mw[3];
   const int G = p.G;
-  const int q0 = p.qo_indptr[b];
   const int nrows = qn * G;
-  const int c0 = (threadIdx.x & 15) * CPT;
-  for (int grow = threadIdx.x >> 4; grow < nrows; grow += kThreads / 16) {
-    float M = kMaskVal;
-    for (int s = 0; s < nsplit; ++s) {
-      const float* prow = p.partials + ((size_t)(wi0 + s) * p.Hkv + h) * ROWS * PSTRIDE +
-                          (size_t)grow * PSTRIDE;
-      M = fmaxf(M, prow[D]);
-    }
-    float o[CPT];
+  for (int item = threadIdx.x; item < nrows * CH; item += kThreads) {
+    const int row = item / CH;
+    const int c0 = (item - row * CH) * 8;
+    const float* base = p.partials + ((size_t)wi0 * p.Hkv + h) * ROWS * PSTRIDE +
+                        (size_t)row * PSTRIDE;
+    const size_t sstride = (size_t)p.Hkv * ROWS * PSTRIDE;
+    float M = kMaskVal, lsum = 0.f;
+    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int sp = 0; sp < nsplit; ++sp) {
+      const float* prow = base + sp * sstride;
+      const floatx4 ml = *reinterpret_cast<const floatx4*>(prow + D);  // m, l, pad, pad
+      const floatx4 a = *reinterpret_cast<const floatx4*>(prow + c0);
+      const floatx4 b = *reinterpret_cast<const floatx4*>(prow + c0 + 4);
+      const float Mn = fmaxf(M, ml[0]);
+      const float sc = __builtin_amdgcn_exp2f(M - Mn);
+      const float wt = __builtin_amdgcn_exp2f(ml[0] - Mn);
+      lsum = lsum * sc + wt * ml[1];
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) o[c] = 0.f;
-    float lsum = 0.f;
-    for (int s = 0; s < nsplit; ++s) {
-      const float* prow = p.partials + ((size_t)(wi0 + s) * p.Hkv + h) * ROWS * PSTRIDE +
-                          (size_t)grow * PSTRIDE;
-      const float wt = exp2f(prow[D] - M);
-      lsum += wt * prow[D + 1];
-#pragma unroll
-      for (int c = 0; c < CPT; c += 4) {
-        const floatx4 v = *reinterpret_cast<const floatx4*>(prow + c0 + c);
-        o[c] += wt * v[0];
-        o[c + 1] += wt * v[1];
-        o[c + 2] += wt * v[2];
-        o[c + 3] += wt * v[3];
+      for (int i = 0; i < 4; ++i) {
+        o[i] = o[i] * sc + wt * a[i];
+        o[4 + i] = o[4 + i] * sc + wt * b[i];
       }
+      M = Mn;
     }
-    const int tau = grow / G;
-    const int gam = grow - tau * G;
-    bf16* orow = p.out + ((size_t)(q0 + qb + tau) * p.Hq + h * G + gam) * D + c0;
+    const int tau = row / G;
+    const int gam = row - tau * G;
+    bf16* orow = p.out + ((size_t)(qs + tau) * p.Hq + h * G + gam) * D + c0;
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-    uint32_t pk[CPT / 2];
-#pragma unroll
-    for (int c = 0; c < CPT / 2; ++c) pk[c] = pack_bf16x2(o[2 * c] * inv, o[2 * c + 1] * inv);
-    if constexpr (CPT == 8) {
-      *reinterpret_cast<u32x4*>(orow) = u32x4{pk[0], pk[1], pk[2], pk[3]};
-    } else {
-      *reinterpret_cast<u32x2*>(orow) = u32x2{pk[0], pk[1]};
-    }
+    *reinterpret_cast<u32x4*>(orow) =
+        u32x4{cvt_pk_bf16(o[0] * inv, o[1] * inv), cvt_pk_bf16(o[2] * inv, o[3] * inv),
+              cvt_pk_bf16(o[4] * inv, o[5] * inv), cvt_pk_bf16(o[6] * inv, o[7] * inv)};
   }
 }
 
@@ -453,7 +446,7 @@ extern "C" int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_i
   const int T = std::max(1, std::min(64 / G, max_ql));
   const int RT = (T * G + 15) / 16;
 
-  struct Group { int b, qb, qn, kv_end; };
+  struct Group { int b, qb, qn, kv_end, lim0; };
   std::vector<Group> groups;
   long long total_it = 0;
   for (int b = 0; b < batch; ++b) {
@@ -466,7 +459,7 @@ extern "C" int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_i
     for (int qb = 0; qb < ql; qb += T) {
       const int qn = std::min(T, ql - qb);
       const int kv_end = causal ? L - ql + qb + qn : L;
-      groups.push_back({b, qb, qn, kv_end});
+      groups.push_back({b, qb, qn, kv_end, causal ? L - ql + qb : L - 1});
       total_it += (kv_end + kTokIt - 1) / kTokIt;
     }
   }
@@ -495,26 +488,26 @@ extern "C" int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_i
     const Group& g = groups[gi];
     const int ns = split_counts[gi];
     max_splits = std::max(max_splits, ns);
-    if (ns > 1) {  // merge item: (b, qb, qn, first work item, splits)
+    const int qs = qo_indptr_h[g.b] + g.qb;
+    if (ns > 1) {  // merge item: (first query token, query tokens, first work item, splits)
       int32_t* w = work_h + (size_t)(n_work + m) * NSG_ATTN_WORK_INTS;
-      w[0] = g.b;
-      w[1] = g.qb;
-      w[2] = g.qn;
-      w[3] = n;
-      w[4] = ns;
-      w[5] = w[6] = w[7] = 0;
+      w[0] = qs;
+      w[1] = g.qn;
+      w[2] = n;
+      w[3] = ns;
+      w[4] = w[5] = w[6] = w[7] = 0;
       ++m;
     }
     for (int s = 0; s < ns; ++s) {
       int32_t* w = work_h + (size_t)n * NSG_ATTN_WORK_INTS;
-      w[0] = g.b;
-      w[1] = g.qb;
-      w[2] = g.qn;
-      w[3] = (int)(s * chunk_it * kTokIt);
-      w[4] = (int)std::min<long long>(g.kv_end, (s + 1) * chunk_it * kTokIt);
-      w[5] = s;
+      w[0] = qs;
+      w[1] = g.qn;
+      w[2] = g.lim0;
+      w[3] = kv_indptr_h[g.b];
+      w[4] = (int)(s * chunk_it * kTokIt);
+      w[5] = (int)std::min<long long>(g.kv_end, (s + 1) * chunk_it * kTokIt);
       w[6] = ns;
-      w[7] = (int)gi;
+      w[7] = 0;
       ++n;
     }
   }

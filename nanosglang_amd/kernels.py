@@ -347,6 +347,35 @@ def rope_kv_write(qkv: torch.Tensor, num_qo_heads: int, num_kv_heads: int, head_
     return q_out
 
 
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+            residual: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """RMSNorm of (T, H) bf16 rows; with ``residual`` first residual += x in
+    place and normalise the sum (C ABI: nsg_rmsnorm)."""
+    _require_gpu(x, "x")
+    T, H = x.shape
+    for name, t in (("x", x), ("weight", weight), ("residual", residual)):
+        if t is not None and (t.dtype != torch.bfloat16 or not t.is_contiguous()):
+            raise ValueError(f"{name} must be contiguous bfloat16")
+    if out is None:
+        out = torch.empty_like(x)
+    check(_lib().nsg_rmsnorm(x.data_ptr(), _ptr(residual), weight.data_ptr(), out.data_ptr(),
+                             T, H, float(eps), _stream_ptr(x.device)), "nsg_rmsnorm")
+    return out
+
+
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """(T, 2I) bf16 [gate | up] -> (T, I) silu(gate) * up (C ABI: nsg_silu_mul)."""
+    _require_gpu(gate_up, "gate_up")
+    T, I2 = gate_up.shape
+    if gate_up.dtype != torch.bfloat16 or not gate_up.is_contiguous():
+        raise ValueError("gate_up must be contiguous bfloat16")
+    if out is None:
+        out = torch.empty(T, I2 // 2, dtype=torch.bfloat16, device=gate_up.device)
+    check(_lib().nsg_silu_mul(gate_up.data_ptr(), out.data_ptr(), T, I2 // 2,
+                              _stream_ptr(gate_up.device)), "nsg_silu_mul")
+    return out
+
+
 def philox_uniform(seed: int, stream_id: int, offset: int, n: int, device) -> torch.Tensor:
     """n float32 uniforms of Philox4x32-10 stream ``stream_id`` (see nsg_spec.h)."""
     out = torch.empty(n, dtype=torch.float32, device=device)

@@ -13,7 +13,8 @@ MI355X-side choices:
 * RoPE + KV-slot write is one HIP kernel (``kernels.rope_kv_write``) with
   the reference's bf16 rounding order; attention is the HIP verify-attention
   kernel behind ``BatchPrefillWithPagedKVCacheWrapper``;
-* RMSNorm uses the reference's fp32-variance formula (:142-145);
+* RMSNorm (and residual add + RMSNorm) and the SwiGLU gate are HIP kernels
+  with the reference's fp32-variance arithmetic (:142-154, :482);
 * a draft made of the first ``n`` layers plus the shared embedding, final
   norm and lm_head is ``forward_packed(..., num_layers=n)`` on the same
   weights.
@@ -136,27 +137,22 @@ class CausalLM:
                          c.intermediate_size)
         k_pool, v_pool = kv_cache
         nl = self.num_layers if num_layers is None else num_layers
-        x = F.embedding(input_ids, self.embed)
-        residual = None
+        eps = c.rms_norm_eps
+        residual = F.embedding(input_ids, self.embed)    # owned: updated in place below
+        x = None
         for li in range(nl):
             L = self.layers[li]
-            if residual is None:
-                residual = x
-                h = rms_norm(x, L["ln1"], c.rms_norm_eps)
-            else:
-                residual = residual + x                          # causal_lm.py:505, 531
-                h = rms_norm(residual, L["ln1"], c.rms_norm_eps)
+            # residual += x (causal_lm.py:505, 531), then RMSNorm -- one kernel
+            h = kernels.rmsnorm(residual if x is None else x, L["ln1"], eps,
+                                residual=None if x is None else residual)
             qkv = F.linear(h, L["qkv"], L["qkv_b"])
             q = kernels.rope_kv_write(qkv, Hq, Hkv, D, positions, self.rope_cos, self.rope_sin,
                                       write_indices, k_pool[li], v_pool[li])
             attn = attn_wrapper.run(q, (k_pool[li], v_pool[li]))
             x = F.linear(attn.view(-1, Hq * D), L["o"])
-            residual = residual + x                               # causal_lm.py:153
-            h = rms_norm(residual, L["ln2"], c.rms_norm_eps)
-            gu = F.linear(h, L["gate_up"])
-            x = F.linear(F.silu(gu[:, :I]) * gu[:, I:], L["down"])
-        x = residual + x
+            h = kernels.rmsnorm(x, L["ln2"], eps, residual=residual)   # causal_lm.py:147-154
+            x = F.linear(kernels.silu_mul(F.linear(h, L["gate_up"])), L["down"])
+        h = kernels.rmsnorm(x, self.norm, eps, residual=residual)
         if logit_indices is not None:
-            x = x[logit_indices]
-        x = rms_norm(x, self.norm, c.rms_norm_eps)
-        return F.linear(x, self.lm_head)
+            h = h[logit_indices]
+        return F.linear(h, self.lm_head)

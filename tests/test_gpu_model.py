@@ -130,3 +130,27 @@ def test_spec_engine_greedy_equals_plain_greedy_and_oracle():
         ref = CPUSpeculativeDecoder(draft, cpu, 4).generate(p, m)
         first = next((i for i, (a, b) in enumerate(zip(o, ref)) if a != b), len(o))
         print(f"  prompt {len(p)}: first divergence from CPU oracle at {first}/{m}", flush=True)
+
+
+def test_rmsnorm_and_silu_kernels_match_reference_arithmetic():
+    """Against the reference's bf16 torch expressions (causal_lm.py:142-154,
+    482) evaluated on the GPU: within one bf16 rounding step."""
+    from nanosglang_amd.kernels import rmsnorm, silu_mul
+    from nanosglang_amd.model.causal_lm import rms_norm
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for H in (896, 4096):
+        x = torch.randn(37, H, generator=g, device="cuda").bfloat16()
+        r = torch.randn(37, H, generator=g, device="cuda").bfloat16()
+        w = (1 + 0.1 * torch.randn(H, generator=g, device="cuda")).bfloat16()
+        ref = rms_norm(x, w, 1e-6)
+        got = rmsnorm(x, w, 1e-6)
+        assert ((got.float() - ref.float()).abs() <= 2 ** -7 * ref.float().abs() + 1e-6).all()
+        r2 = r.clone()
+        got = rmsnorm(x, w, 1e-6, residual=r2)
+        assert torch.equal(r2, r + x)                 # bf16 residual add, bit-exact
+        ref = rms_norm(r + x, w, 1e-6)
+        assert ((got.float() - ref.float()).abs() <= 2 ** -7 * ref.float().abs() + 1e-6).all()
+    gu = torch.randn(29, 2 * 4864, generator=g, device="cuda").bfloat16()
+    ref = torch.nn.functional.silu(gu[:, :4864]) * gu[:, 4864:]
+    got = silu_mul(gu)
+    assert ((got.float() - ref.float()).abs() <= 2 ** -6 * ref.float().abs() + 1e-6).all()

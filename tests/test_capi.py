@@ -1,0 +1,98 @@
+"""The C-ABI library loads on a CPU-only host and exports every function
+include/nsg_spec.h declares; its host-only entry points (the attention
+planner, workspace sizing, argument checks) run without a GPU."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+from nanosglang_amd import _native
+from nanosglang_amd._native import NSG_ATTN_WORK_INTS, AttnPlan
+
+HDR = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                   "nsg_spec.h")
+
+
+def _declared():
+    text = open(HDR).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nsg_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported_and_typed(lib):
+    names = _declared()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _native.SIGNATURES, f"{n} has no ctypes signature"
+    assert lib.nsg_abi_version() == _native.ABI_VERSION
+
+
+def _plan(lib, q_lens, kv_lens, Hq=14, Hkv=2, D=64, P=16, causal=1, cus=256):
+    B = len(q_lens)
+    qo = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    npg = [(L + P - 1) // P for L in kv_lens]
+    kvp = np.concatenate([[0], np.cumsum(npg)]).astype(np.int32)
+    last = np.asarray([(L % P) or P for L in kv_lens], np.int32)
+    cap = 100000
+    work = np.zeros(cap * NSG_ATTN_WORK_INTS, np.int32)
+    pl = AttnPlan()
+    rc = lib.nsg_attn_plan(qo.ctypes.data, kvp.ctypes.data, last.ctypes.data, B, Hq, Hkv, D, P,
+                           causal, cus, work.ctypes.data, cap, C.byref(pl))
+    return rc, pl, work.reshape(cap, NSG_ATTN_WORK_INTS), qo, kvp
+
+
+@pytest.mark.parametrize("cus", [1, 256])
+def test_planner_covers_every_query_row_and_kv_token_once(lib, cus):
+    rng = np.random.default_rng(0)
+    q_lens = [5] * 20 + [1, 300, 17]
+    kv_lens = list(rng.integers(100, 641, 20)) + [50, 300, 17]
+    rc, pl, work, qo, kvp = _plan(lib, q_lens, kv_lens, cus=cus)
+    assert rc == 0
+    items = work[:pl.num_work]
+    merges = work[pl.num_work:pl.num_work + pl.num_merge]
+    G = 7
+    T = pl.q_tile_tokens
+    assert pl.row_tiles == (T * G + 15) // 16 and T * G <= 64
+    seen_q = np.zeros(qo[-1], int)
+    for b in range(len(q_lens)):
+        L, ql = kv_lens[b], q_lens[b]
+        for qb in range(0, ql, T):
+            qn = min(T, ql - qb)
+            qs = qo[b] + qb
+            its = items[(items[:, 0] == qs) & (items[:, 1] == qn)]
+            assert len(its) >= 1
+            seen_q[qs:qs + qn] += 1
+            kv_end = L - ql + qb + qn
+            # KV ranges tile [0, kv_end) exactly, splits numbered consistently
+            rngs = sorted((int(r[4]), int(r[5])) for r in its)
+            assert rngs[0][0] == 0 and rngs[-1][1] == kv_end
+            assert all(a[1] == b_[0] for a, b_ in zip(rngs, rngs[1:]))
+            assert all(r[6] == len(its) for r in its)
+            assert all(r[2] == L - ql + qb and r[3] == kvp[b] for r in its)
+            if len(its) > 1:
+                m = merges[(merges[:, 0] == qs) & (merges[:, 1] == qn)]
+                assert len(m) == 1 and m[0, 3] == len(its)
+                first = m[0, 2]
+                assert (items[first:first + len(its), 0] == qs).all()
+    assert (seen_q == 1).all()
+    assert pl.workspace_bytes >= 256 + pl.num_work * 2 * pl.row_tiles * 16 * (64 + 4) * 4
+
+
+def test_planner_rejects_bad_input(lib):
+    assert _plan(lib, [5], [3])[0] == 1                 # L < q_len under the causal rule
+    assert _plan(lib, [5], [30], D=96)[0] == 2          # unsupported head dim
+    assert _plan(lib, [5], [30], Hq=14, Hkv=3)[0] == 1  # Hq % Hkv
+    assert _plan(lib, [5], [30], P=12)[0] == 1          # page size not a power of two
+    assert "page_size" in lib.nsg_last_error().decode()
+
+
+def test_accept_workspace_and_argument_checks(lib):
+    assert lib.nsg_spec_accept_workspace_bytes(64, 4, 151936) > 64 * 9 * 4 * 8
+    assert lib.nsg_spec_accept_workspace_bytes(-1, 4, 10) == -1
+    # k beyond the kernel's limit is an argument error before any GPU work
+    rc = lib.nsg_spec_accept(None, 0, 0, None, 0, 0, 0, None, None, 1, 99, 10, 0.0, None,
+                             None, None, 16, None, None, None, None, 0, None)
+    assert rc == 1 and "k 99" in lib.nsg_last_error().decode()

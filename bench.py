@@ -131,7 +131,7 @@ def bench_acceptance(torch, dev, greedy, sets=3, reps=60, **kw):
     return {"us": t, "bytes": nbytes, "gbs": nbytes / t / 1e3, "sets_rotated": sets}
 
 
-def cpu_baseline(prompts, outs, n_tokens=16):
+def cpu_baseline(prompts, outs, n_tokens=48):
     """The oracle's fp32 PyTorch CPU speculative loop on request 0 of the
     workload (prompt + n_tokens outputs), batch 1, k 4, 4-layer draft."""
     import torch

@@ -43,7 +43,7 @@ constexpr int kMinSplitSteps = 4;     // 32-token steps per KV split, at least
 constexpr int kTokIt = 32;           // KV tokens per wave step
 constexpr float kMaskVal = -1.0e30f; // finite "minus infinity" (no inf - inf)
 constexpr int64_t kHeaderBytes = 256;  // flags word + padding
-constexpr int kTargetWgPerCu = 2;
+constexpr int kTargetWgPerCu = 8;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -78,28 +78,54 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(floatx2{lo, hi}, bf16x2));
 }
 
+// s_waitcnt immediate that waits until at most n vector-memory ops of this
+// wave are outstanding (gfx9 encoding: vmcnt bits [3:0] and [15:14]; expcnt
+// and lgkmcnt left at their maxima, i.e. not waited on).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
+
+// LDS tile swizzles: 16-byte chunk c of token row t is stored at physical
+// chunk c ^ swz(t).  K fragments read one logical chunk of 16 consecutive
+// tokens (needs distinct banks across t); V^T fragments read two adjacent
+// chunks of 4 rows t = 4g + j (needs distinct chunk pairs across g, and a
+// per-lane constant swizzle so that read offsets stay affine).
+template <int D>
+__device__ __forceinline__ int swz_k(int t) {
+  if constexpr (D == 64) return (t >> 1) & 7;  // 128-byte rows: two rows per bank cycle
+  return t & 15;                               // 256-byte rows: one row per bank cycle
+}
+__device__ __forceinline__ int swz_v(int t) { return 2 * ((t >> 2) & 3); }
+
+constexpr float kLazyRescale = 8.f;  // rescale O only when a row max grows by > 2^8
+
+constexpr int kNBuf = 4;            // LDS ring depth (steps in flight: kNBuf - 1)
+constexpr int kMaxItemPages = 1024; // page ids one work item may span
+
 // One workgroup = one work item x one KV head; wave w owns query rows
-// [16w, 16w + 16) of the item's query tile.  The workgroup walks the item's
-// KV range in 32-token steps: all threads load the next step's K and V rows
-// into registers while the waves compute the current step out of LDS, then
-// the registers go to the other LDS buffer (one barrier per step).
+// [16w, 16w + 16) of the item's query tile.  The item's page ids are staged
+// in LDS once.  K and V rows of each 32-token step go straight from HBM to
+// an LDS ring slot with global_load_lds_dwordx4 (no staging registers), kNBuf
+// - 1 steps ahead of the math; a raw s_barrier plus an explicit vmcnt wait
+// per step keeps the ring full (__syncthreads would drain it).
 template <int D, int RT>
 __global__ __launch_bounds__(RT * 64) void verify_attn_kernel(AttnParams p) {
-  constexpr int NT = RT * 64;
   constexpr int KC = D / 32;              // K-dim chunks of QK^T
   constexpr int DT = D / 16;              // d tiles of PV
   constexpr int ROWS = RT * 16;
-  constexpr int KROW = D + 8;             // LDS row stride (bf16): 16-byte aligned, spreads banks
-  constexpr int VCH = D / 8;              // 16-byte chunks per token row
-  constexpr int TILE_CH = kTokIt * VCH;   // chunks per K (or V) tile
-  constexpr int NLD = (2 * TILE_CH + NT - 1) / NT;  // chunks per thread per step
-  constexpr int TILE = kTokIt * KROW;
+  constexpr int CPR = D / 8;              // 16-byte chunks per token row
+  constexpr int TILE = kTokIt * D;        // bf16 per K (or V) tile
+  constexpr int NINST = 2 * TILE / 512;   // 1 KB DMA instructions per step (K + V)
+  constexpr int TPI = 64 / CPR;           // token rows per DMA instruction
+  constexpr int NI = (NINST + RT - 1) / RT;  // DMA instructions per wave per step
   constexpr int PSTRIDE = D + 4;          // partial row: O[D], m, l, 2 pad
-  __shared__ __attribute__((aligned(16))) bf16 lds[2][2][TILE];
+  __shared__ __attribute__((aligned(16))) bf16 ring[kNBuf][2][TILE];
+  __shared__ int s_pages[kMaxItemPages];
 
-  const int wi = blockIdx.x;
+  // blockIdx.x = KV head (fastest), so the Hkv workgroups of one work item
+  // are dispatched together and read the interleaved head slices of the same
+  // NHD token rows close in time (DRAM row locality).
+  const int wi = blockIdx.y;
   if (wi >= p.num_work) return;
-  const int h = blockIdx.y;
+  const int h = blockIdx.x;
   // Work item (host-precomputed, so the first loads need no index chase):
   // [first query token, query tokens, KV limit of the tile's first row,
   //  first page-table entry, KV begin, KV end, splits, -]
@@ -115,7 +141,12 @@ __global__ __launch_bounds__(RT * 64) void verify_attn_kernel(AttnParams p) {
   const int r16 = lane & 15;
   const int g4 = lane >> 4;
 
-  // This lane's query row (B operand of S^T = K Q^T) and causal limit.
+  // ---- stage the item's page ids in LDS ----
+  const int page0 = kvb >> p.log2P;
+  const int npages = kve > kvb ? ((kve - 1) >> p.log2P) - page0 + 1 : 0;
+  for (int i = tid; i < npages; i += RT * 64) s_pages[i] = p.kv_indices[pb + page0 + i];
+
+  // ---- this lane's query row (B operand of S^T = K Q^T) and causal limit ----
   const int row = wave * 16 + r16;
   const bool row_ok = row < nrows;
   const int tau = row / G;
@@ -129,162 +160,158 @@ __global__ __launch_bounds__(RT * 64) void verify_attn_kernel(AttnParams p) {
       qf[c] = row_ok ? load_bf16x8(qrow + 32 * c + 8 * g4)
                      : __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
   }
+  __syncthreads();  // page ids visible; nothing is in flight yet besides Q
 
   floatx4 oacc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) oacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m_run = kMaskVal, l_run = 0.f;
+  float m_run = kMaskVal, l_run = 0.f;  // m_run: exponent base (lazily raised)
 
   const size_t head_off = (size_t)h * D;
   const size_t tok_stride = (size_t)p.Hkv * D;
   const int n_it = (kve - kvb + kTokIt - 1) / kTokIt;
-
-  // Page ids are fetched one step ahead of the K/V rows so that no data load
-  // waits on an index load (vmcnt retires in order).
-  int pg[NLD], pgn[NLD];  // page ids of the step being loaded / of the one after
-  u32x4 pre[NLD];
   bool bad_page = false;
-  // Loads are unconditional: invalid lanes read a valid dummy address and the
-  // value is replaced by zero only where it is consumed (selecting right
-  // after the load would make the compiler wait for it there).
-  auto chunk_ok = [&](int i, int t0) {
-    const int e = tid + i * NT;
-    const int which = e >= TILE_CH;
-    const int t = (e - which * TILE_CH) / VCH;
-    return e < 2 * TILE_CH && t0 + t < kve;
-  };
-  auto fetch_pages = [&](int it) {
+  // Dummy source for lanes past the item's end or with a bad page id: the
+  // item's first token row (real, finite data); its value is masked out.
+  const int pg_first = npages > 0 ? s_pages[0] : 0;
+  const bf16* dummy_k = p.kc + ((size_t)((unsigned)pg_first < (unsigned)p.num_pages ? pg_first : 0) * P +
+                                (kvb & (P - 1))) * tok_stride + head_off;
+  const bf16* dummy_v = p.vc + (dummy_k - p.kc);
+
+  // Per-lane LDS read offsets (bf16 elements inside one K or V tile).
+  //   K fragment c of sub-tile s: token 16 s + r16, logical chunk 4 c + g4.
+  //   V^T fragment dt: rows 4 g4 + j (+16), column dt * 16 + r16.
+  int koff[KC];
+#pragma unroll
+  for (int c = 0; c < KC; ++c) koff[c] = r16 * D + (((4 * c + g4) ^ swz_k<D>(r16)) * 8);
+  int voff[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+    voff[dt] = 4 * g4 * D + (((2 * dt + (r16 >> 3)) ^ (2 * g4)) * 8) + (r16 & 7);
+
+  // Issue this wave's DMA instructions for step `it` into ring slot `slot`.
+  auto issue = [&](int it, int slot) {
     const int t0 = kvb + it * kTokIt;
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      const int e = tid + i * NT;
-      const int which = e >= TILE_CH;
-      const int t = (e - which * TILE_CH) / VCH;
-      const int j = t0 + t;
-      pgn[i] = p.kv_indices[pb + (chunk_ok(i, t0) ? (j >> p.log2P) : 0)];
-    }
-  };
-  unsigned okbits = 0;  // bit i: chunk i of the prefetched step holds real data
-  auto load_step = [&](int it) {
-    const int t0 = kvb + it * kTokIt;
-    okbits = 0;
-#pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      const int e = tid + i * NT;
-      const int which = e >= TILE_CH;
-      const int r = e - which * TILE_CH;
-      const int t = r / VCH;
-      const int ch = r - t * VCH;
-      const int j = t0 + t;
-      const int page = pg[i];
-      const bool in_req = chunk_ok(i, t0);
-      bad_page |= in_req && (unsigned)page >= (unsigned)p.num_pages;
-      const bool ok = in_req && (unsigned)page < (unsigned)p.num_pages;
-      okbits |= (unsigned)ok << i;
-      const size_t off =
-          ok ? ((size_t)page * P + (j & (P - 1))) * tok_stride + head_off + ch * 8 : 0;
-      pre[i] = *reinterpret_cast<const u32x4*>((which ? p.vc : p.kc) + off);
-    }
-  };
-  auto store_step = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      const int e = tid + i * NT;
-      if (e < 2 * TILE_CH) {
-        const int which = e >= TILE_CH;
-        const int r = e - which * TILE_CH;
-        const int t = r / VCH;
-        const int ch = r - t * VCH;
-        *reinterpret_cast<u32x4*>(&lds[buf][which][t * KROW + ch * 8]) =
-            (okbits >> i) & 1u ? pre[i] : u32x4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < NI; ++i) {
+      const int j = (wave + RT * i) % NINST;      // padding repeats a real copy
+      const int which = j / (NINST / 2);
+      const int jj = j - which * (NINST / 2);
+      const int t = jj * TPI + lane / CPR;        // token row inside the step
+      const int pc = lane % CPR;                   // physical chunk written by this lane
+      const int lc = pc ^ (which ? swz_v(t) : swz_k<D>(t));  // logical chunk it carries
+      const int tok = t0 + t;
+      const bf16* src = which ? dummy_v : dummy_k;
+      if (tok < kve) {
+        const int page = s_pages[(tok >> p.log2P) - page0];
+        if ((unsigned)page < (unsigned)p.num_pages) {
+          src = (which ? p.vc : p.kc) + ((size_t)page * P + (tok & (P - 1))) * tok_stride +
+                head_off + lc * 8;
+        } else {
+          bad_page = true;
+        }
       }
+      // void* operands: with typed pointers the host pass silently drops the
+      // kernel stubs of this template
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+                                       static_cast<void*>(&ring[slot][which][jj * TPI * D]), 16, 0, 0);
     }
   };
 
-  auto next_pages = [&]() {
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) pg[i] = pgn[i];
-  };
-  if (n_it > 0) {
-    fetch_pages(0);
-    next_pages();
-    load_step(0);
-    store_step(0);
-    fetch_pages(1);
-  }
-  __syncthreads();
-  for (int it = 0; it < n_it; ++it) {
-    const int buf = it & 1;
-    const int t0 = kvb + it * kTokIt;
-    // Straight-line prefetch: past the last step chunk_ok() is false, so these
-    // read page 0 of the request's table and no real K/V rows.
-    next_pages();
-    fetch_pages(it + 2);                     // index loads first, then the rows,
-    load_step(it + 1);                       // in flight during this step's math
+  for (int it = 0; it < kNBuf - 1; ++it)
+    if (it < n_it) issue(it, it);
 
-    // ---- S^T = K Q^T: lane holds tokens 16s + 4*g4 + i of query row r16 ----
-    const bf16* Kt = lds[buf][0];
-    floatx4 sacc[2];
+  for (int it0 = 0; it0 < n_it; it0 += kNBuf) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < KC; ++c) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&Kt[(16 * s + r16) * KROW + 32 * c + 8 * g4]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[c], acc, 0, 0, 0);
+    for (int slot = 0; slot < kNBuf; ++slot) {  // unrolled: ring slot is a constant
+      const int it = it0 + slot;
+      if (it >= n_it) break;
+      // steps issued after `it` by this wave: min(kNBuf - 2, n_it - 1 - it)
+      const int later = min(kNBuf - 2, n_it - 1 - it);
+      if (later >= 2) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NI));
+      } else if (later == 1) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(NI));
+      } else {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
       }
-      sacc[s] = acc;
-    }
+      // step `it` landed for every wave and slot (it - 1) is free; the empty
+      // asm statements keep the compiler from moving LDS accesses across the
+      // raw barrier (which, unlike __syncthreads, does not drain the ring)
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (it + kNBuf - 1 < n_it) issue(it + kNBuf - 1, (slot + kNBuf - 1) % kNBuf);
 
-    // ---- online softmax (base 2) ----
-    float sv[8];
+      const int t0 = kvb + it * kTokIt;
+      const bf16* Kt = ring[slot][0];
+      const uint16_t* Vt = reinterpret_cast<const uint16_t*>(ring[slot][1]);
+
+      // ---- S^T = K Q^T: lane holds tokens 16s + 4*g4 + i of query row r16 ----
+      floatx4 sacc[2];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
+      for (int s2 = 0; s2 < 2; ++s2) {
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int j = t0 + 16 * s + 4 * g4 + i;
-        sv[4 * s + i] = (j <= lim && j < kve) ? sacc[s][i] * p.scale_log2 : kMaskVal;
+        for (int c = 0; c < KC; ++c) {
+          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&Kt[16 * s2 * D + koff[c]]);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[c], acc, 0, 0, 0);
+        }
+        sacc[s2] = acc;
+      }
+
+      // ---- online softmax (base 2) with lazy rescaling ----
+      float sv[8];
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = t0 + 16 * s2 + 4 * g4 + i;
+          sv[4 * s2 + i] = (j <= lim && j < kve) ? sacc[s2][i] * p.scale_log2 : kMaskVal;
+        }
+      }
+      float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                       fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // Raise the exponent base only when a row max exceeds it by > 2^8, and
+      // skip the O rescale entirely when no row of the wave needs it.
+      const bool grow = mx > m_run + kLazyRescale;
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float mnew = grow ? mx : m_run;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);
+        m_run = mnew;
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+      }
+      float pv[8];
+      float ps = 0.f;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        pv[x] = __builtin_amdgcn_exp2f(sv[x] - m_run);
+        ps += pv[x];
+      }
+      l_run += ps;
+      const bf16x8 pf = __builtin_bit_cast(
+          bf16x8, u32x4{cvt_pk_bf16(pv[0], pv[1]), cvt_pk_bf16(pv[2], pv[3]),
+                        cvt_pk_bf16(pv[4], pv[5]), cvt_pk_bf16(pv[6], pv[7])});
+
+      // ---- O^T += V^T P^T; element e of lane group g4 is token
+      //      4*g4 + e (e < 4) or 16 + 4*g4 + (e - 4), matching pf ----
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const uint16_t* vp = Vt + voff[dt];
+        const u32x4 w = {
+            (uint32_t)vp[0] | ((uint32_t)vp[D] << 16),
+            (uint32_t)vp[2 * D] | ((uint32_t)vp[3 * D] << 16),
+            (uint32_t)vp[16 * D] | ((uint32_t)vp[17 * D] << 16),
+            (uint32_t)vp[18 * D] | ((uint32_t)vp[19 * D] << 16)};
+        oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w), pf,
+                                                           oacc[dt], 0, 0, 0);
       }
     }
-    float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                     fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(m_run, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);
-    m_run = mnew;
-    float pv[8];
-    float ps = 0.f;
-#pragma unroll
-    for (int x = 0; x < 8; ++x) {
-      pv[x] = __builtin_amdgcn_exp2f(sv[x] - mnew);
-      ps += pv[x];
-    }
-    l_run = l_run * alpha + ps;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
-    const bf16x8 pf = __builtin_bit_cast(
-        bf16x8, u32x4{cvt_pk_bf16(pv[0], pv[1]), cvt_pk_bf16(pv[2], pv[3]),
-                      cvt_pk_bf16(pv[4], pv[5]), cvt_pk_bf16(pv[6], pv[7])});
-
-    // ---- O^T += V^T P^T; element e of lane group g4 is token
-    //      4*g4 + e (e < 4) or 16 + 4*g4 + (e - 4), matching pf ----
-    const uint16_t* Vt = reinterpret_cast<const uint16_t*>(lds[buf][1]);
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const int col = dt * 16 + r16;
-      uint32_t w[4];
-#pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2) {
-        const int ta = e2 < 2 ? 4 * g4 + 2 * e2 : 16 + 4 * g4 + 2 * e2 - 4;
-        w[e2] = (uint32_t)Vt[ta * KROW + col] | ((uint32_t)Vt[(ta + 1) * KROW + col] << 16);
-      }
-      const bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
-      oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, oacc[dt], 0, 0, 0);
-    }
-
-    store_step(buf ^ 1);
-    __syncthreads();
   }
 
   if (bad_page) atomicOr(p.flags, 1);
@@ -370,7 +397,7 @@ __global__ __launch_bounds__(kThreads) void verify_merge_kernel(AttnParams p, co
 template <int D, int RT>
 int32_t launch_rt(const nsg_attn_plan_t* plan, const AttnParams& prm, const int* merge,
                   hipStream_t stream) {
-  hipLaunchKernelGGL((verify_attn_kernel<D, RT>), dim3(plan->num_work, plan->num_kv_heads),
+  hipLaunchKernelGGL((verify_attn_kernel<D, RT>), dim3(plan->num_kv_heads, plan->num_work),
                      dim3(RT * 64), 0, stream, prm);
   int32_t rc = launch_status("verify_attn_kernel");
   if (rc || plan->num_merge == 0) return rc;
@@ -466,8 +493,12 @@ extern "C" int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_i
   const long long target_items = std::max(1, num_cus * kTargetWgPerCu / num_kv_heads);
   // a split is at least kMinSplitSteps steps: its partial rows cost about as
   // much traffic as one step of K and V
-  const long long chunk_it =
+  long long chunk_it =
       std::max<long long>(kMinSplitSteps, (total_it + target_items - 1) / target_items);
+  // a work item's page ids must fit the kernel's LDS list (kMaxItemPages)
+  const long long max_chunk_it =
+      std::max<long long>(1, ((long long)(kMaxItemPages - 2) * page_size) / kTokIt);
+  chunk_it = std::min(chunk_it, max_chunk_it);
 
   int n = 0, max_splits = 0, n_merge = 0;
   std::vector<int> split_counts(groups.size());

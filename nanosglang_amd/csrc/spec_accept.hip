@@ -41,7 +41,7 @@ constexpr int kThreads = 256;
 constexpr int kMaxK = 32;
 constexpr int kMaxBatch = 1 << 14;
 constexpr int kMaxChunks = 64;
-constexpr int kTargetWgs = 2048;
+constexpr int kTargetWgs = 4096;
 constexpr int64_t kFlagBytes = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -219,32 +219,62 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
     }
   };
   int v = v0 + tid * 8;
+  // Per 8 logits: greedy -- one max, and the (rare) index search only when the
+  // vector beats the running best; stochastic -- max on the raw logits (c > 0),
+  // then exp2(fma(x, c, -m)) with the bare v_exp_f32 (arguments <= 0).
   auto take8 = [&](const float* x, int vv) {
+    float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
+                     fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
     if constexpr (GREEDY) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) am_merge(bv, bi, x[e], vv + e);
+      if (mx > bv || bi == INT_MAX) {
+        int e = 0;
+        while (e < 7 && !(x[e] == mx)) ++e;   // first index of the max (NaN-free rows)
+        if (mx > bv || bi == INT_MAX) {
+          bv = mx;
+          bi = vv + e;
+        }
+      }
     } else {
-      float mx = x[0] * p.c;
-#pragma unroll
-      for (int e = 1; e < 8; ++e) mx = fmaxf(mx, x[e] * p.c);
+      mx *= p.c;
       if (mx > m) {
-        s = s * exp2f(m - mx);
+        s = s * __builtin_amdgcn_exp2f(m - mx);
         m = mx;
       }
-      const float mm = m == -INFINITY ? 0.f : m;  // all -inf so far: adds 0
+      const float nm = m == -INFINITY ? 0.f : -m;  // all -inf so far: adds 0
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s += exp2f(x[e] * p.c - mm);
+      for (int e = 0; e < 8; ++e) s += __builtin_amdgcn_exp2f(__builtin_fmaf(x[e], p.c, nm));
     }
   };
   if (vec) {
-    constexpr int U = 4;  // independent 16-byte loads in flight per thread
+    constexpr int U = 8;  // independent 16-byte loads in flight per thread
     constexpr int STRIDE = kThreads * 8;
+    constexpr int W = sizeof(T) * 8 / 16;  // 16-byte loads per 8 logits
     for (; v + (U - 1) * STRIDE + 8 <= v1; v += U * STRIDE) {
-      float x[U][8];
+      u32x4 raw[U][W];
 #pragma unroll
-      for (int u = 0; u < U; ++u) Logit<T>::load8(base, roff + v + u * STRIDE, x[u]);
+      for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int u = 0; u < U; ++u) take8(x[u], v + u * STRIDE);
+        for (int w = 0; w < W; ++w)
+          raw[u][w] = *reinterpret_cast<const u32x4*>(
+              reinterpret_cast<const char*>(base) + (roff + v + u * STRIDE) * sizeof(T) + 16 * w);
+      // all U*W loads are issued before any is consumed (the compiler would
+      // otherwise sink each load to its use and serialise them)
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float x[8];
+        if constexpr (sizeof(T) == 2) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            x[2 * i] = __uint_as_float(raw[u][0][i] << 16);
+            x[2 * i + 1] = __uint_as_float(raw[u][0][i] & 0xffff0000u);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) x[i] = __uint_as_float(raw[u][i >> 2][i & 3]);
+        }
+        take8(x, v + u * STRIDE);
+      }
     }
     for (; v + 8 <= v1; v += STRIDE) {
       float x[8];
@@ -325,67 +355,88 @@ struct Decision {
   float Mt, iZt, Md, iZd;
 };
 
-// Stochastic decision of request b, computed by one wave (lane 0 returns it;
-// other lanes return garbage).  With `write`, lane 0 also writes the
-// accepted prefix, num_emitted and the rollback slots.
+// Stochastic decision of request b, computed by one wave, returned to every
+// lane.  Lane i (i <= k) reduces the chunk stats of target row i, lane i < k
+// also those of draft row i and runs ratio test i; a ballot finds the first
+// rejection.  Three dependent load rounds in all (stats, draft ids, logits).
+// With `write`, the wave also writes the accepted prefix, num_emitted, the
+// rollback slots and the decision record read by select_kernel.
 template <typename T>
 __device__ Decision decide(const AccParams& p, int b, bool write) {
-  __shared__ float sM[2 * kMaxK + 1], sZ[2 * kMaxK + 1];
   const int lane = threadIdx.x & 63;
   const int k = p.k;
-  for (int i = 0; i < 2 * k + 1; ++i) {
-    const int r = i <= k ? b * (k + 1) + i : p.B * (k + 1) + b * k + (i - k - 1);
-    float m = -INFINITY, s = 0.f;
-    for (int c = lane; c < p.nch; c += 64) {
-      const float2 st = p.stats[(int64_t)r * p.nch + c];
-      ms_merge(m, s, st.x, st.y);
-    }
-    wave_ms(m, s);
-    if (lane == 0) {
-      sM[i] = m;
-      sZ[i] = s;
+  float mt = -INFINITY, zt = 0.f, md = -INFINITY, zd = 0.f;
+  if (lane <= k) {
+    const float2* st = p.stats + (int64_t)(b * (k + 1) + lane) * p.nch;
+#pragma unroll 8
+    for (int c = 0; c < p.nch; ++c) {
+      const float2 v = st[c];
+      ms_merge(mt, zt, v.x, v.y);
     }
   }
-  Decision d = {k, 1, 0.f, 0.f, 0.f, 0.f};
-  if (lane != 0) return d;
-  int64_t* em = p.emitted + (int64_t)b * (k + 1);
-  int j = k;
-  for (int i = 0; i < k; ++i) {
-    const int64_t x = p.dtok[(int64_t)b * k + i];
-    bool acc;
+  if (lane < k) {
+    const float2* st = p.stats + (int64_t)(p.B * (k + 1) + b * k + lane) * p.nch;
+#pragma unroll 8
+    for (int c = 0; c < p.nch; ++c) {
+      const float2 v = st[c];
+      ms_merge(md, zd, v.x, v.y);
+    }
+  }
+  bool reject = false;
+  int64_t x = 0;
+  if (lane < k) {
+    x = p.dtok[(int64_t)b * k + lane];
     if (x < 0 || x >= p.V) {
       if (write) atomicOr(p.flags, 4);
-      acc = false;
+      reject = true;
     } else {
-      const float lt = Logit<T>::at(p.tl, trow(p, b, i) + x) * p.c;
-      const float ld = Logit<T>::at(p.dl, drow(p, b, i) + x) * p.c;
-      const float pt = exp2f(lt - sM[i]) / sZ[i];
-      const float pd = exp2f(ld - sM[k + 1 + i]) / sZ[k + 1 + i];
-      acc = pd > 0.f ? (p.u[(int64_t)b * (k + 1) + i] < fminf(1.f, pt / pd)) : true;
+      const float lt = Logit<T>::at(p.tl, trow(p, b, lane) + x) * p.c;
+      const float ld = Logit<T>::at(p.dl, drow(p, b, lane) + x) * p.c;
+      const float pt = exp2f(lt - mt) / zt;
+      const float pd = exp2f(ld - md) / zd;
+      reject = pd > 0.f && !(p.u[(int64_t)b * (k + 1) + lane] < fminf(1.f, pt / pd));
     }
-    if (!acc) {
-      j = i;
-      break;
-    }
-    if (write) em[i] = x;
   }
+  const uint64_t rej = __builtin_amdgcn_ballot_w64(reject);
+  const int j = rej ? min(k, (int)__builtin_ctzll(rej)) : k;
+  Decision d;
   d.j = j;
   d.mode = j < k ? 0 : 1;
-  d.Mt = sM[j];
-  d.iZt = 1.f / sZ[j];
-  d.Md = j < k ? sM[k + 1 + j] : 0.f;
-  d.iZd = j < k ? 1.f / sZ[k + 1 + j] : 0.f;
+  d.Mt = __shfl(mt, j, 64);
+  d.iZt = 1.f / __shfl(zt, j, 64);
+  d.Md = j < k ? __shfl(md, j, 64) : 0.f;
+  d.iZd = j < k ? 1.f / __shfl(zd, j, 64) : 0.f;
   if (write) {
-    for (int i = j; i <= k; ++i) em[i] = -1;
-    p.n_out[b] = j + 1;
-    write_rollback(p, b, j + 1);
-    float* dd = p.dec + (int64_t)b * 8;
-    dd[0] = __int_as_float(d.j);
-    dd[1] = __int_as_float(d.mode);
-    dd[2] = d.Mt;
-    dd[3] = d.iZt;
-    dd[4] = d.Md;
-    dd[5] = d.iZd;
+    int64_t* em = p.emitted + (int64_t)b * (k + 1);
+    if (lane < j) em[lane] = x;
+    else if (lane <= k) em[lane] = -1;
+    const int n = j + 1;
+    if (lane == 0) p.n_out[b] = n;
+    if (p.rollback && lane < k) {
+      // flat slot of rejected verify position start + n + lane (if <= start + k)
+      int64_t slot = -1;
+      const int pos = p.start_pos[b] + n + lane;
+      if (n + lane <= k) {
+        const int pb = p.kv_indptr[b];
+        const int np = p.kv_indptr[b + 1] - pb;
+        const int pg = pos >> p.log2P;
+        if (pos >= 0 && pg < np) {
+          slot = ((int64_t)p.kv_indices[pb + pg] << p.log2P) + (pos & ((1 << p.log2P) - 1));
+        } else {
+          atomicOr(p.flags, 2);
+        }
+      }
+      p.rollback[(int64_t)b * k + lane] = slot;
+    }
+    if (lane == 0) {
+      float* dd = p.dec + (int64_t)b * 8;
+      dd[0] = __int_as_float(d.j);
+      dd[1] = __int_as_float(d.mode);
+      dd[2] = d.Mt;
+      dd[3] = d.iZt;
+      dd[4] = d.Md;
+      dd[5] = d.iZd;
+    }
   }
   return d;
 }
@@ -394,9 +445,9 @@ __device__ Decision decide(const AccParams& p, int b, bool write) {
 template <typename T>
 __device__ __forceinline__ float weight(const AccParams& p, int64_t to, int64_t dof, int mode,
                                         float Mt, float iZt, float Md, float iZd, int v) {
-  const float pt = exp2f(Logit<T>::at(p.tl, to + v) * p.c - Mt) * iZt;
+  const float pt = __builtin_amdgcn_exp2f(__builtin_fmaf(Logit<T>::at(p.tl, to + v), p.c, -Mt)) * iZt;
   if (mode != 0) return pt;
-  const float pd = exp2f(Logit<T>::at(p.dl, dof + v) * p.c - Md) * iZd;
+  const float pd = __builtin_amdgcn_exp2f(__builtin_fmaf(Logit<T>::at(p.dl, dof + v), p.c, -Md)) * iZd;
   return fmaxf(0.f, pt - pd);
 }
 
@@ -416,20 +467,27 @@ __device__ float block_incl_scan(float x, float* sh) {
   return pre + x;
 }
 
-// Chunk sums of the decided weights; chunk 0 also publishes the decision.
+// One wave per request: the decision, the accepted prefix, counts and slots.
+template <typename T>
+__global__ __launch_bounds__(64) void decide_kernel(AccParams p) {
+  decide<T>(p, blockIdx.x, true);
+}
+
+// Chunk sums of the decided weights (residual of row j, or target row j).
 template <typename T>
 __global__ __launch_bounds__(kThreads) void sum_kernel(AccParams p) {
   __shared__ float sh[kThreads / 64];
-  __shared__ Decision s_dec;
   const int b = blockIdx.y;
   const int chunk = blockIdx.x;
   const int tid = threadIdx.x;
-  if (tid < 64) {
-    const Decision d = decide<T>(p, b, chunk == 0);
-    if (tid == 0) s_dec = d;
-  }
-  __syncthreads();
-  const Decision d = s_dec;
+  const float* dd = p.dec + (int64_t)b * 8;
+  Decision d;
+  d.j = __float_as_int(dd[0]);
+  d.mode = __float_as_int(dd[1]);
+  d.Mt = dd[2];
+  d.iZt = dd[3];
+  d.Md = dd[4];
+  d.iZd = dd[5];
   const int64_t to = trow(p, b, d.j);
   const int64_t dof = d.mode == 0 ? drow(p, b, d.j) : 0;
   const int v0 = chunk * p.cs2;
@@ -443,8 +501,10 @@ __global__ __launch_bounds__(kThreads) void sum_kernel(AccParams p) {
       if (d.mode == 0) Logit<T>::load8(p.dl, dof + v, xd);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float pt = exp2f(xt[e] * p.c - d.Mt) * d.iZt;
-        acc += d.mode == 0 ? fmaxf(0.f, pt - exp2f(xd[e] * p.c - d.Md) * d.iZd) : pt;
+        const float pt = __builtin_amdgcn_exp2f(__builtin_fmaf(xt[e], p.c, -d.Mt)) * d.iZt;
+        acc += d.mode == 0
+                   ? fmaxf(0.f, pt - __builtin_amdgcn_exp2f(__builtin_fmaf(xd[e], p.c, -d.Md)) * d.iZd)
+                   : pt;
       }
     }
   }
@@ -461,13 +521,44 @@ __global__ __launch_bounds__(kThreads) void sum_kernel(AccParams p) {
   }
 }
 
-// One workgroup per request: chunk by a sequential prefix, token by a block
-// scan over contiguous runs of that chunk.
+// One workgroup per request: the chunk by a wave scan over the chunk sums,
+// the token by a block scan over 8-element runs (one 16-byte vector per
+// thread; chunks are at most 8 * kSelThreads elements).
+constexpr int kSelThreads = 1024;
+
 template <typename T>
-__global__ __launch_bounds__(kThreads) void select_kernel(AccParams p) {
-  __shared__ float sh[kThreads / 64];
-  __shared__ int s_tok, s_chunk, s_full;
-  __shared__ float s_rem;
+__device__ __forceinline__ float run_weights(const AccParams& p, int64_t to, int64_t dof, int mode,
+                                             float Mt, float iZt, float Md, float iZd, int v0,
+                                             int v1, bool vec, float* w) {
+  float xt[8], xd[8];
+  if (vec && v0 + 8 <= v1) {
+    Logit<T>::load8(p.tl, to + v0, xt);
+    if (mode == 0) Logit<T>::load8(p.dl, dof + v0, xd);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      xt[e] = v0 + e < v1 ? Logit<T>::at(p.tl, to + v0 + e) : -INFINITY;
+      xd[e] = (mode == 0 && v0 + e < v1) ? Logit<T>::at(p.dl, dof + v0 + e) : -INFINITY;
+    }
+  }
+  float run = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float pt = __builtin_amdgcn_exp2f(__builtin_fmaf(xt[e], p.c, -Mt)) * iZt;
+    w[e] = v0 + e < v1
+               ? (mode == 0 ? fmaxf(0.f, pt - __builtin_amdgcn_exp2f(__builtin_fmaf(xd[e], p.c, -Md)) * iZd)
+                            : pt)
+               : 0.f;
+    run += w[e];
+  }
+  return run;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kSelThreads) void select_kernel(AccParams p) {
+  __shared__ float sh[kSelThreads / 64];
+  __shared__ int s_tok, s_chunk;
+  __shared__ float s_rem, s_tot;
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const float* dd = p.dec + (int64_t)b * 8;
@@ -477,38 +568,41 @@ __global__ __launch_bounds__(kThreads) void select_kernel(AccParams p) {
   const int64_t to = trow(p, b, j);
   const int64_t dof = mode == 0 ? drow(p, b, j) : 0;
   const float u = p.u[(int64_t)b * (p.k + 1) + p.k];
-  if (tid == 0) {
-    const float* ps = p.psum + (int64_t)b * p.nch2;
-    float tot = 0.f;
-    for (int c = 0; c < p.nch2; ++c) tot += ps[c];
-    s_full = 0;
-    if (tot > 0.f) {
-      const float target = u * tot;
-      float pre = 0.f;
-      int cs = -1, lastnz = -1;
-      for (int c = 0; c < p.nch2; ++c) {
-        if (ps[c] > 0.f) lastnz = c;
-        if (cs < 0 && pre + ps[c] > target) {
-          cs = c;
-          s_rem = target - pre;
-        }
-        pre += ps[c];
-      }
-      if (cs < 0) {
-        cs = lastnz;
-        s_rem = INFINITY;  // take the last positive weight of that chunk
-      }
-      s_chunk = cs;
-    } else {
-      // residual summed to zero: sample the target row itself over the whole
-      // vocabulary (mirrors speculative.py:163-169)
-      s_full = 1;
+  if (tid < 64) {
+    // chunk sums -> inclusive wave scan (nch2 <= 64), fixed order
+    const float v = tid < p.nch2 ? p.psum[(int64_t)b * p.nch2 + tid] : 0.f;
+    float incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const float y = __shfl_up(incl, o, 64);
+      if (tid >= o) incl += y;
     }
-    s_tok = -1;
+    const float tot = __shfl(incl, 63, 64);
+    const float target = u * tot;
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(tid < p.nch2 && incl > target);
+    const uint64_t pos = __builtin_amdgcn_ballot_w64(tid < p.nch2 && v > 0.f);
+    // (all 64 lanes take part in the shuffles; lane 0 publishes)
+    const int cs = hit ? (int)__builtin_ctzll(hit) : 0;
+    const float at_incl = __shfl(incl, cs, 64);
+    const float at_v = __shfl(v, cs, 64);
+    if (tid == 0) {
+      s_tot = tot;
+      s_tok = -1;
+      if (hit) {
+        s_chunk = cs;
+        s_rem = target - (at_incl - at_v);
+      } else {
+        s_chunk = pos ? 63 - (int)__builtin_clzll(pos) : 0;
+        s_rem = INFINITY;  // rounding left no crossing: last positive weight
+      }
+    }
   }
   __syncthreads();
   int a, e;
-  if (s_full) {
+  const bool full = !(s_tot > 0.f);
+  if (full) {
+    // residual summed to zero: sample the target row itself over the whole
+    // vocabulary (mirrors speculative.py:163-169), in kSelThreads * 8 slices
     mode = 1;
     a = 0;
     e = p.V;
@@ -516,34 +610,58 @@ __global__ __launch_bounds__(kThreads) void select_kernel(AccParams p) {
     a = s_chunk * p.cs2;
     e = min(p.V, a + p.cs2);
   }
-  const int R = (e - a + kThreads - 1) / kThreads;
-  const int ra = min(e, a + tid * R), rb = min(e, ra + R);
-  float run = 0.f;
-  for (int v = ra; v < rb; ++v) run += weight<T>(p, to, dof, mode, Mt, iZt, Md, iZd, v);
-  const float incl = block_incl_scan(run, sh);
-  const float excl = incl - run;
-  if (s_full && tid == kThreads - 1) s_rem = u * incl;
-  __syncthreads();
-  const float rem = s_rem;
-  if (run > 0.f && incl > rem && !(excl > rem)) {
-    float cum = 0.f;  // same order as `run`, so excl + cum reaches incl
-    for (int v = ra; v < rb; ++v) {
-      cum += weight<T>(p, to, dof, mode, Mt, iZt, Md, iZd, v);
-      if (excl + cum > rem) {
-        atomicMax(&s_tok, v);
-        break;
+  const bool vec = ((to | dof) % Logit<T>::kAlign) == 0;
+  float base = 0.f;        // prefix of earlier slices (full-row fallback only)
+  float target_full = 0.f;
+  if (full) {
+    float tot = 0.f;
+    for (int v0 = a + tid * 8; v0 < e; v0 += kSelThreads * 8) {
+      float w[8];
+      tot += run_weights<T>(p, to, dof, mode, Mt, iZt, Md, iZd, v0, e, vec, w);
+    }
+    tot = wave_sum(tot);
+    if ((tid & 63) == 0) sh[tid >> 6] = tot;
+    __syncthreads();
+    float t2 = 0.f;
+    for (int w = 0; w < kSelThreads / 64; ++w) t2 += sh[w];
+    __syncthreads();
+    target_full = u * t2;
+  }
+  for (int s0 = a; s0 < e; s0 += kSelThreads * 8) {
+    const int v0 = s0 + tid * 8;
+    float w[8];
+    const float run = v0 < e ? run_weights<T>(p, to, dof, mode, Mt, iZt, Md, iZd, v0, e, vec, w)
+                             : 0.f;
+    const float incl = block_incl_scan(run, sh) + base;
+    const float excl = incl - run;
+    const float rem = full ? target_full : s_rem;
+    if (v0 < e && run > 0.f && incl > rem && !(excl > rem)) {
+      float cum = 0.f;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        cum += w[q];
+        if (w[q] > 0.f && excl + cum > rem) {
+          atomicMax(&s_tok, v0 + q);
+          break;
+        }
       }
     }
+    // carry the slice total into the next slice
+    if (tid == kSelThreads - 1) sh[0] = incl;
+    __syncthreads();
+    base = sh[0];
+    __syncthreads();
+    if (s_tok >= 0) break;
   }
-  __syncthreads();
   if (s_tok < 0) {
     // rounding left no crossing: last positive weight in the range
     int last = -1;
-    for (int v = rb - 1; v >= ra; --v) {
-      if (weight<T>(p, to, dof, mode, Mt, iZt, Md, iZd, v) > 0.f) {
-        last = v;
-        break;
-      }
+    for (int v0 = a + tid * 8; v0 < e; v0 += kSelThreads * 8) {
+      float w[8];
+      run_weights<T>(p, to, dof, mode, Mt, iZt, Md, iZd, v0, e, vec, w);
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (w[q] > 0.f) last = max(last, v0 + q);
     }
     atomicMax(&s_tok, last);
     __syncthreads();
@@ -564,6 +682,7 @@ Layout layout(int B, int k, int V, bool greedy) {
   L.cs = ((V + L.nch - 1) / L.nch + 7) / 8 * 8;
   L.nch = (V + L.cs - 1) / L.cs;
   L.nch2 = std::max(1, std::min(max_ch, (kTargetWgs + B - 1) / std::max(1, B)));
+  L.nch2 = std::min(kMaxChunks, std::max(L.nch2, (V + 8 * kSelThreads - 1) / (8 * kSelThreads)));
   L.cs2 = ((V + L.nch2 - 1) / L.nch2 + 7) / 8 * 8;
   L.nch2 = (V + L.cs2 - 1) / L.cs2;
   auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
@@ -588,10 +707,13 @@ int32_t launch_accept(const AccParams& p, int rows, hipStream_t s) {
   hipLaunchKernelGGL((stats_kernel<T, false>), g1, dim3(kThreads), 0, s, p);
   int32_t rc = launch_status("stats_kernel");
   if (rc) return rc;
+  hipLaunchKernelGGL((decide_kernel<T>), dim3(p.B), dim3(64), 0, s, p);
+  rc = launch_status("decide_kernel");
+  if (rc) return rc;
   hipLaunchKernelGGL((sum_kernel<T>), dim3(p.nch2, p.B), dim3(kThreads), 0, s, p);
   rc = launch_status("sum_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL((select_kernel<T>), dim3(p.B), dim3(kThreads), 0, s, p);
+  hipLaunchKernelGGL((select_kernel<T>), dim3(p.B), dim3(kSelThreads), 0, s, p);
   return launch_status("select_kernel");
 }
 

@@ -181,7 +181,11 @@ def main():
         f"output tokens {sum(outs)}")
     model = CausalLM(ModelConfig(), device=dev, seed=0)
     engine = SpecEngine(model, draft_layers=4, num_speculative=4, num_blocks=8000,
-                        block_size=16, temperature=0.0)
+                        block_size=16, temperature=0.0, max_batch=len(prompts))
+    t_cap = time.perf_counter()
+    sizes = engine.capture()        # engine start-up, as the reference captures at start()
+    log(f"captured spec-step graphs for batch sizes {sizes} in "
+        f"{time.perf_counter() - t_cap:.1f} s")
     for w in range(args.warmup):
         engine.generate(prompts, outs)
         log(f"warmup {w}: {engine.stats}")

@@ -42,7 +42,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 2
+#define NSG_ABI_VERSION 3
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -81,6 +81,28 @@ int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
                       int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                       int32_t page_size, int32_t causal, int32_t num_cus,
                       int32_t* work_h, int32_t work_capacity, nsg_attn_plan_t* plan);
+
+/* Graph-capturable planning: the counterpart of the FlashInfer wrapper built
+ * with use_cuda_graph=True and fixed-address buffers (engine.py:110-133,
+ * planned before each replay at engine.py:396-410).
+ *
+ * nsg_attn_fixed_capacity gives the work-list size that every plan of at most
+ * `batch` requests with at most `max_q_len` query tokens each fits.
+ * nsg_attn_plan_fixed is nsg_attn_plan with that size fixed: the work list is
+ * always max_work work items followed by max_merge merge items (unused ones
+ * are empty and cost one early-exiting workgroup each), and the tile shape
+ * follows max_q_len, so nsg_attn_run launches the same grid with the same
+ * arguments for every such plan.  A plan that does not fit returns
+ * NSG_ERR_WORKSPACE. */
+int32_t nsg_attn_fixed_capacity(int32_t batch, int32_t max_q_len, int32_t num_qo_heads,
+                                int32_t num_kv_heads, int32_t num_cus, int32_t* max_work,
+                                int32_t* max_merge);
+int32_t nsg_attn_plan_fixed(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
+                            const int32_t* kv_last_page_len_h, int32_t batch,
+                            int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                            int32_t page_size, int32_t causal, int32_t num_cus,
+                            int32_t max_q_len, int32_t max_work, int32_t max_merge,
+                            int32_t* work_h, int32_t work_capacity, nsg_attn_plan_t* plan);
 
 /* Bytes of device workspace nsg_attn_run needs for this plan (split partials
  * and an error-flag word, which should start at zero). */

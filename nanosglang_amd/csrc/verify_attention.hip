@@ -132,6 +132,7 @@ __global__ __launch_bounds__(RT * 64) void verify_attn_kernel(AttnParams p) {
   const int* wk = p.work + (size_t)wi * NSG_ATTN_WORK_INTS;
   const int qs = wk[0], qn = wk[1], lim0 = wk[2], pb = wk[3], kvb = wk[4], kve = wk[5];
   const int nsplit = wk[6];
+  if (qn == 0) return;  // padding item of a fixed-size (graph-captured) work list
   const int P = 1 << p.log2P;
   const int G = p.G;
   const int nrows = qn * G;
@@ -357,6 +358,7 @@ __global__ __launch_bounds__(kThreads) void verify_merge_kernel(AttnParams p, co
   // merge item: [first query token, query tokens, first work item, splits, -...]
   const int* mw = merge + (size_t)mi * NSG_ATTN_WORK_INTS;
   const int qs = mw[0], qn = mw[1], wi0 = mw[2], nsplit = mw[3];
+  if (nsplit < 2) return;  // padding item of a fixed-size (graph-captured) work list
   const int G = p.G;
   const int nrows = qn * G;
   for (int item = threadIdx.x; item < nrows * CH; item += kThreads) {
@@ -435,11 +437,35 @@ extern "C" int64_t nsg_attn_workspace_bytes(const nsg_attn_plan_t* plan) {
   return plan->workspace_bytes;
 }
 
-extern "C" int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
-                                 const int32_t* kv_last_page_len_h, int32_t batch,
-                                 int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
-                                 int32_t page_size, int32_t causal, int32_t num_cus,
-                                 int32_t* work_h, int32_t work_capacity, nsg_attn_plan_t* plan) {
+namespace nsg {
+namespace {
+
+// Query-tile shape of a plan: T query tokens per tile (T * G <= 64 rows).
+int q_tile_tokens(int G, int max_ql) { return std::max(1, std::min(64 / G, max_ql)); }
+
+// Work-list capacity that any plan with at most `batch` requests of at most
+// `max_ql` query tokens fits: the split size is chosen so that the KV steps
+// make at most target_items items, plus at most one rounding item per
+// (request, query tile) group; every group needs at most one merge item.
+void fixed_capacity(int batch, int max_ql, int G, int num_kv_heads, int num_cus,
+                    int* max_work, int* max_merge) {
+  const int T = q_tile_tokens(G, max_ql);
+  const int groups = batch * ((std::max(1, max_ql) + T - 1) / T);
+  const int target_items = std::max(1, num_cus * kTargetWgPerCu / num_kv_heads);
+  *max_work = target_items + groups;
+  *max_merge = groups;
+}
+
+// Shared planner.  fixed_work < 0: the work list holds exactly the items the
+// plan needs.  fixed_work >= 0: it holds exactly fixed_work work items (the
+// tail padded with empty items, query tokens 0) followed by fixed_merge merge
+// items (padded with split count 0), so that nsg_attn_run launches the same
+// grid for every plan and a captured graph replays after re-planning.
+int32_t plan_impl(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
+                  const int32_t* kv_last_page_len_h, int32_t batch, int32_t num_qo_heads,
+                  int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int32_t causal,
+                  int32_t num_cus, int32_t* work_h, int32_t work_capacity, int32_t fixed_work,
+                  int32_t fixed_merge, int32_t fixed_q_len, nsg_attn_plan_t* plan) {
   NSG_CHECK_ARG(plan && qo_indptr_h && kv_indptr_h && kv_last_page_len_h, "null argument");
   NSG_CHECK_ARG(batch >= 0, "batch %d < 0", batch);
   NSG_CHECK_ARG(num_kv_heads > 0 && num_qo_heads > 0 && num_qo_heads % num_kv_heads == 0,
@@ -470,7 +496,14 @@ extern "C" int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_i
     }
     max_ql = std::max(max_ql, ql);
   }
-  const int T = std::max(1, std::min(64 / G, max_ql));
+  if (fixed_work >= 0) {
+    // the tile shape (a kernel template parameter) must not change between
+    // plans of one captured graph: it follows the graph's query length
+    NSG_CHECK_ARG(max_ql <= fixed_q_len, "a request has %d query tokens, the fixed plan "
+                  "allows %d", max_ql, fixed_q_len);
+    max_ql = fixed_q_len;
+  }
+  const int T = q_tile_tokens(G, max_ql);
   const int RT = (T * G + 15) / 16;
 
   struct Group { int b, qb, qn, kv_end, lim0; };
@@ -508,11 +541,18 @@ extern "C" int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_i
     n += split_counts[gi];
     n_merge += split_counts[gi] > 1;
   }
-  if (!work_h || n + n_merge > work_capacity) {
-    set_error("work list needs %d items, buffer holds %d", n + n_merge, work_capacity);
+  if (fixed_work >= 0 && (n > fixed_work || n_merge > fixed_merge)) {
+    set_error("plan needs %d work and %d merge items, the fixed list holds %d and %d", n,
+              n_merge, fixed_work, fixed_merge);
     return NSG_ERR_WORKSPACE;
   }
-  const int n_work = n;
+  const int n_work = fixed_work >= 0 ? fixed_work : n;
+  const int n_merge_slots = fixed_work >= 0 ? fixed_merge : n_merge;
+  if (!work_h || n_work + n_merge_slots > work_capacity) {
+    set_error("work list needs %d items, buffer holds %d", n_work + n_merge_slots,
+              work_capacity);
+    return NSG_ERR_WORKSPACE;
+  }
   n = 0;
   int m = 0;
   for (size_t gi = 0; gi < groups.size(); ++gi) {
@@ -542,8 +582,13 @@ extern "C" int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_i
       ++n;
     }
   }
-  plan->num_work = n;
-  plan->num_merge = m;
+  // padding: empty work items (query tokens 0), merge items with 0 splits
+  std::fill(work_h + (size_t)n * NSG_ATTN_WORK_INTS,
+            work_h + (size_t)n_work * NSG_ATTN_WORK_INTS, 0);
+  std::fill(work_h + (size_t)(n_work + m) * NSG_ATTN_WORK_INTS,
+            work_h + (size_t)(n_work + n_merge_slots) * NSG_ATTN_WORK_INTS, 0);
+  plan->num_work = n_work;
+  plan->num_merge = n_merge_slots;
   plan->num_groups = (int)groups.size();
   plan->row_tiles = RT;
   plan->q_tile_tokens = T;
@@ -552,9 +597,53 @@ extern "C" int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_i
   plan->num_qo_heads = num_qo_heads;
   plan->num_kv_heads = num_kv_heads;
   plan->workspace_bytes =
-      kHeaderBytes + (int64_t)n * num_kv_heads * RT * 16 * (head_dim + 4) * 4;
+      kHeaderBytes + (int64_t)n_work * num_kv_heads * RT * 16 * (head_dim + 4) * 4;
   clear_error();
   return NSG_OK;
+}
+
+}  // namespace
+}  // namespace nsg
+
+extern "C" int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
+                                 const int32_t* kv_last_page_len_h, int32_t batch,
+                                 int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                                 int32_t page_size, int32_t causal, int32_t num_cus,
+                                 int32_t* work_h, int32_t work_capacity, nsg_attn_plan_t* plan) {
+  return plan_impl(qo_indptr_h, kv_indptr_h, kv_last_page_len_h, batch, num_qo_heads,
+                   num_kv_heads, head_dim, page_size, causal, num_cus, work_h, work_capacity,
+                   -1, 0, 0, plan);
+}
+
+extern "C" int32_t nsg_attn_fixed_capacity(int32_t batch, int32_t max_q_len,
+                                           int32_t num_qo_heads, int32_t num_kv_heads,
+                                           int32_t num_cus, int32_t* max_work,
+                                           int32_t* max_merge) {
+  NSG_CHECK_ARG(max_work && max_merge, "null argument");
+  NSG_CHECK_ARG(batch >= 1 && max_q_len >= 1, "batch %d and max_q_len %d must be >= 1", batch,
+                max_q_len);
+  NSG_CHECK_ARG(num_kv_heads > 0 && num_qo_heads > 0 && num_qo_heads % num_kv_heads == 0 &&
+                    num_qo_heads / num_kv_heads <= 64,
+                "num_qo_heads %d / num_kv_heads %d", num_qo_heads, num_kv_heads);
+  if (num_cus <= 0) num_cus = 256;
+  fixed_capacity(batch, max_q_len, num_qo_heads / num_kv_heads, num_kv_heads, num_cus, max_work,
+                 max_merge);
+  clear_error();
+  return NSG_OK;
+}
+
+extern "C" int32_t nsg_attn_plan_fixed(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
+                                       const int32_t* kv_last_page_len_h, int32_t batch,
+                                       int32_t num_qo_heads, int32_t num_kv_heads,
+                                       int32_t head_dim, int32_t page_size, int32_t causal,
+                                       int32_t num_cus, int32_t max_q_len, int32_t max_work,
+                                       int32_t max_merge, int32_t* work_h,
+                                       int32_t work_capacity, nsg_attn_plan_t* plan) {
+  NSG_CHECK_ARG(max_q_len >= 1 && max_work >= 1 && max_merge >= 0,
+                "max_q_len %d, max_work %d, max_merge %d", max_q_len, max_work, max_merge);
+  return plan_impl(qo_indptr_h, kv_indptr_h, kv_last_page_len_h, batch, num_qo_heads,
+                   num_kv_heads, head_dim, page_size, causal, num_cus, work_h, work_capacity,
+                   max_work, max_merge, max_q_len, plan);
 }
 
 extern "C" int32_t nsg_attn_run(const nsg_attn_plan_t* plan, const int32_t* work_d,

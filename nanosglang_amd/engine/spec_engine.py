@@ -26,6 +26,17 @@ the two for a batch of requests:
 4. a request finishes after ``max_new_tokens`` tokens (EOS ignored, as the
    reference's benchmark asks for, bench_throughput.py:67-72).
 
+Graph mode (default): as the reference's engine captures one CUDA graph of
+the decode forward per batch size in ``[1, 2, 4] + range(8, max_bs + 1, 8)``
+(engine.py:110-214) and pads a batch to the next captured size with rows on a
+dummy page (engine.py:357-394), this engine captures one HIP graph of the
+WHOLE speculative step per such size -- the k draft forwards and their
+samplers, the verify forward and the acceptance kernels.  Before each replay
+the host plans all k + 1 attention calls (fixed-size work lists) and writes
+every per-step input (tokens, positions, KV slots, page tables, work lists)
+into one pinned staging buffer, uploaded with a single copy; after the replay
+it reads back the counts and tokens (the reference's ``.item()`` sites).
+
 Sampling: greedy when ``temperature < 1e-6`` (sampling.py:44); otherwise
 draft tokens, ratio tests and resamples use Philox uniforms from
 ``kernels.philox_uniform`` (stream 0: acceptance, stream 1: draft sampling).
@@ -54,10 +65,98 @@ class _Req:
     start: int = 0          # position of out[-1]; KV holds positions < start
 
 
+def graph_batch_sizes(max_bs: int) -> list[int]:
+    """The reference's captured decode sizes (engine.py:117-119), plus max_bs."""
+    return sorted(set([b for b in (1, 2, 4) if b <= max_bs] + list(range(8, max_bs + 1, 8))
+                      + [max_bs]))
+
+
+class _Arena:
+    """Named int/float arrays that live in one pinned host buffer and one
+    device buffer at the same offsets: the host fills the pinned views, one
+    ``upload`` copies them all (the device views have fixed addresses, so a
+    captured graph reads them)."""
+
+    def __init__(self, specs, device):
+        offs, o = {}, 0
+        for name, dt, n in specs:
+            o = (o + 255) // 256 * 256
+            es = torch.empty(0, dtype=dt).element_size()
+            offs[name] = (o, dt, n, es)
+            o += n * es
+        self.nbytes = max(256, (o + 255) // 256 * 256)
+        self.host = torch.zeros(self.nbytes, dtype=torch.uint8, pin_memory=True)
+        self.dev = torch.zeros(self.nbytes, dtype=torch.uint8, device=device)
+        self.h, self.d = {}, {}
+        for name, (o, dt, n, es) in offs.items():
+            self.d[name] = self.dev[o:o + n * es].view(dt)
+            self.h[name] = self.host[o:o + n * es].view(dt).numpy()
+
+    def upload(self):
+        self.dev.copy_(self.host, non_blocking=True)
+
+
+class _StepGraph:
+    """Static buffers, attention wrappers and the captured graph of one
+    speculative step at padded batch size ``bs``."""
+
+    def __init__(self, eng: "SpecEngine", bs: int, max_pages: int):
+        c = eng.model.config
+        k, dev = eng.k, eng.device
+        Hq, Hkv = c.num_attention_heads, c.num_key_value_heads
+        self.bs = bs
+        lib = kernels._lib()
+        specs = [("tok0", torch.int64, bs), ("start", torch.int32, bs),
+                 ("vpos", torch.int64, bs * (k + 1)), ("vslot", torch.int64, bs * (k + 1))]
+        for i in range(k):
+            specs += [(f"pos{i}", torch.int64, bs), (f"slot{i}", torch.int64, bs)]
+        caps = []
+        for a in range(k + 1):                       # attention calls: k drafts, 1 verify
+            ql = 1 if a < k else k + 1
+            mw, mm = kernels.C.c_int32(0), kernels.C.c_int32(0)
+            kernels.check(lib.nsg_attn_fixed_capacity(bs, ql, Hq, Hkv, kernels.MI355X_CUS,
+                                                      kernels.C.byref(mw), kernels.C.byref(mm)),
+                          "nsg_attn_fixed_capacity")
+            nw = (mw.value + mm.value) * kernels.NSG_ATTN_WORK_INTS
+            caps.append(ql)
+            specs += [(f"qo{a}", torch.int32, bs + 1), (f"kvp{a}", torch.int32, bs + 1),
+                      (f"last{a}", torch.int32, bs), (f"idx{a}", torch.int32, bs * max_pages),
+                      (f"work{a}", torch.int32, nw)]
+        self.arena = A = _Arena(specs, dev)
+        self.attn = []
+        for a in range(k + 1):
+            hb = {"qo_indptr": A.h[f"qo{a}"], "kv_indptr": A.h[f"kvp{a}"],
+                  "kv_indices": A.h[f"idx{a}"], "kv_last": A.h[f"last{a}"], "work": A.h[f"work{a}"]}
+            self.attn.append(BatchPrefillWithPagedKVCacheWrapper(
+                eng.attn_ws, "NHD", use_cuda_graph=True, qo_indptr_buf=A.d[f"qo{a}"],
+                paged_kv_indptr_buf=A.d[f"kvp{a}"], paged_kv_indices_buf=A.d[f"idx{a}"],
+                paged_kv_last_page_len_buf=A.d[f"last{a}"], work_buf=A.d[f"work{a}"],
+                host_bufs=hb, max_q_len=caps[a]))
+        V = c.vocab_size
+        self.drafts = torch.zeros(bs, k, dtype=torch.int64, device=dev)
+        self.vids = torch.zeros(bs, k + 1, dtype=torch.int64, device=dev)
+        self.n_out = torch.zeros(bs, dtype=torch.int32, device=dev)
+        self.emitted = torch.zeros(bs, k + 1, dtype=torch.int64, device=dev)
+        self.rollback = torch.zeros(bs, k, dtype=torch.int64, device=dev)
+        self.n1 = torch.zeros(bs, dtype=torch.int32, device=dev)
+        self.em1 = torch.zeros(bs, 1, dtype=torch.int64, device=dev)
+        self.rb1 = torch.zeros(bs, 0, dtype=torch.int64, device=dev)
+        if not eng.greedy:
+            self.u = torch.zeros(bs, k + 1, dtype=torch.float32, device=dev)
+            self.ud = torch.zeros(k, bs, dtype=torch.float32, device=dev)
+            self.dlog = torch.zeros(bs, k, V, dtype=eng.model.dtype, device=dev)
+        else:
+            self.u = self.ud = self.dlog = None
+        self.n_h = torch.zeros(bs, dtype=torch.int32, pin_memory=True)
+        self.em_h = torch.zeros(bs, k + 1, dtype=torch.int64, pin_memory=True)
+        self.graph = None
+
+
 class SpecEngine:
     def __init__(self, model, draft_layers: int, num_speculative: int, num_blocks: int,
                  block_size: int = 16, temperature: float = 0.0, seed: int = 0,
-                 workspace_bytes: int = 256 << 20):
+                 workspace_bytes: int = 256 << 20, use_graphs: bool = True,
+                 max_batch: int = 32):
         c = model.config
         self.model = model
         self.k = num_speculative
@@ -70,10 +169,15 @@ class SpecEngine:
                                c.head_dim, dtype=torch.bfloat16, device=self.device)
         self.kv = PagedKVCache(self.bm)
         self.P = block_size
-        ws = torch.empty(workspace_bytes, dtype=torch.uint8, device=self.device)
-        self.attn = BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+        self.attn_ws = torch.empty(workspace_bytes, dtype=torch.uint8, device=self.device)
+        self.attn = BatchPrefillWithPagedKVCacheWrapper(self.attn_ws, "NHD")
         self._rng_offset = [0, 0]
         self.stats = {}
+        self.use_graphs = use_graphs
+        self.max_batch = max_batch
+        self._graphs: dict[int, _StepGraph] = {}
+        self._accept_ws = kernels.AcceptWorkspace(self.device)
+        self._dummy_block = None
 
     # ---- helpers ----
     def _uniforms(self, stream: int, n: int) -> torch.Tensor:
@@ -127,11 +231,174 @@ class SpecEngine:
         _, em, _ = kernels.spec_accept(logits.view(B, 1, -1), None, None, u, self.temperature)
         return em[:, 0]
 
+    # ---- graph mode ----
+    def _max_pages(self) -> int:
+        c = self.model.config
+        return (c.max_position_embeddings + self.P - 1) // self.P
+
+    def capture(self, max_batch: int | None = None) -> list[int]:
+        """Capture one graph per padded batch size up to ``max_batch`` (the
+        reference captures at engine start, engine.py:153-156, 164-216).  The
+        KV pool contents are untouched except for the dummy page."""
+        c = self.model.config
+        if max_batch is not None:
+            self.max_batch = max_batch
+        if self._dummy_block is None:
+            self._dummy_block = self.bm.allocate()       # engine.py:139-140
+        if self.k + 1 > self._max_pages() * self.P:
+            raise ValueError("verify window exceeds the position range")
+        V = c.vocab_size
+        # every accept call of every graph shares one workspace, sized once
+        need = max(kernels._lib().nsg_spec_accept_workspace_bytes(self.max_batch, self.k, V),
+                   kernels._lib().nsg_spec_accept_workspace_bytes(self.max_batch, 0, V))
+        self._accept_ws.get(need)
+        pool = torch.cuda.graph_pool_handle()
+        for bs in graph_batch_sizes(self.max_batch):
+            if bs in self._graphs:
+                continue
+            g = _StepGraph(self, bs, self._max_pages())
+            self._fill_step(g, [])                       # all rows on the dummy page
+            g.arena.upload()
+            for _ in range(2):                           # warm-up (allocator, GEMM heuristics)
+                self._graph_body(g)
+            torch.cuda.synchronize(self.device)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, pool=pool):
+                self._graph_body(g)
+            torch.cuda.synchronize(self.device)
+            g.graph = graph
+            self._graphs[bs] = g
+        return sorted(self._graphs)
+
+    def _graph_body(self, g: _StepGraph) -> None:
+        """The captured step: k drafts, verify, acceptance (all on device)."""
+        m, k, A = self.model, self.k, g.arena.d
+        bs = g.bs
+        pool = self._pool()
+        tok = A["tok0"]
+        for i in range(k):
+            lg = m.forward_packed(tok, A[f"pos{i}"], pool, g.attn[i], A[f"slot{i}"], None,
+                                  self.draft_layers)
+            if g.dlog is not None:
+                g.dlog[:, i].copy_(lg)
+            u = None if g.ud is None else g.ud[i].view(bs, 1)
+            kernels.spec_accept(lg.view(bs, 1, -1), None, None, u, self.temperature,
+                                workspace=self._accept_ws, out=(g.n1, g.em1, g.rb1))
+            g.drafts[:, i].copy_(g.em1[:, 0])
+            tok = g.em1[:, 0]
+        g.vids[:, 0].copy_(A["tok0"])
+        g.vids[:, 1:].copy_(g.drafts)
+        tl = m.forward_packed(g.vids.view(-1), A["vpos"], pool, g.attn[k], A["vslot"])
+        kernels.spec_accept(tl.view(bs, k + 1, -1), g.dlog, g.drafts, g.u, self.temperature,
+                            A[f"kvp{k}"], A[f"idx{k}"], A["start"], page_size=self.P,
+                            workspace=self._accept_ws, out=(g.n_out, g.emitted, g.rollback))
+
+    def _fill_step(self, g: _StepGraph, active: list) -> None:
+        """Host side of one step: page tables, slots, positions and the k + 1
+        attention plans, written into the graph's pinned staging views."""
+        c = self.model.config
+        k, P, bs = self.k, self.P, g.bs
+        H = g.arena.h
+        B = len(active)
+        maxp = max([len(r.table.block_indices) for r in active] + [(k + P) // P])
+        tab = np.full((bs, maxp), self._dummy_block, np.int32)
+        for j, r in enumerate(active):
+            bt = r.table.block_indices
+            tab[j, :len(bt)] = bt
+        starts = np.zeros(bs, np.int64)
+        starts[:B] = [r.start for r in active]
+        H["tok0"][:B] = [r.out[-1] for r in active]
+        H["tok0"][B:] = 0
+        H["start"][:] = starts
+        rows = np.arange(bs)
+        cols = np.arange(maxp)[None, :]
+        Hq, Hkv, D = c.num_attention_heads, c.num_key_value_heads, c.head_dim
+        for a in range(k + 1):
+            ql = 1 if a < k else k + 1
+            L = starts + (a + 1 if a < k else k + 1)
+            npg = (L + P - 1) // P
+            kvp = np.zeros(bs + 1, np.int32)
+            np.cumsum(npg, out=kvp[1:])
+            idx = tab[cols < npg[:, None]]
+            last = (L - (npg - 1) * P).astype(np.int32)
+            qo = (np.arange(bs + 1) * ql).astype(np.int32)
+            g.attn[a].plan(qo, kvp, idx, last, Hq, Hkv, D, P, causal=True)
+            if a < k:
+                pos = starts + a
+                H[f"pos{a}"][:] = pos
+                H[f"slot{a}"][:] = tab[rows, pos // P].astype(np.int64) * P + pos % P
+        vpos = (starts[:, None] + np.arange(k + 1)[None, :])
+        H["vpos"][:] = vpos.reshape(-1)
+        H["vslot"][:] = (tab[rows[:, None], vpos // P].astype(np.int64) * P
+                         + vpos % P).reshape(-1)
+
+    def _step_graph(self, active: list):
+        B = len(active)
+        bs = min(b for b in self._graphs if b >= B)
+        g = self._graphs[bs]
+        self._fill_step(g, active)
+        g.arena.upload()
+        if not self.greedy:
+            k = self.k
+            o0, o1 = self._rng_offset
+            lib = kernels._lib()
+            sp = kernels._stream_ptr(self.device)
+            kernels.check(lib.nsg_philox_uniform(self.seed, 0, o0, bs * (k + 1), g.u.data_ptr(),
+                                                 sp), "nsg_philox_uniform")
+            kernels.check(lib.nsg_philox_uniform(self.seed, 1, o1, bs * k, g.ud.data_ptr(), sp),
+                          "nsg_philox_uniform")
+            self._rng_offset = [o0 + bs * (k + 1), o1 + bs * k]
+        g.graph.replay()
+        g.n_h.copy_(g.n_out, non_blocking=True)
+        g.em_h.copy_(g.emitted, non_blocking=True)
+        torch.cuda.current_stream(self.device).synchronize()
+        return g.n_h.numpy()[:B], g.em_h.numpy()[:B]
+
+    # ---- eager mode ----
+    def _step_eager(self, active: list):
+        k, dev = self.k, self.device
+        B = len(active)
+        starts = [r.start for r in active]
+        start_pos = np.asarray(starts, np.int64)
+        tok = self._to_dev(np.asarray([r.out[-1] for r in active], np.int64))
+        ones = [1] * B
+        drafts = torch.empty(B, k, dtype=torch.int64, device=dev)
+        dlog = None
+        for i in range(k):
+            self._plan(active, ones, [s + i + 1 for s in starts])
+            sl = self._to_dev(self._slots(active, [s + i for s in starts], ones))
+            lg = self.model.forward_packed(tok, self._to_dev(start_pos + i), self._pool(),
+                                           self.attn, sl, None, self.draft_layers)
+            if not self.greedy:
+                if dlog is None:
+                    dlog = torch.empty(B, k, lg.shape[-1], dtype=lg.dtype, device=dev)
+                dlog[:, i] = lg
+            tok = self._sample_rows(lg)
+            drafts[:, i] = tok
+        # verify: [last, d_0 .. d_{k-1}] at start .. start+k
+        kvp, idx = self._plan(active, [k + 1] * B, [s + k + 1 for s in starts])
+        vids = torch.empty(B, k + 1, dtype=torch.int64, device=dev)
+        vids[:, 0] = self._to_dev(np.asarray([r.out[-1] for r in active], np.int64))
+        vids[:, 1:] = drafts
+        vpos = self._to_dev((start_pos[:, None] + np.arange(k + 1)[None]).reshape(-1))
+        sl = self._to_dev(self._slots(active, starts, [k + 1] * B))
+        tl = self.model.forward_packed(vids.view(-1), vpos, self._pool(), self.attn, sl)
+        u = None if self.greedy else self._uniforms(0, B * (k + 1)).view(B, k + 1)
+        n_out, emitted, _ = kernels.spec_accept(
+            tl.view(B, k + 1, -1), dlog, drafts, u, self.temperature,
+            self._to_dev(kvp), self._to_dev(idx), self._to_dev(start_pos, torch.int32),
+            page_size=self.P)
+        return n_out.cpu().numpy(), emitted.cpu().numpy()
+
     # ---- main entry ----
     @torch.inference_mode()
     def generate(self, prompts: list[list[int]], max_new_tokens: list[int]):
-        k, dev = self.k, self.device
+        k = self.k
         reqs = [_Req(i, list(p), int(m)) for i, (p, m) in enumerate(zip(prompts, max_new_tokens))]
+        if self.use_graphs and len(reqs) > self.max_batch:
+            raise ValueError(f"{len(reqs)} requests > max_batch {self.max_batch} of the graphs")
+        if self.use_graphs and not self._graphs:
+            self.capture()
         t0 = time.perf_counter()
         # 1. admission
         for r in reqs:
@@ -157,40 +424,12 @@ class SpecEngine:
         # 3. speculative steps
         while active:
             B = len(active)
-            starts = [r.start for r in active]
             for r in active:
                 self.kv.reserve(r.table, r.start + k + 1)
-            start_pos = np.asarray(starts, np.int64)
-            tok = self._to_dev(np.asarray([r.out[-1] for r in active], np.int64))
-            ones = [1] * B
-            drafts = torch.empty(B, k, dtype=torch.int64, device=dev)
-            dlog = None
-            for i in range(k):
-                self._plan(active, ones, [s + i + 1 for s in starts])
-                sl = self._to_dev(self._slots(active, [s + i for s in starts], ones))
-                lg = self.model.forward_packed(tok, self._to_dev(start_pos + i), self._pool(),
-                                               self.attn, sl, None, self.draft_layers)
-                if not self.greedy:
-                    if dlog is None:
-                        dlog = torch.empty(B, k, lg.shape[-1], dtype=lg.dtype, device=dev)
-                    dlog[:, i] = lg
-                tok = self._sample_rows(lg)
-                drafts[:, i] = tok
-            # verify: [last, d_0 .. d_{k-1}] at start .. start+k
-            kvp, idx = self._plan(active, [k + 1] * B, [s + k + 1 for s in starts])
-            vids = torch.empty(B, k + 1, dtype=torch.int64, device=dev)
-            vids[:, 0] = self._to_dev(np.asarray([r.out[-1] for r in active], np.int64))
-            vids[:, 1:] = drafts
-            vpos = self._to_dev((start_pos[:, None] + np.arange(k + 1)[None]).reshape(-1))
-            sl = self._to_dev(self._slots(active, starts, [k + 1] * B))
-            tl = self.model.forward_packed(vids.view(-1), vpos, self._pool(), self.attn, sl)
-            u = None if self.greedy else self._uniforms(0, B * (k + 1)).view(B, k + 1)
-            n_out, emitted, rollback = kernels.spec_accept(
-                tl.view(B, k + 1, -1), dlog, drafts, u, self.temperature,
-                self._to_dev(kvp), self._to_dev(idx), self._to_dev(start_pos, torch.int32),
-                page_size=self.P)
-            n_h = n_out.cpu().numpy()
-            em_h = emitted.cpu().numpy()
+            if self.use_graphs:
+                n_h, em_h = self._step_graph(active)
+            else:
+                n_h, em_h = self._step_eager(active)
             steps += 1
             req_steps += B
             proposed += B * k
@@ -207,7 +446,7 @@ class SpecEngine:
                 else:
                     still.append(r)
             active = still
-        torch.cuda.synchronize(dev)
+        torch.cuda.synchronize(self.device)
         t_total = time.perf_counter() - t0
         n_tok = sum(len(r.out) for r in reqs)
         self.stats = {
@@ -217,5 +456,6 @@ class SpecEngine:
             "tokens_per_step": (accepted + req_steps) / max(1, req_steps),
             "tok_per_s": n_tok / t_total,
             "decode_tok_per_s": (n_tok - len(reqs)) / max(1e-9, t_total - t_prefill),
+            "graphs": sorted(self._graphs),
         }
         return [r.out for r in reqs]

@@ -77,7 +77,21 @@ class BatchPrefillWithPagedKVCacheWrapper:
     """
 
     def __init__(self, float_workspace_buffer: torch.Tensor, kv_layout: str = "NHD",
-                 num_cus: int = MI355X_CUS):
+                 use_cuda_graph: bool = False, qo_indptr_buf: torch.Tensor | None = None,
+                 paged_kv_indptr_buf: torch.Tensor | None = None,
+                 paged_kv_indices_buf: torch.Tensor | None = None,
+                 paged_kv_last_page_len_buf: torch.Tensor | None = None,
+                 num_cus: int = MI355X_CUS, work_buf: torch.Tensor | None = None,
+                 host_bufs: dict | None = None, max_q_len: int | None = None):
+        """``use_cuda_graph=True`` with the four ``*_buf`` int32 device tensors
+        is the reference's graph mode (engine.py:121-133): ``plan`` rewrites
+        those fixed-address buffers and a fixed-size work list (``work_buf``,
+        allocated at the first plan if not given), so a graph captured around
+        ``run`` replays correctly after each re-plan.  The batch is
+        ``len(qo_indptr_buf) - 1``; the tile shape follows ``max_q_len``
+        (default: the first plan's longest query).  With ``host_bufs`` (numpy
+        mirrors keyed qo_indptr / kv_indptr / kv_indices / kv_last / work),
+        ``plan`` writes only the mirrors and the caller uploads them."""
         if kv_layout != "NHD":
             raise ValueError(f"kv_layout {kv_layout!r}: only 'NHD' (the reference's layout)")
         _require_gpu(float_workspace_buffer, "workspace")
@@ -89,6 +103,76 @@ class BatchPrefillWithPagedKVCacheWrapper:
         self._work_d: torch.Tensor | None = None
         self._work_h = np.zeros(0, np.int32)
         self._plan: AttnPlan | None = None
+        self._graph = bool(use_cuda_graph)
+        if self._graph:
+            bufs = {"qo_indptr": qo_indptr_buf, "kv_indptr": paged_kv_indptr_buf,
+                    "kv_indices": paged_kv_indices_buf, "kv_last": paged_kv_last_page_len_buf}
+            for name, t in bufs.items():
+                if t is None:
+                    raise ValueError(f"use_cuda_graph=True needs the {name} buffer")
+                _require_gpu(t, name)
+                if t.dtype != torch.int32 or not t.is_contiguous():
+                    raise ValueError(f"{name} buffer must be contiguous int32")
+            self._batch = qo_indptr_buf.numel() - 1
+            if (paged_kv_indptr_buf.numel() != self._batch + 1
+                    or paged_kv_last_page_len_buf.numel() != self._batch):
+                raise ValueError("graph buffers disagree on the batch size")
+            if host_bufs is not None:
+                for name, t in bufs.items():
+                    if host_bufs[name].shape != (t.numel(),) or host_bufs[name].dtype != np.int32:
+                        raise ValueError(f"host mirror {name} must be int32 ({t.numel()},)")
+            self._gbufs = bufs
+            self._host_bufs = host_bufs
+            self._fixed_q = max_q_len
+            self._fixed = None          # (max_q_len, max_work, max_merge) from the first plan
+            self._work_d = work_buf
+
+    def _plan_fixed(self, lib, qo_h, kvp_h, last_h, B, num_qo_heads, num_kv_heads, head_dim_qk,
+                    page_size, causal, kv_indices) -> AttnPlan:
+        if B != self._batch:
+            raise ValueError(f"graph-mode wrapper holds batch {self._batch}, plan has {B}")
+        if self._fixed is None:
+            mq = self._fixed_q or max(1, int(np.diff(qo_h).max(initial=1)))
+            mw, mm = C.c_int32(0), C.c_int32(0)
+            check(lib.nsg_attn_fixed_capacity(B, mq, num_qo_heads, num_kv_heads, self._num_cus,
+                                              C.byref(mw), C.byref(mm)), "nsg_attn_fixed_capacity")
+            need = (mw.value + mm.value) * NSG_ATTN_WORK_INTS
+            if self._work_d is None:
+                self._work_d = torch.zeros(need, dtype=torch.int32, device=self._device)
+            elif self._work_d.numel() < need or self._work_d.dtype != torch.int32:
+                raise ValueError(f"work_buf must hold {need} int32")
+            if self._host_bufs is not None:
+                self._work_h = self._host_bufs["work"]
+                if self._work_h.dtype != np.int32 or self._work_h.shape[0] < need:
+                    raise ValueError(f"host work mirror must hold {need} int32")
+            else:
+                self._work_h = np.zeros(need, np.int32)
+            self._fixed = (mq, mw.value, mm.value)
+        mq, mw, mm = self._fixed
+        pl = AttnPlan()
+        check(lib.nsg_attn_plan_fixed(qo_h.ctypes.data, kvp_h.ctypes.data, last_h.ctypes.data, B,
+                                      num_qo_heads, num_kv_heads, head_dim_qk, page_size,
+                                      1 if causal else 0, self._num_cus, mq, mw, mm,
+                                      self._work_h.ctypes.data, self._work_h.shape[0],
+                                      C.byref(pl)), "nsg_attn_plan_fixed")
+        nnz = int(kvp_h[-1])
+        idx_buf = self._gbufs["kv_indices"]
+        if nnz > idx_buf.numel():
+            raise ValueError(f"{nnz} page ids exceed the kv_indices buffer ({idx_buf.numel()})")
+        idx_h = _host_i32(kv_indices)[:nnz]
+        if self._host_bufs is not None:
+            hb = self._host_bufs
+            hb["qo_indptr"][:] = qo_h
+            hb["kv_indptr"][:] = kvp_h
+            hb["kv_last"][:] = last_h
+            hb["kv_indices"][:nnz] = idx_h
+        else:
+            n = (pl.num_work + pl.num_merge) * NSG_ATTN_WORK_INTS
+            for name, h in (("qo_indptr", qo_h), ("kv_indptr", kvp_h), ("kv_last", last_h),
+                            ("kv_indices", idx_h)):
+                self._gbufs[name][:h.shape[0]].copy_(torch.from_numpy(h))
+            self._work_d[:n].copy_(torch.from_numpy(self._work_h[:n]))
+        return pl
 
     def plan(self, qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len,
              num_qo_heads: int, num_kv_heads: int, head_dim_qk: int, page_size: int,
@@ -102,6 +186,34 @@ class BatchPrefillWithPagedKVCacheWrapper:
         if len(kvp_h) != B + 1 or len(last_h) != B:
             raise ValueError("qo_indptr, paged_kv_indptr and last_page_len disagree on batch")
         lib = _lib()
+        if self._graph:
+            pl = self._plan_fixed(lib, qo_h, kvp_h, last_h, B, num_qo_heads, num_kv_heads,
+                                  head_dim_qk, page_size, causal, paged_kv_indices)
+        else:
+            pl = self._plan_dynamic(lib, qo_h, kvp_h, last_h, B, num_qo_heads, num_kv_heads,
+                                    head_dim_qk, page_size, causal)
+        if pl.workspace_bytes > self._ws.numel() * self._ws.element_size():
+            raise RuntimeError(
+                f"attention workspace too small: plan needs {pl.workspace_bytes} bytes, "
+                f"buffer has {self._ws.numel() * self._ws.element_size()}")
+        self._plan = pl
+        if self._graph:
+            g = self._gbufs
+            self._qo_indptr, self._kv_indptr = g["qo_indptr"], g["kv_indptr"]
+            self._kv_indices, self._kv_last = g["kv_indices"], g["kv_last"]
+        else:
+            self._qo_indptr = _dev_i32(qo_indptr, self._device)
+            self._kv_indptr = _dev_i32(paged_kv_indptr, self._device)
+            self._kv_indices = _dev_i32(paged_kv_indices, self._device)
+            self._kv_last = _dev_i32(paged_kv_last_page_len, self._device)
+        self._total_q = int(qo_h[-1])
+        self._page_size = page_size
+        self._causal = causal
+        self._sm_scale = (1.0 / math.sqrt(head_dim_qk)) if sm_scale is None else float(sm_scale)
+        self._dims = (num_qo_heads, num_kv_heads, head_dim_qk)
+
+    def _plan_dynamic(self, lib, qo_h, kvp_h, last_h, B, num_qo_heads, num_kv_heads,
+                      head_dim_qk, page_size, causal) -> AttnPlan:
         # an upper bound on work items: every query tile split into every 32-token step
         bound = 0
         G = max(1, num_qo_heads // max(1, num_kv_heads))
@@ -122,23 +234,10 @@ class BatchPrefillWithPagedKVCacheWrapper:
                                1 if causal else 0, self._num_cus, self._work_h.ctypes.data,
                                self._work_cap, C.byref(pl))
         check(rc, "nsg_attn_plan")
-        if pl.workspace_bytes > self._ws.numel() * self._ws.element_size():
-            raise RuntimeError(
-                f"attention workspace too small: plan needs {pl.workspace_bytes} bytes, "
-                f"buffer has {self._ws.numel() * self._ws.element_size()}")
         n = (pl.num_work + pl.num_merge) * NSG_ATTN_WORK_INTS
         if n:
             self._work_d[:n].copy_(torch.from_numpy(self._work_h[:n]), non_blocking=False)
-        self._plan = pl
-        self._qo_indptr = _dev_i32(qo_indptr, self._device)
-        self._kv_indptr = _dev_i32(paged_kv_indptr, self._device)
-        self._kv_indices = _dev_i32(paged_kv_indices, self._device)
-        self._kv_last = _dev_i32(paged_kv_last_page_len, self._device)
-        self._total_q = int(qo_h[-1])
-        self._page_size = page_size
-        self._causal = causal
-        self._sm_scale = (1.0 / math.sqrt(head_dim_qk)) if sm_scale is None else float(sm_scale)
-        self._dims = (num_qo_heads, num_kv_heads, head_dim_qk)
+        return pl
 
     @property
     def plan_info(self) -> AttnPlan:

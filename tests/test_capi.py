@@ -81,6 +81,59 @@ def test_planner_covers_every_query_row_and_kv_token_once(lib, cus):
     assert pl.workspace_bytes >= 256 + pl.num_work * 2 * pl.row_tiles * 16 * (64 + 4) * 4
 
 
+def _plan_fixed(lib, q_lens, kv_lens, batch_cap, max_q, Hq=14, Hkv=2, D=64, P=16, cus=256):
+    mw, mm = C.c_int32(0), C.c_int32(0)
+    assert lib.nsg_attn_fixed_capacity(batch_cap, max_q, Hq, Hkv, cus, C.byref(mw),
+                                       C.byref(mm)) == 0
+    B = len(q_lens)
+    qo = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    npg = [(L + P - 1) // P for L in kv_lens]
+    kvp = np.concatenate([[0], np.cumsum(npg)]).astype(np.int32)
+    last = np.asarray([(L % P) or P for L in kv_lens], np.int32)
+    cap = mw.value + mm.value
+    work = np.full(cap * NSG_ATTN_WORK_INTS, 77, np.int32)    # garbage: padding must clear it
+    pl = AttnPlan()
+    rc = lib.nsg_attn_plan_fixed(qo.ctypes.data, kvp.ctypes.data, last.ctypes.data, B, Hq, Hkv,
+                                 D, P, 1, cus, max_q, mw.value, mm.value, work.ctypes.data, cap,
+                                 C.byref(pl))
+    return rc, pl, work.reshape(cap, NSG_ATTN_WORK_INTS), (mw.value, mm.value)
+
+
+@pytest.mark.parametrize("q,B", [(1, 32), (5, 32), (5, 7), (9, 64)])
+def test_fixed_plan_pads_to_a_constant_grid(lib, q, B):
+    """The graph-mode plan: same grid and tile shape for every step; the real
+    items are exactly the dynamic planner's; the rest are empty."""
+    rng = np.random.default_rng(q * 100 + B)
+    shapes = set()
+    for step in range(6):
+        kv_lens = list(rng.integers(q, 700 * (step + 1), B))
+        rc, pl, work, (mw, mm) = _plan_fixed(lib, [q] * B, kv_lens, B, q)
+        assert rc == 0, lib.nsg_last_error()
+        shapes.add((pl.num_work, pl.num_merge, pl.row_tiles, pl.q_tile_tokens,
+                    pl.workspace_bytes))
+        assert (pl.num_work, pl.num_merge) == (mw, mm)
+        rc2, pd, wd, _, _ = _plan(lib, [q] * B, kv_lens)
+        assert rc2 == 0
+        n, m = pd.num_work, pd.num_merge
+        assert np.array_equal(work[:n], wd[:n])                       # real work items
+        assert (work[n:mw] == 0).all()                                # empty work items
+        assert np.array_equal(work[mw:mw + m], wd[n:n + m])           # real merge items
+        assert (work[mw + m:] == 0).all()                             # empty merge items
+    assert len(shapes) == 1
+
+
+def test_fixed_plan_keeps_tile_shape_and_rejects_longer_queries(lib):
+    # fewer query tokens than the graph's length: same tile shape as the full one
+    rc, pl, _, _ = _plan_fixed(lib, [2] * 8, [100] * 8, 8, 5)
+    rc5, pl5, _, _ = _plan_fixed(lib, [5] * 8, [100] * 8, 8, 5)
+    assert rc == rc5 == 0
+    assert (pl.row_tiles, pl.q_tile_tokens) == (pl5.row_tiles, pl5.q_tile_tokens)
+    assert _plan_fixed(lib, [6] * 8, [100] * 8, 8, 5)[0] == 1       # longer than fixed
+    assert "fixed plan" in lib.nsg_last_error().decode()
+    # capacity for one request on one CU; three long requests need more merge items
+    assert _plan_fixed(lib, [5] * 3, [2000] * 3, 1, 5, cus=1)[0] == 3
+
+
 def test_planner_rejects_bad_input(lib):
     assert _plan(lib, [5], [3])[0] == 1                 # L < q_len under the causal rule
     assert _plan(lib, [5], [30], D=96)[0] == 2          # unsupported head dim

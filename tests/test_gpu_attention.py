@@ -144,3 +144,60 @@ def test_bad_arguments_raise():
         w.plan([0, 1], [0, 1], [0], [3], 14, 2, 96, 16)      # head_dim 96
     with pytest.raises(NativeError):
         w.plan([0, 1], [0, 1], [0], [3], 14, 3, 64, 16)      # 14 % 3
+
+
+@pytest.mark.parametrize("q_len,B", [(5, 32), (1, 32)])
+def test_graph_mode_replays_after_replanning(q_len, B):
+    """use_cuda_graph=True: one captured run() replayed after re-planning new
+    page tables and KV lengths into the fixed buffers equals the eager
+    wrapper bit for bit and the oracle within tolerance, on every replay,
+    with eager work between replays."""
+    from nanosglang_amd.kernels import BatchPrefillWithPagedKVCacheWrapper
+    Hq, Hkv, D, P, N = 14, 2, 64, 16, 4000
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    ws_e = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    bufs = dict(qo_indptr_buf=torch.zeros(B + 1, dtype=torch.int32, device="cuda"),
+                paged_kv_indptr_buf=torch.zeros(B + 1, dtype=torch.int32, device="cuda"),
+                paged_kv_indices_buf=torch.zeros(N, dtype=torch.int32, device="cuda"),
+                paged_kv_last_page_len_buf=torch.zeros(B, dtype=torch.int32, device="cuda"))
+    wg = BatchPrefillWithPagedKVCacheWrapper(ws, "NHD", use_cuda_graph=True, **bufs)
+    we = BatchPrefillWithPagedKVCacheWrapper(ws_e, "NHD")
+    q_s = torch.zeros(B * q_len, Hq, D, dtype=torch.bfloat16, device="cuda")
+    k_s = torch.zeros(N, P, Hkv, D, dtype=torch.bfloat16, device="cuda")
+    v_s = torch.zeros_like(k_s)
+    out_s = torch.zeros_like(q_s)
+    graph = None
+    for step in range(4):
+        lo, hi = [(q_len, 40), (100, 640), (600, 1500), (q_len, 3000)][step]
+        c = workloads.verify_attention_batch(batch=B, q_len=q_len, num_pages=N, min_len=lo,
+                                             max_len=hi, seed=40 + step)
+        print(f"case: graph step {step} q_len={q_len} B={B} L in [{lo}, {hi}]", flush=True)
+        args = (c["qo_indptr"], c["kv_indptr"], c["kv_indices"], c["kv_last_page_len"],
+                Hq, Hkv, D, P)
+        wg.plan(*args, causal=True)
+        q_s.copy_(_dev(c["q"]))
+        k_s.copy_(_dev(c["k"]))
+        v_s.copy_(_dev(c["v"]))
+        if graph is None:
+            wg.run(q_s, (k_s, v_s), out=out_s)            # warm-up outside capture
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                wg.run(q_s, (k_s, v_s), out=out_s)
+        out_s.zero_()
+        graph.replay()
+        we.plan(*args, causal=True)
+        eager = we.run(q_s, (k_s, v_s))                  # eager work after the replay
+        torch.cuda.synchronize()
+        grid = (wg.plan_info.num_work, wg.plan_info.num_merge, wg.plan_info.row_tiles)
+        if step == 0:
+            grid0 = grid
+        assert grid == grid0                              # the captured launch stays valid
+        got = out_s.float().cpu().numpy()
+        assert np.array_equal(got, eager.float().cpu().numpy())
+        ref = _oracle(c)
+        err = np.abs(got - ref).max()
+        print(f"  max abs err {err:.3e}", flush=True)
+        assert err <= TOL_SPEC
+        assert (np.abs(got - ref) <= TOL_TIGHT + 2.0 ** -8 * np.abs(ref)).all()
+    assert wg.check_flags() == 0

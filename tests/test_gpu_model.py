@@ -104,21 +104,27 @@ def test_packed_forward_matches_cpu_oracle(scale, dtype, tol):
         off += S
 
 
-def test_spec_engine_greedy_equals_plain_greedy_and_oracle():
+@pytest.mark.parametrize("graphs", [True, False])
+def test_spec_engine_greedy_equals_plain_greedy_and_oracle(graphs):
     from nanosglang_amd.engine.spec_engine import SpecEngine
+    print(f"case: spec engine greedy, graphs={graphs}", flush=True)
     cpu, gpu = _tiny_models()
     rng = np.random.default_rng(1)
     prompts = [rng.integers(0, 1000, n).tolist() for n in (20, 33, 5, 64)]
     max_new = [24, 17, 30, 9]
-    spec = SpecEngine(gpu, draft_layers=2, num_speculative=4, num_blocks=64)
+    spec = SpecEngine(gpu, draft_layers=2, num_speculative=4, num_blocks=64, use_graphs=graphs,
+                      max_batch=4)
     out_spec = spec.generate(prompts, max_new)
     st = spec.stats
-    print(f"  spec: acceptance {st['acceptance_rate']:.2f} tokens/step {st['tokens_per_step']:.2f}",
-          flush=True)
-    plain = SpecEngine(gpu, draft_layers=2, num_speculative=0, num_blocks=64)
+    print(f"  spec: acceptance {st['acceptance_rate']:.2f} tokens/step {st['tokens_per_step']:.2f}"
+          f" graphs {st['graphs']}", flush=True)
+    plain = SpecEngine(gpu, draft_layers=2, num_speculative=0, num_blocks=64, use_graphs=graphs,
+                       max_batch=4)
     out_plain = plain.generate(prompts, max_new)
     assert [len(o) for o in out_spec] == max_new
-    assert spec.bm.num_free_blocks == 64 and plain.bm.num_free_blocks == 64
+    reserved = 1 if graphs else 0                       # the graphs' dummy padding page
+    assert spec.bm.num_free_blocks == 64 - reserved
+    assert plain.bm.num_free_blocks == 64 - reserved
     same = sum(a == b for a, b in zip(out_spec, out_plain))
     print(f"  spec == plain greedy for {same}/{len(prompts)} requests", flush=True)
     assert same == len(prompts)
@@ -130,6 +136,32 @@ def test_spec_engine_greedy_equals_plain_greedy_and_oracle():
         ref = CPUSpeculativeDecoder(draft, cpu, 4).generate(p, m)
         first = next((i for i, (a, b) in enumerate(zip(o, ref)) if a != b), len(o))
         print(f"  prompt {len(p)}: first divergence from CPU oracle at {first}/{m}", flush=True)
+
+
+def test_spec_engine_graph_equals_eager_stochastic():
+    """Stochastic speculative decoding (T = 0.8): with one request per graph
+    size (no padding rows) the captured step consumes the same Philox words
+    as the eager step, so both produce the same tokens unless a decision
+    sits within rounding of its uniform."""
+    from nanosglang_amd.engine.spec_engine import SpecEngine
+    print("case: spec engine stochastic graph vs eager", flush=True)
+    _, gpu = _tiny_models(scale=1.0)
+    rng = np.random.default_rng(2)
+    prompts = [rng.integers(0, 1000, 40).tolist()]
+    outs, stats = [], []
+    for graphs in (True, False):
+        eng = SpecEngine(gpu, draft_layers=2, num_speculative=3, num_blocks=64, temperature=0.8,
+                         seed=5, use_graphs=graphs, max_batch=1)
+        outs.append(eng.generate(prompts, [40])[0])
+        stats.append(eng.stats)
+        assert eng.bm.num_free_blocks == 64 - (1 if graphs else 0)
+    print(f"  acceptance graph {stats[0]['acceptance_rate']:.2f} "
+          f"eager {stats[1]['acceptance_rate']:.2f}", flush=True)
+    assert len(outs[0]) == len(outs[1]) == 40
+    assert all(0 <= t < 1000 for t in outs[0])
+    first = next((i for i, (a, b) in enumerate(zip(*outs)) if a != b), 40)
+    print(f"  first graph/eager difference at {first}/40", flush=True)
+    assert first >= 20
 
 
 def test_rmsnorm_and_silu_kernels_match_reference_arithmetic():

@@ -216,6 +216,27 @@ int32_t nsg_rmsnorm(const void* x, void* residual, const void* weight, void* out
 int32_t nsg_silu_mul(const void* gate_up, void* out, int64_t num_tokens,
                      int32_t intermediate, nsg_stream_t stream);
 
+/* Linear layers at decode / verify row counts (M <= nsg_linear_max_rows(),
+ * 160): y[m, n] = x[m, :] . w[n, :] for bf16 x (M x K, row stride ldx) and
+ * w (row stride ldw), fp32 accumulation, one rounding to bf16.
+ *   NSG_LINEAR_BIAS:     y = bf16(acc + bias[n]) (bias may be NULL) -- the
+ *                        q/k/v, o_proj, down_proj and lm_head calls of
+ *                        causal_lm.py:229-231, 261, 482, 643-645;
+ *   NSG_LINEAR_SILU_MUL: w has 2N rows [gate; up] and
+ *                        y = bf16(bf16(silu(bf16(g))) * bf16(u)), the gate_proj /
+ *                        up_proj pair plus F.silu(gate) * up (causal_lm.py:481-482).
+ * K must be a multiple of 64 and N of 4; x and w rows 16-byte aligned.  Larger
+ * M returns NSG_ERR_UNSUPPORTED (a library GEMM serves prefill). */
+#define NSG_LINEAR_BIAS 0
+#define NSG_LINEAR_SILU_MUL 1
+int32_t nsg_linear_max_rows(void);
+/* 1 if nsg_linear is the faster choice for this shape on MI355X (few rows;
+ * measured against hipBLASLt), 0 if a library GEMM is. */
+int32_t nsg_linear_preferred(int32_t M, int32_t N, int32_t K);
+int32_t nsg_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias,
+                   void* y, int64_t ldy, int32_t M, int32_t N, int32_t K, int32_t epilogue,
+                   nsg_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Philox4x32-10 uniforms: out[i] = u(seed, stream_id, offset + i) with
  * u = (word >> 8) * 2^-24 and word n of a stream = component n % 4 of

@@ -38,6 +38,9 @@ SIGNATURES = {
     "nsg_attn_plan_fixed": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, i32, i32,
                                   vp, i32, C.POINTER(AttnPlan)]),
     "nsg_attn_workspace_bytes": (i64, [C.POINTER(AttnPlan)]),
+    "nsg_linear_max_rows": (i32, []),
+    "nsg_linear_preferred": (i32, [i32, i32, i32]),
+    "nsg_linear": (i32, [vp, i64, vp, i64, vp, vp, i64, i32, i32, i32, i32, vp]),
     "nsg_attn_run": (i32, [C.POINTER(AttnPlan), vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32,
                            f32, i32, vp, i64, vp]),
     "nsg_attn_check_flags": (i32, [vp, C.POINTER(i32), vp]),

@@ -1,0 +1,320 @@
+// Skinny linear layers of the decode / verify forwards on gfx950.
+//
+// The decoder layers around the verify step (nano_sglang/model/causal_lm.py:
+// q/k/v projections :229-231 and :281-283, o_proj :261 and :307, the SwiGLU
+// MLP :481-482, lm_head :643-645) run on M = batch * tokens-per-request rows:
+// 32 for a draft step and 160 for a verify step at batch 32, k = 4.  At such
+// M a linear layer is a stream of its weight matrix W (N x K bf16) with a
+// little arithmetic per byte, and the work is latency-bound rather than
+// throughput-bound for the small matrices (1.6 - 17 MB).  Library GEMMs tile
+// for large M; this kernel is shaped for the weight stream instead:
+//
+// * a workgroup owns 16 * NT rows of W (output columns) and all M rows of x;
+//   its NW waves split K in 64-element chunks (wave w takes chunks w, w + NW,
+//   ...), so every lane issues its loads for the next chunk while the MFMAs
+//   of the current one run, and the waves' partial sums meet in LDS;
+// * W and x^T fragments go from global memory straight into the operand
+//   layout of v_mfma_f32_16x16x32_bf16 (A = 16 W rows x 32 k, lane l holds
+//   row l % 16, k 8 * (l / 16) .. + 8; B = 32 k x 16 x rows, same lane map),
+//   so no LDS staging is needed: each W row segment is read once, x (a few
+//   hundred KB at most) is served by L2;
+// * the epilogue applies the bias (y = bf16(acc + bias), one rounding, as a
+//   bf16 GEMM with a bias epilogue does), or the SwiGLU gate: W holds the
+//   fused [gate; up] rows, and y = bf16(bf16(silu(bf16(g))) * bf16(u)), the
+//   rounding order of F.silu(gate) * up on bf16 tensors (causal_lm.py:482).
+#include <algorithm>
+
+#include "common.hpp"
+
+namespace nsg {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kChunk = 64;  // K elements per wave step (two MFMA k-slices)
+constexpr int kMaxMT = 10;  // up to 160 rows of x
+
+struct LinParams {
+  const bf16* x;
+  const bf16* w;
+  const bf16* bias;
+  bf16* y;
+  int64_t ldx, ldw, ldy;
+  int M, N, K;     // N: output columns (SwiGLU: the intermediate size I)
+  int w_rows;      // rows of W (N, or 2 I for SwiGLU)
+};
+
+enum { kEpiBias = 0, kEpiSilu = 1 };
+
+__device__ __forceinline__ float silu_bf16(float g) {
+  return bf16_bits_to_float(float_to_bf16_bits(g / (1.f + __expf(-g))));
+}
+
+// One workgroup: output columns [16 NT * blockIdx.x, + 16 NT) (SwiGLU: NT / 2
+// column tiles, each with a gate and an up row block of W), all M rows.  Its
+// MG * NW waves form MG groups of NW: group g owns m tiles [g MT, g MT + MT)
+// and its NW waves split K (more rows per wave would not fit the registers of
+// two load stages; the groups read the same W rows, the second from L2).
+template <int MT, int MG, int NT, int NW, int EPI>
+__global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
+  static_assert(EPI != kEpiSilu || NT % 2 == 0, "SwiGLU pairs gate and up tiles");
+  constexpr int NP = EPI == kEpiSilu ? 2 : 1;  // physical tiles reduced together
+  __shared__ floatx4 red[MG][NP][NW][MT][64];
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int wave = wid % NW;
+  const int grp = wid / NW;
+  const int r16 = lane & 15;
+
+  // Loads are coalesced: for a 16-row x 32-k fragment, lane l reads row
+  // l / 4, 16-byte segment l % 4, so each lane quad covers one row's 64
+  // contiguous bytes (the MFMA layout itself -- lane l = row l % 16 -- puts
+  // four different cache lines in every quad, which the vector L1 serves at a
+  // quarter of its rate).  ds_bpermute then moves segment g of row r from
+  // lane 4 r + g to its MFMA lane r + 16 g.  Rows past the end are clamped
+  // to a valid row; their results are not stored.
+  const int lrow = lane >> 2;
+  const int lseg = (lane & 3) * 8;
+  const int perm_src = 4 * (4 * r16 + (lane >> 4));  // byte address of the source lane
+  const bf16* wp[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    int row;
+    if constexpr (EPI == kEpiSilu) {
+      const int col_tile = blockIdx.x * (NT / 2) + (nt >> 1);
+      row = ((nt & 1) ? p.N : 0) + col_tile * 16 + lrow;
+    } else {
+      row = (blockIdx.x * NT + nt) * 16 + lrow;
+    }
+    row = min(row, p.w_rows - 1);
+    wp[nt] = p.w + (int64_t)row * p.ldw + lseg;
+  }
+  const bf16* xp[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    xp[mt] = p.x + (int64_t)min((grp * MT + mt) * 16 + lrow, p.M - 1) * p.ldx + lseg;
+  auto to_mfma = [&](u32x4 v) {
+    u32x4 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = __builtin_amdgcn_ds_bpermute(perm_src, (int)v[j]);
+    return __builtin_bit_cast(bf16x8, r);
+  };
+
+  floatx4 acc[NT][MT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int nchunks = p.K / kChunk;
+  // workgroups start their K sweep at different chunks: otherwise all of them
+  // read the same x lines at the same moment, from the same L2 channels
+  const int rot = (int)(blockIdx.x % (unsigned)nchunks);
+  // two register stages: loads of chunk c + NW are in flight while chunk c
+  // is multiplied
+  u32x4 wa[NT][2], xa[MT][2], wb[NT][2], xb[MT][2];
+  auto load = [&](int c, u32x4 (&wv)[NT][2], u32x4 (&xv)[MT][2]) {
+    int cr = c + rot;
+    cr = cr >= nchunks ? cr - nchunks : cr;
+    const int k0 = cr * kChunk;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      wv[nt][0] = *reinterpret_cast<const u32x4*>(wp[nt] + k0);
+      wv[nt][1] = *reinterpret_cast<const u32x4*>(wp[nt] + k0 + 32);
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      xv[mt][0] = *reinterpret_cast<const u32x4*>(xp[mt] + k0);
+      xv[mt][1] = *reinterpret_cast<const u32x4*>(xp[mt] + k0 + 32);
+    }
+  };
+  auto mma = [&](const u32x4 (&wv)[NT][2], const u32x4 (&xv)[MT][2]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      bf16x8 wf[NT], xf[MT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) wf[nt] = to_mfma(wv[nt][h]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) xf[mt] = to_mfma(xv[mt][h]);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          acc[nt][mt] =
+              __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[nt], xf[mt], acc[nt][mt], 0, 0, 0);
+    }
+  };
+  // This wave's chunks are wave + NW i for i < n.  The loop body issues its
+  // loads unconditionally: a load under a branch would make the wait-count
+  // pass assume it might be outstanding and drain the next chunk's loads
+  // before the current chunk's MFMAs.
+  const int n = (nchunks - wave + NW - 1) / NW;
+  if (n > 0) load(wave, wa, xa);
+  int i = 0;
+  // sched_barrier(0): the machine scheduler would otherwise sink the next
+  // chunk's loads next to their MFMAs (to shorten live ranges), which turns
+  // the two-stage pipeline back into one memory latency per chunk
+  for (; i + 2 < n; i += 2) {
+    load(wave + (i + 1) * NW, wb, xb);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(wa, xa);
+    __builtin_amdgcn_sched_barrier(0);
+    load(wave + (i + 2) * NW, wa, xa);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(wb, xb);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (i + 1 < n) {
+    load(wave + (i + 1) * NW, wb, xb);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(wa, xa);
+    mma(wb, xb);
+  } else if (i < n) {
+    mma(wa, xa);
+  }
+
+  // cross-wave reduction and epilogue, NP physical tiles at a time.  Lane l
+  // of tile (nt, mt) holds y rows m = 16 mt + l % 16, columns 4 (l / 16) + i.
+#pragma unroll
+  for (int t0 = 0; t0 < NT; t0 += NP) {
+#pragma unroll
+    for (int q = 0; q < NP; ++q)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) red[grp][q][wave][mt][lane] = acc[t0 + q][mt];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < MG * MT * 64; idx += MG * NW * 64) {
+      const int g = idx / (MT * 64);
+      const int mt = (idx >> 6) % MT;
+      const int l = idx & 63;
+      const int m = (g * MT + mt) * 16 + (l & 15);
+      floatx4 s[NP];
+#pragma unroll
+      for (int q = 0; q < NP; ++q) {
+        s[q] = red[g][q][0][mt][l];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) s[q] += red[g][q][w][mt][l];
+      }
+      int n;
+      if constexpr (EPI == kEpiSilu)
+        n = (blockIdx.x * (NT / 2) + t0 / 2) * 16 + 4 * (l >> 4);
+      else
+        n = (blockIdx.x * NT + t0) * 16 + 4 * (l >> 4);
+      if (m >= p.M || n >= p.N) continue;
+      float v[4];
+      if constexpr (EPI == kEpiSilu) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float g = bf16_bits_to_float(float_to_bf16_bits(s[0][i]));
+          const float u = bf16_bits_to_float(float_to_bf16_bits(s[1][i]));
+          v[i] = silu_bf16(g) * u;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = s[0][i];
+        if (p.bias) {
+          const u32x2 b = *reinterpret_cast<const u32x2*>(p.bias + n);
+          v[0] += bf16_bits_to_float(b[0] & 0xffff);
+          v[1] += bf16_bits_to_float(b[0] >> 16);
+          v[2] += bf16_bits_to_float(b[1] & 0xffff);
+          v[3] += bf16_bits_to_float(b[1] >> 16);
+        }
+      }
+      *reinterpret_cast<u32x2*>(p.y + (int64_t)m * p.ldy + n) =
+          u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    }
+    __syncthreads();
+  }
+}
+
+// Tile shape per row count: more W rows per workgroup as M grows, so that x
+// (read from L2 once per workgroup) stays a small multiple of W's bytes.
+template <int MT, int MG, int NT, int NW, int EPI>
+int32_t launch_cfg(const LinParams& p, hipStream_t s) {
+  const int cols_per_wg = 16 * (EPI == kEpiSilu ? NT / 2 : NT);
+  const int grid = (p.N + cols_per_wg - 1) / cols_per_wg;
+  hipLaunchKernelGGL((linear_kernel<MT, MG, NT, NW, EPI>), dim3(grid), dim3(MG * NW * 64), 0, s,
+                     p);
+  return launch_status("linear_kernel");
+}
+
+template <int EPI>
+int32_t launch_epi(const LinParams& p, hipStream_t s) {
+  constexpr int N1 = EPI == kEpiSilu ? 2 : 1;  // M <= 32: one column tile per workgroup
+  switch ((p.M + 15) / 16) {
+    case 1: return launch_cfg<1, 1, N1, 8, EPI>(p, s);
+    case 2: return launch_cfg<2, 1, N1, 8, EPI>(p, s);
+    case 3: return launch_cfg<3, 1, 2, 8, EPI>(p, s);
+    case 4: return launch_cfg<4, 1, 2, 8, EPI>(p, s);
+    case 5: return launch_cfg<5, 1, 2, 8, EPI>(p, s);
+    case 6: return launch_cfg<3, 2, 4, 4, EPI>(p, s);
+    case 7:
+    case 8: return launch_cfg<4, 2, 2, 4, EPI>(p, s);
+    case 9:
+    case 10: return launch_cfg<5, 2, 2, 4, EPI>(p, s);
+    default: break;
+  }
+  set_error("M %d > %d rows", p.M, kMaxMT * 16);
+  return NSG_ERR_UNSUPPORTED;
+}
+
+}  // namespace
+}  // namespace nsg
+
+using namespace nsg;
+
+// Where this kernel beats a library GEMM on MI355X (measured per shape, with
+// weights streamed from HBM): every x row re-read per workgroup costs L2
+// bandwidth, so the kernel serves few rows, and for very wide outputs (the
+// lm_head) only up to 16.
+constexpr int kFastRows = 64;
+constexpr int kFastRowsWide = 16;
+constexpr int kWideN = 65536;
+
+extern "C" int32_t nsg_linear_max_rows(void) { return kMaxMT * 16; }
+
+extern "C" int32_t nsg_linear_preferred(int32_t M, int32_t N, int32_t K) {
+  if (M < 1 || K % kChunk != 0 || N % 4 != 0) return 0;
+  return M <= (N >= kWideN ? kFastRowsWide : kFastRows) ? 1 : 0;
+}
+
+extern "C" int32_t nsg_linear(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                              const void* bias, void* y, int64_t ldy, int32_t M, int32_t N,
+                              int32_t K, int32_t epilogue, nsg_stream_t stream) {
+  NSG_CHECK_ARG(M >= 0 && N > 0 && K > 0, "M %d, N %d, K %d", M, N, K);
+  if (M == 0) {
+    clear_error();
+    return NSG_OK;
+  }
+  NSG_CHECK_ARG(x && w && y, "null pointer argument");
+  NSG_CHECK_ARG(epilogue == NSG_LINEAR_BIAS || epilogue == NSG_LINEAR_SILU_MUL,
+                "unknown epilogue %d", epilogue);
+  NSG_CHECK_ARG(!(epilogue == NSG_LINEAR_SILU_MUL && bias), "SwiGLU epilogue takes no bias");
+  if (M > kMaxMT * 16) {
+    set_error("M %d > %d rows (use a library GEMM)", M, kMaxMT * 16);
+    return NSG_ERR_UNSUPPORTED;
+  }
+  if (K % kChunk != 0 || N % 4 != 0) {
+    set_error("K %d must be a multiple of %d and N %d of 4", K, kChunk, N);
+    return NSG_ERR_UNSUPPORTED;
+  }
+  NSG_CHECK_ARG(ldx >= K && ldw >= K && ldy >= N, "leading dimensions too small");
+  NSG_CHECK_ARG(ldx % 8 == 0 && ldw % 8 == 0 && ldy % 4 == 0 &&
+                    ((uintptr_t)x | (uintptr_t)w) % 16 == 0 && (uintptr_t)y % 8 == 0 &&
+                    (uintptr_t)bias % 8 == 0,
+                "x and w rows must be 16-byte aligned, y rows and bias 8-byte aligned");
+  LinParams p;
+  p.x = static_cast<const bf16*>(x);
+  p.w = static_cast<const bf16*>(w);
+  p.bias = static_cast<const bf16*>(bias);
+  p.y = static_cast<bf16*>(y);
+  p.ldx = ldx;
+  p.ldw = ldw;
+  p.ldy = ldy;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.w_rows = epilogue == NSG_LINEAR_SILU_MUL ? 2 * N : N;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return epilogue == NSG_LINEAR_SILU_MUL ? launch_epi<kEpiSilu>(p, s) : launch_epi<kEpiBias>(p, s);
+}

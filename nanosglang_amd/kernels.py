@@ -475,6 +475,47 @@ def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Te
     return out
 
 
+LINEAR_BIAS, LINEAR_SILU_MUL = 0, 1
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
+           swiglu: bool = False, out: torch.Tensor | None = None,
+           force: bool = False) -> torch.Tensor:
+    """y = x @ weight.T (+ bias) for bf16 (M, K) rows (C ABI: nsg_linear).
+
+    ``swiglu``: weight holds the fused [gate; up] rows (2I, K) and the
+    result is bf16(silu(gate)) * up, (M, I).  Shapes where the library is
+    faster (``nsg_linear_preferred``: many rows, prefill) go to hipBLASLt via
+    F.linear, plus the SwiGLU kernel; ``force`` runs nsg_linear whenever it
+    supports the shape (tests)."""
+    _require_gpu(x, "x")
+    M, K = x.shape
+    rows = weight.shape[0]
+    N = rows // 2 if swiglu else rows
+    lib = _lib()
+    fits = (M <= lib.nsg_linear_max_rows() and K % 64 == 0 and N % 4 == 0 and x.stride(1) == 1
+            and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0 and x.dtype == torch.bfloat16)
+    if not fits or not (force or lib.nsg_linear_preferred(M, N, K)):
+        y = torch.nn.functional.linear(x, weight, bias)
+        if swiglu:
+            return silu_mul(y, out)
+        if out is not None:
+            out.copy_(y)
+            return out
+        return y
+    if weight.dtype != torch.bfloat16 or weight.stride(1) != 1 or weight.shape[1] != K:
+        raise ValueError("weight must be bf16 (N, K) with unit inner stride")
+    if bias is not None and (bias.dtype != torch.bfloat16 or not bias.is_contiguous()):
+        raise ValueError("bias must be contiguous bf16")
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
+    check(lib.nsg_linear(x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
+                         _ptr(bias), out.data_ptr(), out.stride(0), M, N, K,
+                         LINEAR_SILU_MUL if swiglu else LINEAR_BIAS, _stream_ptr(x.device)),
+          "nsg_linear")
+    return out
+
+
 def philox_uniform(seed: int, stream_id: int, offset: int, n: int, device) -> torch.Tensor:
     """n float32 uniforms of Philox4x32-10 stream ``stream_id`` (see nsg_spec.h)."""
     out = torch.empty(n, dtype=torch.float32, device=device)

@@ -9,7 +9,10 @@ layer writes its K/V into the paged pool and runs paged attention
 (:329-342).
 
 MI355X-side choices:
-* q/k/v are one fused GEMM (and gate/up another), via torch / hipBLASLt;
+* q/k/v are one fused GEMM (and gate/up another, with the SwiGLU gate in its
+  epilogue); at decode / verify row counts (<= 160) every linear layer runs
+  the HIP weight-streaming kernel ``kernels.linear``, at prefill sizes
+  hipBLASLt;
 * RoPE + KV-slot write is one HIP kernel (``kernels.rope_kv_write``) with
   the reference's bf16 rounding order; attention is the HIP verify-attention
   kernel behind ``BatchPrefillWithPagedKVCacheWrapper``;
@@ -145,14 +148,14 @@ class CausalLM:
             # residual += x (causal_lm.py:505, 531), then RMSNorm -- one kernel
             h = kernels.rmsnorm(residual if x is None else x, L["ln1"], eps,
                                 residual=None if x is None else residual)
-            qkv = F.linear(h, L["qkv"], L["qkv_b"])
+            qkv = kernels.linear(h, L["qkv"], L["qkv_b"])
             q = kernels.rope_kv_write(qkv, Hq, Hkv, D, positions, self.rope_cos, self.rope_sin,
                                       write_indices, k_pool[li], v_pool[li])
             attn = attn_wrapper.run(q, (k_pool[li], v_pool[li]))
-            x = F.linear(attn.view(-1, Hq * D), L["o"])
+            x = kernels.linear(attn.view(-1, Hq * D), L["o"])
             h = kernels.rmsnorm(x, L["ln2"], eps, residual=residual)   # causal_lm.py:147-154
-            x = F.linear(kernels.silu_mul(F.linear(h, L["gate_up"])), L["down"])
+            x = kernels.linear(kernels.linear(h, L["gate_up"], swiglu=True), L["down"])
         h = kernels.rmsnorm(x, self.norm, eps, residual=residual)
         if logit_indices is not None:
             h = h[logit_indices]
-        return F.linear(h, self.lm_head)
+        return kernels.linear(h, self.lm_head)

@@ -18,19 +18,23 @@
 // XCD's L2):
 //   stats_kernel   grid (chunks, rows): every target row (and draft row when
 //     stochastic) is cut into chunks; a workgroup reduces its chunk to
-//     (max, sum 2^x) -- or (max, first argmax) when greedy -- with 16-byte
-//     loads and wave-shuffle reductions.  This pass streams every logit once.
+//     (max, sum 2^x) -- or (max, first argmax) when greedy -- from batches of
+//     non-temporal 16-byte loads issued together, with a lazily rescaled
+//     running sum (fma + exp + add per logit).  This pass streams every logit
+//     once.
 //   greedy: finalize_kernel, one wave per request: combine the argmax chunks,
 //     compare with the drafts, write tokens and rollback slots.
-//   stochastic: sum_kernel grid (chunks, B): each workgroup recombines the
-//     (tiny) chunk stats of its request, runs the k ratio tests, and sums the
-//     residual (or bonus) weights of its chunk of the one decided row pair;
-//     select_kernel, one workgroup per request: picks the chunk by a
-//     sequential prefix and the token by a block scan over contiguous
-//     per-thread runs, re-reading one chunk only.  The decided rows were just
-//     streamed by stats_kernel.
+//   stochastic (V % 8 == 0): resolve_kernel grid (16, B): each workgroup
+//     runs the decision (the k ratio tests, a ballot for the first
+//     rejection), then its 4 waves stream 4 of the request's 64 vocabulary
+//     ranges of the one decided row pair and write per-step weight sums;
+//     select_kernel2, one wave per request, walks those sums to the step and
+//     recomputes that one step for the token.
+//   stochastic (other V): decide_kernel, sum_kernel (chunk sums) and
+//     select_kernel (chunk prefix, block scan of one chunk).
 #include <cfloat>
 #include <climits>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -44,6 +48,7 @@ constexpr int kMaxChunks = 64;
 constexpr int kTargetWgs = 4096;
 constexpr int64_t kFlagBytes = 256;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kSlack = 16.f;  // lazy-rescale headroom of the running sums (log2 units)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -69,6 +74,7 @@ struct AccParams {
   float2* stats;  // [rows][nch]
   float* dec;     // [B][8]
   float* psum;    // [B][nch2]
+  float2* rsum;   // [B][kRsRanges][kRsMaxSteps] step sums (residual, target)
   int* flags;
 };
 
@@ -203,7 +209,10 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
   const int tid = threadIdx.x;
   const bool vec = ((roff % Logit<T>::kAlign) == 0);
 
-  float m = -INFINITY, s = 0.f;  // stochastic: running max / sum of 2^(x c - m)
+  // stochastic: running reference m and sum of 2^(x c - m).  m starts finite
+  // (-FLT_MAX): an all -inf chunk then sums exact zeros instead of NaN.
+  float m = -FLT_MAX, s = 0.f;
+  float m_hi = -FLT_MAX;         // rescale threshold: m + kSlack
   float bv = -INFINITY;          // greedy: best value / index
   int bi = INT_MAX;
   auto take = [&](float x, int v) {
@@ -214,8 +223,9 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
       if (y > m) {
         s = s * exp2f(m - y);
         m = y;
+        m_hi = m + kSlack;
       }
-      s += exp2f(y - (m == -INFINITY ? 0.f : m));
+      s += exp2f(y - m);
     }
   };
   int v = v0 + tid * 8;
@@ -223,8 +233,8 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
   // vector beats the running best; stochastic -- max on the raw logits (c > 0),
   // then exp2(fma(x, c, -m)) with the bare v_exp_f32 (arguments <= 0).
   auto take8 = [&](const float* x, int vv) {
-    float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
-                     fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+    float mx = fmaxf(fmaxf(fmaxf(fmaxf(x[0], x[1]), x[2]), fmaxf(x[3], x[4])),
+                     fmaxf(fmaxf(x[5], x[6]), x[7]));  // v_max3 x 3 + v_max
     if constexpr (GREEDY) {
       if (mx > bv || bi == INT_MAX) {
         int e = 0;
@@ -235,33 +245,50 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
         }
       }
     } else {
+      // lazy rescale: the reference m moves only when a logit exceeds it by
+      // more than kSlack (terms stay <= 2^kSlack), so the common path is one
+      // compare per 8 logits and fma + exp + add per logit
       mx *= p.c;
-      if (mx > m) {
-        s = s * __builtin_amdgcn_exp2f(m - mx);
+      if (__builtin_expect(mx > m_hi, 0)) {
+        s = s * __builtin_amdgcn_exp2f(m - mx);  // argument < 0; 0 from the -FLT_MAX start
         m = mx;
+        m_hi = m + kSlack;
       }
-      const float nm = m == -INFINITY ? 0.f : -m;  // all -inf so far: adds 0
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s += __builtin_amdgcn_exp2f(__builtin_fmaf(x[e], p.c, nm));
+      for (int e = 0; e < 8; ++e) s += __builtin_amdgcn_exp2f(__builtin_fmaf(x[e], p.c, -m));
     }
   };
+  // Full 8-vectors of the chunk (chunk starts are multiples of 8), read in
+  // batches of U independent 16-byte loads per thread: every load of a batch
+  // is issued before any is consumed, the batch's missing tail predicated
+  // off, so a chunk costs one or two memory round trips, not one per vector.
+  const int vfull = v0 + ((v1 - v0) & ~7);
   if (vec) {
-    constexpr int U = 8;  // independent 16-byte loads in flight per thread
+    constexpr int U = 8;
     constexpr int STRIDE = kThreads * 8;
     constexpr int W = sizeof(T) * 8 / 16;  // 16-byte loads per 8 logits
-    for (; v + (U - 1) * STRIDE + 8 <= v1; v += U * STRIDE) {
+    auto batch = [&](int vb, auto full) {
       u32x4 raw[U][W];
 #pragma unroll
       for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int w = 0; w < W; ++w)
-          raw[u][w] = *reinterpret_cast<const u32x4*>(
-              reinterpret_cast<const char*>(base) + (roff + v + u * STRIDE) * sizeof(T) + 16 * w);
+        for (int w = 0; w < W; ++w) {
+          const u32x4* src = reinterpret_cast<const u32x4*>(
+              reinterpret_cast<const char*>(base) + (roff + vb + u * STRIDE) * sizeof(T) + 16 * w);
+          if constexpr (decltype(full)::value)
+            raw[u][w] = __builtin_nontemporal_load(src);
+          else
+            raw[u][w] = vb + u * STRIDE < vfull ? __builtin_nontemporal_load(src)
+                                                 : u32x4{0u, 0u, 0u, 0u};
+        }
       // all U*W loads are issued before any is consumed (the compiler would
-      // otherwise sink each load to its use and serialise them)
+      // otherwise sink each load to its use and serialise them).  Non-temporal:
+      // a streaming read of every logit once, which MI355X serves faster than
+      // cached loads
       asm volatile("" ::: "memory");
 #pragma unroll
       for (int u = 0; u < U; ++u) {
+        if (!decltype(full)::value && vb + u * STRIDE >= vfull) break;
         float x[8];
         if constexpr (sizeof(T) == 2) {
 #pragma unroll
@@ -273,19 +300,16 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
 #pragma unroll
           for (int i = 0; i < 8; ++i) x[i] = __uint_as_float(raw[u][i >> 2][i & 3]);
         }
-        take8(x, v + u * STRIDE);
+        take8(x, vb + u * STRIDE);
       }
-    }
-    for (; v + 8 <= v1; v += STRIDE) {
-      float x[8];
-      Logit<T>::load8(base, roff + v, x);
-      take8(x, v);
-    }
+    };
+    int vb = v;
+    for (; vb + (U - 1) * STRIDE < vfull; vb += U * STRIDE) batch(vb, std::true_type{});
+    if (vb < vfull) batch(vb, std::false_type{});
   }
-  // tail (and unaligned rows): scalar, still in increasing index per thread
-  for (; v < v1; v += kThreads * 8) {
-    for (int e = 0; e < 8 && v + e < v1; ++e) take(Logit<T>::at(base, roff + v + e), v + e);
-  }
+  // the chunk's partial last vector, or every element of an unaligned row:
+  // scalar, in increasing index per thread
+  for (int vv = (vec ? vfull : v0) + tid; vv < v1; vv += kThreads) take(Logit<T>::at(base, roff + vv), vv);
 
   const int lane = tid & 63, wave = tid >> 6;
   if constexpr (GREEDY) {
@@ -669,9 +693,243 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(AccParams p) {
   if (tid == 0) p.emitted[(int64_t)b * (p.k + 1) + j] = s_tok;
 }
 
+// ---- stochastic tail in two launches (V % 8 == 0, V <= kRsMaxV) ----
+//
+// resolve_kernel, grid (kRsSplits, B) x 256 threads: every workgroup of
+// request b runs the (identical) decision in wave 0 -- split 0 also writes
+// the accepted prefix, counts, slots and the decision record -- then each of
+// its waves streams one of the request's kRsRanges contiguous vocabulary
+// ranges of the decided row pair in 512-logit steps (lane l: logits
+// 8 l .. 8 l + 7 of a step, 1 KB contiguous per wave load) and writes the
+// step sums of the residual max(0, pt - pd) and of pt (the zero-residual
+// fallback needs no second pass) -- each an inclusive wave scan of the
+// lanes' 8-logit runs.
+// select_kernel2, one wave per request: lane r sums range r's steps in
+// order, a wave scan orders the ranges, the crossing lane finds its step,
+// and the whole wave recomputes that one step with the same arithmetic
+// (step_runs) to find the lane and the logit.  Rounding that leaves no
+// crossing picks the last positive weight.
+constexpr int kRsThreads = 256;
+constexpr int kRsWaves = kRsThreads / 64;
+constexpr int kRsSplits = 16;
+constexpr int kRsRanges = kRsSplits * kRsWaves;  // 64: one per lane of select_kernel2
+constexpr int kRsMaxSteps = 16;
+constexpr int kRsStep = 512;
+constexpr int kRsMaxV = kRsRanges * kRsMaxSteps * kRsStep;
+
+__device__ __forceinline__ float wave_incl_scan(float x, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+__device__ __forceinline__ int rs_steps(int V) {
+  return ((V + kRsStep - 1) / kRsStep + kRsRanges - 1) / kRsRanges;
+}
+
+// This lane's 8 logits of a step, loaded from a clamped, in-range address
+// (V % 8 == 0 on this path) ...
+template <typename T>
+struct StepRaw {
+  static constexpr int W = sizeof(T) * 8 / 16;  // 16-byte loads per 8 logits
+  u32x4 t[W], d[W];
+};
+
+template <typename T>
+__device__ __forceinline__ void step_load(const AccParams& p, int64_t to, int64_t dof, int mode,
+                                          int v, StepRaw<T>& r) {
+  const int vc = min(v, p.V - 8);
+#pragma unroll
+  for (int w = 0; w < StepRaw<T>::W; ++w) {
+    r.t[w] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(p.tl) +
+                                             (to + vc) * sizeof(T) + 16 * w);
+    r.d[w] = mode == 0 ? *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(p.dl) +
+                                                         (dof + vc) * sizeof(T) + 16 * w)
+                       : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ float raw_at(const u32x4* r, int e) {
+  if constexpr (sizeof(T) == 2) {
+    const uint32_t w = r[0][e >> 1];
+    return __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
+  } else {
+    return __uint_as_float(r[e >> 2][e & 3]);
+  }
+}
+
+// ... and its residual and target weights (zero past V) and their runs.
+template <typename T>
+__device__ __forceinline__ void step_weights(const AccParams& p, int mode, const Decision& d,
+                                             int v, const StepRaw<T>& r, float* wres,
+                                             float* wpt, float& res, float& pts) {
+  res = 0.f;
+  pts = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const bool in = v < p.V;
+    const float pt =
+        in ? __builtin_amdgcn_exp2f(__builtin_fmaf(raw_at<T>(r.t, e), p.c, -d.Mt)) * d.iZt : 0.f;
+    const float rr =
+        mode == 0 && in
+            ? fmaxf(0.f, pt - __builtin_amdgcn_exp2f(__builtin_fmaf(raw_at<T>(r.d, e), p.c, -d.Md)) * d.iZd)
+            : pt;
+    wres[e] = rr;
+    wpt[e] = pt;
+    res += rr;
+    pts += pt;
+  }
+}
+
+__device__ __forceinline__ void store_decision(float* dd, const Decision& d) {
+  dd[0] = __int_as_float(d.j);
+  dd[1] = __int_as_float(d.mode);
+  dd[2] = d.Mt;
+  dd[3] = d.iZt;
+  dd[4] = d.Md;
+  dd[5] = d.iZd;
+}
+
+__device__ __forceinline__ Decision load_decision(const float* dd) {
+  Decision d;
+  d.j = __float_as_int(dd[0]);
+  d.mode = __float_as_int(dd[1]);
+  d.Mt = dd[2];
+  d.iZt = dd[3];
+  d.Md = dd[4];
+  d.iZd = dd[5];
+  return d;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kRsThreads) void resolve_kernel(AccParams p) {
+  __shared__ Decision s_d;
+  const int b = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  if (wave == 0) {
+    const Decision d = decide<T>(p, b, blockIdx.x == 0);  // split 0 writes the outputs
+    if (lane == 0) s_d = d;
+  }
+  __syncthreads();
+  const Decision d = s_d;
+  const int64_t to = trow(p, b, d.j);
+  const int64_t dof = d.mode == 0 ? drow(p, b, d.j) : 0;
+  const int ns = rs_steps(p.V);
+  const int r = blockIdx.x * kRsWaves + wave;
+  const int v0 = r * ns * kRsStep + 8 * lane;
+  float2* out = p.rsum + ((int64_t)b * kRsRanges + r) * kRsMaxSteps;
+  constexpr int G = 8;  // steps whose loads are in flight together
+  for (int q0 = 0; q0 < ns; q0 += G) {
+    StepRaw<T> raw[G];
+#pragma unroll
+    for (int i = 0; i < G; ++i) step_load<T>(p, to, dof, d.mode, v0 + (q0 + i) * kRsStep, raw[i]);
+    __builtin_amdgcn_sched_barrier(0);  // all G steps' loads before any arithmetic
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      if (q0 + i >= ns) break;
+      float wr[8], wp[8], res, pts;
+      step_weights<T>(p, d.mode, d, v0 + (q0 + i) * kRsStep, raw[i], wr, wp, res, pts);
+      const float sr = __shfl(wave_incl_scan(res, lane), 63, 64);
+      const float sp = __shfl(wave_incl_scan(pts, lane), 63, 64);
+      if (lane == 0) out[q0 + i] = make_float2(sr, sp);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(64) void select_kernel2(AccParams p) {
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x;
+  const Decision d = load_decision(p.dec + (int64_t)b * 8);
+  const int64_t to = trow(p, b, d.j);
+  const int64_t dof = d.mode == 0 ? drow(p, b, d.j) : 0;
+  const float u = p.u[(int64_t)b * (p.k + 1) + p.k];
+  const int ns = rs_steps(p.V);
+  const float2* rs = p.rsum + ((int64_t)b * kRsRanges + lane) * kRsMaxSteps;
+  float sr[kRsMaxSteps], sp[kRsMaxSteps];
+  float lr = 0.f, lp = 0.f;
+#pragma unroll
+  for (int q = 0; q < kRsMaxSteps; ++q) {
+    const float2 v = q < ns ? rs[q] : make_float2(0.f, 0.f);
+    sr[q] = v.x;
+    sp[q] = v.y;
+    lr += v.x;
+    lp += v.y;
+  }
+  const float tr = __shfl(wave_incl_scan(lr, lane), 63, 64);
+  // residual summed to zero: sample the target row itself (speculative.py:163-169)
+  const bool use_pt = d.mode == 1 || !(tr > 0.f);
+  const int mode = use_pt ? 1 : 0;
+  const float ls = use_pt ? lp : lr;
+  const float incl = wave_incl_scan(ls, lane);
+  const float excl = __shfl_up(incl, 1, 64);
+  const float tot = __shfl(incl, 63, 64);
+  const float target = u * tot;
+  const uint64_t hitr = __builtin_amdgcn_ballot_w64(ls > 0.f && incl > target);
+  const uint64_t posr = __builtin_amdgcn_ballot_w64(ls > 0.f);
+  if (!posr) {  // degenerate row (no positive weight anywhere)
+    if (lane == 0) p.emitted[(int64_t)b * (p.k + 1) + d.j] = -1;
+    return;
+  }
+  bool fallback = !hitr;
+  const int rsel = hitr ? (int)__builtin_ctzll(hitr) : 63 - (int)__builtin_clzll(posr);
+  // the chosen range's step (sequential, in the order the range was summed)
+  int qs = -1;
+  float acc = lane == 0 ? 0.f : excl;
+  if (lane == rsel) {
+#pragma unroll
+    for (int q = 0; q < kRsMaxSteps; ++q) {
+      const float sq = use_pt ? sp[q] : sr[q];
+      if (qs < 0 && q < ns) {
+        if (!fallback && sq > 0.f && acc + sq > target) qs = q;
+        else acc += sq;
+      }
+    }
+    if (qs < 0) {  // rounding: last positive step of the range
+      fallback = true;
+#pragma unroll
+      for (int q = 0; q < kRsMaxSteps; ++q)
+        if (q < ns && (use_pt ? sp[q] : sr[q]) > 0.f) qs = q;
+    }
+  }
+  qs = __shfl(qs, rsel, 64);
+  acc = __shfl(acc, rsel, 64);
+  fallback = __shfl((int)fallback, rsel, 64) != 0;
+  // recompute that step exactly as resolve_kernel summed it
+  const int v = (rsel * ns + qs) * kRsStep + 8 * lane;
+  StepRaw<T> raw;
+  step_load<T>(p, to, dof, d.mode, v, raw);
+  float wr[8], wp[8], res, pts;
+  step_weights<T>(p, mode, d, v, raw, wr, wp, res, pts);
+  const float run = use_pt ? pts : res;
+  const float* w = use_pt ? wp : wr;
+  const float li = acc + wave_incl_scan(run, lane);
+  const uint64_t hit = fallback ? 0 : __builtin_amdgcn_ballot_w64(run > 0.f && li > target);
+  const uint64_t pos = __builtin_amdgcn_ballot_w64(run > 0.f);
+  const int sel = hit ? (int)__builtin_ctzll(hit) : (pos ? 63 - (int)__builtin_clzll(pos) : 0);
+  if (lane == sel) {
+    float cum = li - run;  // exclusive prefix of this lane
+    int tok = -1, last = -1;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      cum += w[e];
+      if (w[e] > 0.f) {
+        last = v + e;
+        if (tok < 0 && cum > target) tok = v + e;
+      }
+    }
+    p.emitted[(int64_t)b * (p.k + 1) + d.j] = (hit && tok >= 0) ? tok : last;
+  }
+}
+
 struct Layout {
   int rows, nch, cs, nch2, cs2;
-  int64_t stats_off, dec_off, psum_off, total;
+  int64_t stats_off, dec_off, psum_off, rsum_off, total;
 };
 
 Layout layout(int B, int k, int V, bool greedy) {
@@ -690,8 +948,15 @@ Layout layout(int B, int k, int V, bool greedy) {
   L.stats_off = kFlagBytes;
   L.dec_off = L.stats_off + al((int64_t)rows_max * kMaxChunks * 8);
   L.psum_off = L.dec_off + al((int64_t)B * 8 * 4);
-  L.total = L.psum_off + al((int64_t)B * kMaxChunks * 4);
+  L.rsum_off = L.psum_off + al((int64_t)B * kMaxChunks * 4);
+  L.total = L.rsum_off + al((int64_t)B * kRsRanges * kRsMaxSteps * 8);
   return L;
+}
+
+// The two-launch stochastic tail needs whole 8-logit vectors everywhere.
+bool rs_path(const AccParams& p) {
+  return p.V <= kRsMaxV && p.V % 8 == 0 &&
+         (p.t_req | p.t_row | (p.dl ? (p.d_req | p.d_row) : 0)) % 8 == 0;
 }
 
 template <typename T>
@@ -707,6 +972,13 @@ int32_t launch_accept(const AccParams& p, int rows, hipStream_t s) {
   hipLaunchKernelGGL((stats_kernel<T, false>), g1, dim3(kThreads), 0, s, p);
   int32_t rc = launch_status("stats_kernel");
   if (rc) return rc;
+  if (rs_path(p)) {
+    hipLaunchKernelGGL((resolve_kernel<T>), dim3(kRsSplits, p.B), dim3(kRsThreads), 0, s, p);
+    rc = launch_status("resolve_kernel");
+    if (rc) return rc;
+    hipLaunchKernelGGL((select_kernel2<T>), dim3(p.B), dim3(64), 0, s, p);
+    return launch_status("select_kernel");
+  }
   hipLaunchKernelGGL((decide_kernel<T>), dim3(p.B), dim3(64), 0, s, p);
   rc = launch_status("decide_kernel");
   if (rc) return rc;
@@ -800,6 +1072,7 @@ extern "C" int32_t nsg_spec_accept(const void* target_logits, int64_t target_req
   p.stats = reinterpret_cast<float2*>(ws + L.stats_off);
   p.dec = reinterpret_cast<float*>(ws + L.dec_off);
   p.psum = reinterpret_cast<float*>(ws + L.psum_off);
+  p.rsum = reinterpret_cast<float2*>(ws + L.rsum_off);
   // 16-byte vector loads need 16-byte aligned bases; rows are checked per row
   const uintptr_t mis = reinterpret_cast<uintptr_t>(target_logits) |
                         (greedy ? 0 : reinterpret_cast<uintptr_t>(draft_logits));

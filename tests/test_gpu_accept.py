@@ -119,8 +119,9 @@ def test_stochastic_fp32_logits_and_k8():
     _assert_stochastic(n, em, rb, ref)
 
 
-def test_k0_samples_one_token():
-    a = workloads.acceptance_batch(batch=32, k=0, vocab=3001, temperature=0.7, seed=5)
+@pytest.mark.parametrize("vocab", [3001, 3000])   # 3000: the one-launch tail (V % 8 == 0)
+def test_k0_samples_one_token(vocab):
+    a = workloads.acceptance_batch(batch=32, k=0, vocab=vocab, temperature=0.7, seed=5)
     u = _uniforms(32, 0, 5)
     n, em, rb, ref = _run(a, 0.7, u, with_pt=False)
     assert (n == 1).all()

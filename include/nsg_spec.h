@@ -42,7 +42,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 3
+#define NSG_ABI_VERSION 4
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -67,6 +67,7 @@ typedef struct {
   int32_t head_dim;
   int32_t num_qo_heads;
   int32_t num_kv_heads;
+  int32_t kv_groups;       /* KV groups per workgroup (1, or several in the latency regime) */
   int64_t workspace_bytes; /* device workspace nsg_attn_run needs for this plan  */
 } nsg_attn_plan_t;
 

@@ -13,7 +13,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libnsg_spec.so")
 
 NSG_ATTN_WORK_INTS = 8
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 i32, i64, u32, u64, f32 = C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_float
 vp = C.c_void_p
@@ -24,7 +24,7 @@ class AttnPlan(C.Structure):
     _fields_ = [
         ("num_work", i32), ("num_merge", i32), ("num_groups", i32), ("row_tiles", i32), ("q_tile_tokens", i32),
         ("max_splits", i32), ("head_dim", i32), ("num_qo_heads", i32), ("num_kv_heads", i32),
-        ("workspace_bytes", i64),
+        ("kv_groups", i32), ("workspace_bytes", i64),
     ]
 
 

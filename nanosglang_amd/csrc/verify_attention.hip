@@ -40,6 +40,9 @@ namespace {
 
 constexpr int kThreads = 256;         // merge kernel
 constexpr int kMinSplitSteps = 4;     // 32-token steps per KV split, at least
+// ... per KV group in the latency regime, where a split costs a merge launch
+// (~4 us) and a step of a group ~0.35 us
+constexpr int kMinGroupSteps = 8;
 constexpr int kTokIt = 32;           // KV tokens per wave step
 constexpr float kMaskVal = -1.0e30f; // finite "minus infinity" (no inf - inf)
 constexpr int64_t kHeaderBytes = 256;  // flags word + padding
@@ -83,6 +86,23 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
 // and lgkmcnt left at their maxima, i.e. not waited on).
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
+// s_waitcnt until at most `later` ring steps (NI DMA instructions each) of
+// this wave are still in flight.  `later` is a runtime value in [0, L]; each
+// case has its own immediate.  vmcnt counts to 63: a larger count waits for
+// 63, which is only more conservative.
+template <int NI, int L>
+__device__ __forceinline__ void wait_steps(int later) {
+  if constexpr (L == 0) {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  } else {
+    if (later >= L) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(L * NI < 63 ? L * NI : 63));
+      return;
+    }
+    wait_steps<NI, L - 1>(later);
+  }
+}
+
 // LDS tile swizzles: 16-byte chunk c of token row t is stored at physical
 // chunk c ^ swz(t).  K fragments read one logical chunk of 16 consecutive
 // tokens (needs distinct banks across t); V^T fragments read two adjacent
@@ -98,16 +118,27 @@ __device__ __forceinline__ int swz_v(int t) { return 2 * ((t >> 2) & 3); }
 constexpr float kLazyRescale = 8.f;  // rescale O only when a row max grows by > 2^8
 
 constexpr int kNBuf = 4;            // LDS ring depth (steps in flight: kNBuf - 1)
+// KV groups per workgroup in the latency regime: as many 4-deep rings as
+// fit 128 KB of LDS (8 KB per step at head_dim 64, 16 KB at 128).
+constexpr int kv_groups_max(int D) { return D == 64 ? 4 : 2; }
 constexpr int kMaxItemPages = 1024; // page ids one work item may span
 
-// One workgroup = one work item x one KV head; wave w owns query rows
-// [16w, 16w + 16) of the item's query tile.  The item's page ids are staged
-// in LDS once.  K and V rows of each 32-token step go straight from HBM to
-// an LDS ring slot with global_load_lds_dwordx4 (no staging registers), kNBuf
-// - 1 steps ahead of the math; a raw s_barrier plus an explicit vmcnt wait
-// per step keeps the ring full (__syncthreads would drain it).
-template <int D, int RT>
-__global__ __launch_bounds__(RT * 64) void verify_attn_kernel(AttnParams p) {
+// One workgroup = one work item x one KV head.  Its KS * RT waves form KS
+// groups of RT; group g takes the g-th contiguous share of the item's 32-token
+// KV steps, and wave w of a group owns query rows [16w, 16w + 16) of the
+// item's query tile.  KS > 1 is the latency regime (few, short items: the
+// verify and draft steps of a decode batch): the groups run side by side and
+// their partial results meet in LDS, so the item needs neither a second
+// launch nor more sequential steps per wave.
+// The item's page ids are staged in LDS once.  K and V rows of each step go
+// straight from HBM to a ring slot of the group with global_load_lds_dwordx4
+// (no staging registers), kNBuf - 1 steps ahead of the math; an explicit
+// vmcnt wait per step (plus a raw s_barrier when a group has several waves)
+// keeps the ring full (__syncthreads would drain it).  Every group iterates
+// the same number of steps (idle ones do nothing but the barrier), so the
+// workgroup-wide barrier stays matched.
+template <int D, int RT, int KS>
+__global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p) {
   constexpr int KC = D / 32;              // K-dim chunks of QK^T
   constexpr int DT = D / 16;              // d tiles of PV
   constexpr int ROWS = RT * 16;
@@ -117,7 +148,8 @@ __global__ __launch_bounds__(RT * 64) void verify_attn_kernel(AttnParams p) {
   constexpr int TPI = 64 / CPR;           // token rows per DMA instruction
   constexpr int NI = (NINST + RT - 1) / RT;  // DMA instructions per wave per step
   constexpr int PSTRIDE = D + 4;          // partial row: O[D], m, l, 2 pad
-  __shared__ __attribute__((aligned(16))) bf16 ring[kNBuf][2][TILE];
+  constexpr int NTHR = RT * KS * 64;
+  __shared__ __attribute__((aligned(16))) bf16 ring[KS][kNBuf][2][TILE];
   __shared__ int s_pages[kMaxItemPages];
 
   // blockIdx.x = KV head (fastest), so the Hkv workgroups of one work item
@@ -138,14 +170,16 @@ __global__ __launch_bounds__(RT * 64) void verify_attn_kernel(AttnParams p) {
   const int nrows = qn * G;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wid / RT;   // KV group
+  const int wave = wid % RT;  // row tile inside the group
   const int r16 = lane & 15;
   const int g4 = lane >> 4;
 
   // ---- stage the item's page ids in LDS ----
   const int page0 = kvb >> p.log2P;
   const int npages = kve > kvb ? ((kve - 1) >> p.log2P) - page0 + 1 : 0;
-  for (int i = tid; i < npages; i += RT * 64) s_pages[i] = p.kv_indices[pb + page0 + i];
+  for (int i = tid; i < npages; i += NTHR) s_pages[i] = p.kv_indices[pb + page0 + i];
 
   // ---- this lane's query row (B operand of S^T = K Q^T) and causal limit ----
   const int row = wave * 16 + r16;
@@ -170,7 +204,10 @@ __global__ __launch_bounds__(RT * 64) void verify_attn_kernel(AttnParams p) {
 
   const size_t head_off = (size_t)h * D;
   const size_t tok_stride = (size_t)p.Hkv * D;
-  const int n_it = (kve - kvb + kTokIt - 1) / kTokIt;
+  const int n_all = (kve - kvb + kTokIt - 1) / kTokIt;  // steps of the item
+  const int per = (n_all + KS - 1) / KS;                // steps per group (loop count)
+  const int n_it = max(0, min(per, n_all - grp * per)); // this group's real steps
+  const int gkvb = kvb + grp * per * kTokIt;            // this group's first token
   bool bad_page = false;
   // Dummy source for lanes past the item's end or with a bad page id: the
   // item's first token row (real, finite data); its value is masked out.
@@ -190,24 +227,37 @@ __global__ __launch_bounds__(RT * 64) void verify_attn_kernel(AttnParams p) {
   for (int dt = 0; dt < DT; ++dt)
     voff[dt] = 4 * g4 * D + (((2 * dt + (r16 >> 3)) ^ (2 * g4)) * 8) + (r16 & 7);
 
+  // Loop-invariant parts of this lane's DMA copies: token row inside the
+  // step, source offset inside the token's head slice, and LDS destination.
+  int d_t[NI];
+  int d_off[NI];
+  int d_lds[NI];
+  bool d_v[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int j = (wave + RT * i) % NINST;      // padding repeats a real copy
+    const int which = j / (NINST / 2);
+    const int jj = j - which * (NINST / 2);
+    const int t = jj * TPI + lane / CPR;        // token row inside the step
+    const int pc = lane % CPR;                   // physical chunk written by this lane
+    const int lc = pc ^ (which ? swz_v(t) : swz_k<D>(t));  // logical chunk it carries
+    d_t[i] = t;
+    d_off[i] = lc * 8;
+    d_lds[i] = which * TILE + jj * TPI * D;
+    d_v[i] = which != 0;
+  }
   // Issue this wave's DMA instructions for step `it` into ring slot `slot`.
   auto issue = [&](int it, int slot) {
-    const int t0 = kvb + it * kTokIt;
+    const int t0 = gkvb + it * kTokIt;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int j = (wave + RT * i) % NINST;      // padding repeats a real copy
-      const int which = j / (NINST / 2);
-      const int jj = j - which * (NINST / 2);
-      const int t = jj * TPI + lane / CPR;        // token row inside the step
-      const int pc = lane % CPR;                   // physical chunk written by this lane
-      const int lc = pc ^ (which ? swz_v(t) : swz_k<D>(t));  // logical chunk it carries
-      const int tok = t0 + t;
-      const bf16* src = which ? dummy_v : dummy_k;
+      const int tok = t0 + d_t[i];
+      const bf16* src = d_v[i] ? dummy_v : dummy_k;
       if (tok < kve) {
         const int page = s_pages[(tok >> p.log2P) - page0];
         if ((unsigned)page < (unsigned)p.num_pages) {
-          src = (which ? p.vc : p.kc) + ((size_t)page * P + (tok & (P - 1))) * tok_stride +
-                head_off + lc * 8;
+          src = (d_v[i] ? p.vc : p.kc) + ((size_t)page * P + (tok & (P - 1))) * tok_stride +
+                head_off + d_off[i];
         } else {
           bad_page = true;
         }
@@ -215,7 +265,8 @@ __global__ __launch_bounds__(RT * 64) void verify_attn_kernel(AttnParams p) {
       // void* operands: with typed pointers the host pass silently drops the
       // kernel stubs of this template
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
-                                       static_cast<void*>(&ring[slot][which][jj * TPI * D]), 16, 0, 0);
+                                       static_cast<void*>(&ring[grp][slot][0][0] + d_lds[i]), 16,
+                                       0, 0);
     }
   };
 
@@ -223,31 +274,31 @@ __global__ __launch_bounds__(RT * 64) void verify_attn_kernel(AttnParams p) {
   for (int it = 0; it < kNBuf - 1; ++it)
     if (it < n_it) issue(it, it);
 
-  for (int it0 = 0; it0 < n_it; it0 += kNBuf) {
+  for (int it0 = 0; it0 < per; it0 += kNBuf) {
 #pragma unroll
     for (int slot = 0; slot < kNBuf; ++slot) {  // unrolled: ring slot is a constant
       const int it = it0 + slot;
-      if (it >= n_it) break;
-      // steps issued after `it` by this wave: min(kNBuf - 2, n_it - 1 - it)
-      const int later = min(kNBuf - 2, n_it - 1 - it);
-      if (later >= 2) {
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * NI));
-      } else if (later == 1) {
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(NI));
-      } else {
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      if (it >= per) break;
+      const bool real = it < n_it;
+      if (real) {
+        // steps issued after `it` by this wave: min(kNBuf - 2, n_it - 1 - it)
+        wait_steps<NI, kNBuf - 2>(min(kNBuf - 2, n_it - 1 - it));
       }
-      // step `it` landed for every wave and slot (it - 1) is free; the empty
-      // asm statements keep the compiler from moving LDS accesses across the
-      // raw barrier (which, unlike __syncthreads, does not drain the ring)
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
+      if constexpr (RT > 1) {
+        // step `it` landed for every wave of the group and slot (it - 1) is
+        // free; the empty asm statements keep the compiler from moving LDS
+        // accesses across the raw barrier (which, unlike __syncthreads, does
+        // not drain the ring)
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+      }
       if (it + kNBuf - 1 < n_it) issue(it + kNBuf - 1, (slot + kNBuf - 1) % kNBuf);
+      if (!real) continue;
 
-      const int t0 = kvb + it * kTokIt;
-      const bf16* Kt = ring[slot][0];
-      const uint16_t* Vt = reinterpret_cast<const uint16_t*>(ring[slot][1]);
+      const int t0 = gkvb + it * kTokIt;
+      const bf16* Kt = ring[grp][slot][0];
+      const uint16_t* Vt = reinterpret_cast<const uint16_t*>(ring[grp][slot][1]);
 
       // ---- S^T = K Q^T: lane holds tokens 16s + 4*g4 + i of query row r16 ----
       floatx4 sacc[2];
@@ -316,10 +367,43 @@ __global__ __launch_bounds__(RT * 64) void verify_attn_kernel(AttnParams p) {
   }
 
   if (bad_page) atomicOr(p.flags, 1);
-  // ---- finish: the 4 lane groups sharing query row r16 hold partial sums ----
+  // ---- the 4 lane groups sharing query row r16 hold partial sums ----
   float l = l_run;
   l += __shfl_xor(l, 16, 64);
   l += __shfl_xor(l, 32, 64);
+  if constexpr (KS > 1) {
+    // ---- combine the KV groups through LDS (the rings are idle: every
+    //      group's last real step waited for all of its copies) ----
+    constexpr int SROW = D + 4;  // O[D], m, l, 2 pad
+    float* sc = reinterpret_cast<float*>(&ring[0][0][0][0]);
+    static_assert((size_t)KS * ROWS * SROW * 4 <= sizeof(ring), "combine scratch fits the rings");
+    __syncthreads();
+    float* mine = sc + ((size_t)grp * ROWS + row) * SROW;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<floatx4*>(mine + dt * 16 + 4 * g4) = oacc[dt];
+    if (g4 == 0) {
+      mine[D] = m_run;
+      mine[D + 1] = l;
+    }
+    __syncthreads();
+    if (grp != 0) return;
+    float M = kMaskVal;
+#pragma unroll
+    for (int g = 0; g < KS; ++g) M = fmaxf(M, sc[((size_t)g * ROWS + row) * SROW + D]);
+    l = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) oacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < KS; ++g) {
+      const float* o = sc + ((size_t)g * ROWS + row) * SROW;
+      const float wgt = __builtin_amdgcn_exp2f(o[D] - M);
+      l += wgt * o[D + 1];
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        oacc[dt] += wgt * *reinterpret_cast<const floatx4*>(o + dt * 16 + 4 * g4);
+    }
+    m_run = M;
+  }
   if (!row_ok) return;
   if (nsplit == 1) {
     const float inv = l > 0.f ? 1.f / l : 0.f;
@@ -399,8 +483,16 @@ __global__ __launch_bounds__(kThreads) void verify_merge_kernel(AttnParams p, co
 template <int D, int RT>
 int32_t launch_rt(const nsg_attn_plan_t* plan, const AttnParams& prm, const int* merge,
                   hipStream_t stream) {
-  hipLaunchKernelGGL((verify_attn_kernel<D, RT>), dim3(plan->num_kv_heads, plan->num_work),
-                     dim3(RT * 64), 0, stream, prm);
+  const dim3 grid(plan->num_kv_heads, plan->num_work);
+  constexpr int KSX = kv_groups_max(D);
+  if (plan->kv_groups == KSX) {
+    hipLaunchKernelGGL((verify_attn_kernel<D, RT, KSX>), grid, dim3(RT * KSX * 64), 0, stream, prm);
+  } else if (plan->kv_groups == 1) {
+    hipLaunchKernelGGL((verify_attn_kernel<D, RT, 1>), grid, dim3(RT * 64), 0, stream, prm);
+  } else {
+    set_error("kv_groups %d not supported for head_dim %d", plan->kv_groups, D);
+    return NSG_ERR_ARG;
+  }
   int32_t rc = launch_status("verify_attn_kernel");
   if (rc || plan->num_merge == 0) return rc;
   hipLaunchKernelGGL((verify_merge_kernel<D, RT>), dim3(plan->num_merge, plan->num_kv_heads),
@@ -447,12 +539,19 @@ int q_tile_tokens(int G, int max_ql) { return std::max(1, std::min(64 / G, max_q
 // `max_ql` query tokens fits: the split size is chosen so that the KV steps
 // make at most target_items items, plus at most one rounding item per
 // (request, query tile) group; every group needs at most one merge item.
+// Work items the KV split aims for: with one KV group a workgroup is small
+// (kTargetWgPerCu fit a CU); with several (latency regime) it holds 128 KB of
+// LDS and a CU runs one.
+long long target_items(int kv_groups, int num_cus, int num_kv_heads) {
+  return std::max(1, (kv_groups > 1 ? num_cus : num_cus * kTargetWgPerCu) / num_kv_heads);
+}
+
+// Graph-captured plans are decode / verify steps: the latency regime, fixed.
 void fixed_capacity(int batch, int max_ql, int G, int num_kv_heads, int num_cus,
                     int* max_work, int* max_merge) {
   const int T = q_tile_tokens(G, max_ql);
   const int groups = batch * ((std::max(1, max_ql) + T - 1) / T);
-  const int target_items = std::max(1, num_cus * kTargetWgPerCu / num_kv_heads);
-  *max_work = target_items + groups;
+  *max_work = (int)target_items(2, num_cus, num_kv_heads) + groups;
   *max_merge = groups;
 }
 
@@ -523,11 +622,17 @@ int32_t plan_impl(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
       total_it += (kv_end + kTokIt - 1) / kTokIt;
     }
   }
-  const long long target_items = std::max(1, num_cus * kTargetWgPerCu / num_kv_heads);
-  // a split is at least kMinSplitSteps steps: its partial rows cost about as
-  // much traffic as one step of K and V
-  long long chunk_it =
-      std::max<long long>(kMinSplitSteps, (total_it + target_items - 1) / target_items);
+  // KV groups: several per workgroup when even minimum-length items cannot
+  // fill the GPU (the latency regime), one otherwise; graph-captured plans
+  // always take the latency shape.  A split is at least kMinSplitSteps steps
+  // per group: its partial rows cost about as much traffic as one step of K
+  // and V.
+  const long long t1 = target_items(1, num_cus, num_kv_heads);
+  const bool latency = fixed_work >= 0 || (total_it + t1 - 1) / t1 <= kMinSplitSteps;
+  const int KS = latency ? kv_groups_max(head_dim) : 1;
+  const long long tgt = target_items(KS, num_cus, num_kv_heads);
+  long long chunk_it = std::max<long long>(
+      (long long)(KS > 1 ? kMinGroupSteps : kMinSplitSteps) * KS, (total_it + tgt - 1) / tgt);
   // a work item's page ids must fit the kernel's LDS list (kMaxItemPages)
   const long long max_chunk_it =
       std::max<long long>(1, ((long long)(kMaxItemPages - 2) * page_size) / kTokIt);
@@ -596,6 +701,7 @@ int32_t plan_impl(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
   plan->head_dim = head_dim;
   plan->num_qo_heads = num_qo_heads;
   plan->num_kv_heads = num_kv_heads;
+  plan->kv_groups = KS;
   plan->workspace_bytes =
       kHeaderBytes + (int64_t)n_work * num_kv_heads * RT * 16 * (head_dim + 4) * 4;
   clear_error();

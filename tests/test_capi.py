@@ -44,16 +44,9 @@ def _plan(lib, q_lens, kv_lens, Hq=14, Hkv=2, D=64, P=16, causal=1, cus=256):
     return rc, pl, work.reshape(cap, NSG_ATTN_WORK_INTS), qo, kvp
 
 
-@pytest.mark.parametrize("cus", [1, 256])
-def test_planner_covers_every_query_row_and_kv_token_once(lib, cus):
-    rng = np.random.default_rng(0)
-    q_lens = [5] * 20 + [1, 300, 17]
-    kv_lens = list(rng.integers(100, 641, 20)) + [50, 300, 17]
-    rc, pl, work, qo, kvp = _plan(lib, q_lens, kv_lens, cus=cus)
-    assert rc == 0
-    items = work[:pl.num_work]
-    merges = work[pl.num_work:pl.num_work + pl.num_merge]
-    G = 7
+def _check_cover(pl, items, merges, q_lens, kv_lens, qo, kvp, G=7):
+    """Every query row in exactly one tile; each tile's KV range [0, end)
+    tiled exactly by its splits; merge items point at their splits."""
     T = pl.q_tile_tokens
     assert pl.row_tiles == (T * G + 15) // 16 and T * G <= 64
     seen_q = np.zeros(qo[-1], int)
@@ -78,7 +71,28 @@ def test_planner_covers_every_query_row_and_kv_token_once(lib, cus):
                 first = m[0, 2]
                 assert (items[first:first + len(its), 0] == qs).all()
     assert (seen_q == 1).all()
+
+
+@pytest.mark.parametrize("cus", [1, 256])
+def test_planner_covers_every_query_row_and_kv_token_once(lib, cus):
+    rng = np.random.default_rng(0)
+    q_lens = [5] * 20 + [1, 300, 17]
+    kv_lens = list(rng.integers(100, 641, 20)) + [50, 300, 17]
+    rc, pl, work, qo, kvp = _plan(lib, q_lens, kv_lens, cus=cus)
+    assert rc == 0
+    _check_cover(pl, work[:pl.num_work], work[pl.num_work:pl.num_work + pl.num_merge], q_lens,
+                 kv_lens, qo, kvp)
     assert pl.workspace_bytes >= 256 + pl.num_work * 2 * pl.row_tiles * 16 * (64 + 4) * 4
+
+
+def test_planner_kv_groups_follow_the_work_size(lib):
+    """Latency regime (few short items) -> several KV groups per workgroup;
+    long contexts -> one, with more work items."""
+    rc, small, _, _, _ = _plan(lib, [5] * 32, [370] * 32)
+    rc2, big, _, _, _ = _plan(lib, [9] * 64, [5000] * 64, Hq=32, Hkv=8, D=128)
+    assert rc == rc2 == 0
+    assert small.kv_groups == 4 and small.num_merge == 0
+    assert big.kv_groups == 1 and big.num_work >= 256
 
 
 def _plan_fixed(lib, q_lens, kv_lens, batch_cap, max_q, Hq=14, Hkv=2, D=64, P=16, cus=256):
@@ -106,7 +120,9 @@ def test_fixed_plan_pads_to_a_constant_grid(lib, q, B):
     rng = np.random.default_rng(q * 100 + B)
     shapes = set()
     for step in range(6):
-        kv_lens = list(rng.integers(q, 700 * (step + 1), B))
+        # decode / verify contexts: the latency regime, where the dynamic
+        # planner takes the same shape the graph does
+        kv_lens = list(rng.integers(q, 180 * (step + 1), B))
         rc, pl, work, (mw, mm) = _plan_fixed(lib, [q] * B, kv_lens, B, q)
         assert rc == 0, lib.nsg_last_error()
         shapes.add((pl.num_work, pl.num_merge, pl.row_tiles, pl.q_tile_tokens,
@@ -114,12 +130,25 @@ def test_fixed_plan_pads_to_a_constant_grid(lib, q, B):
         assert (pl.num_work, pl.num_merge) == (mw, mm)
         rc2, pd, wd, _, _ = _plan(lib, [q] * B, kv_lens)
         assert rc2 == 0
+        assert pd.kv_groups == pl.kv_groups > 1
         n, m = pd.num_work, pd.num_merge
         assert np.array_equal(work[:n], wd[:n])                       # real work items
         assert (work[n:mw] == 0).all()                                # empty work items
         assert np.array_equal(work[mw:mw + m], wd[n:n + m])           # real merge items
         assert (work[mw + m:] == 0).all()                             # empty merge items
     assert len(shapes) == 1
+
+
+def test_fixed_plan_covers_long_contexts(lib):
+    rng = np.random.default_rng(3)
+    kv_lens = list(rng.integers(2000, 8000, 16))
+    rc, pl, work, (mw, mm) = _plan_fixed(lib, [5] * 16, kv_lens, 16, 5)
+    assert rc == 0, lib.nsg_last_error()
+    qo = np.concatenate([[0], np.cumsum([5] * 16)]).astype(np.int32)
+    kvp = np.concatenate([[0], np.cumsum([(L + 15) // 16 for L in kv_lens])]).astype(np.int32)
+    items = work[:mw][work[:mw, 1] > 0]
+    merges = work[mw:][work[mw:, 3] > 1]
+    _check_cover(pl, items, merges, [5] * 16, kv_lens, qo, kvp)
 
 
 def test_fixed_plan_keeps_tile_shape_and_rejects_longer_queries(lib):

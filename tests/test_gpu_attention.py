@@ -46,7 +46,7 @@ def _check(c, Hq, Hkv, D, causal=True, **kw):
     ref = _oracle(c, causal)
     err = np.abs(got - ref).max()
     print(f"  max abs err {err:.3e}  |ref| max {np.abs(ref).max():.3e}  "
-          f"work={plan.num_work} splits<={plan.max_splits} rt={plan.row_tiles}", flush=True)
+          f"work={plan.num_work} splits<={plan.max_splits} rt={plan.row_tiles} ks={plan.kv_groups}", flush=True)
     assert flags == 0
     assert np.isfinite(got).all()
     assert err <= TOL_SPEC
@@ -62,7 +62,22 @@ def test_verify_c2_shape_small_pool():
 def test_verify_c2_full():
     c = workloads.verify_attention_batch(seed=0)   # 32 x 5 queries, 14/2 heads, D=64
     plan = _check(c, 14, 2, 64)
-    assert plan.max_splits > 1   # exercises the cross-split merge
+    # the latency regime: four KV groups per workgroup, one launch, no merge
+    assert plan.kv_groups == 4 and plan.max_splits == 1 and plan.num_merge == 0
+
+
+def test_latency_regime_long_contexts_split_and_merge():
+    c = workloads.verify_attention_batch(batch=3, min_len=2000, max_len=3000, num_pages=600,
+                                         seed=12)
+    plan = _check(c, 14, 2, 64)
+    assert plan.kv_groups == 4 and plan.max_splits > 1   # KV groups and cross-split merge
+
+
+def test_throughput_regime_split_and_merge():
+    c = workloads.verify_attention_batch(batch=32, min_len=4000, max_len=4400, num_pages=9000,
+                                         seed=13)
+    plan = _check(c, 14, 2, 64)
+    assert plan.kv_groups == 1 and plan.max_splits > 1
 
 
 def test_verify_c2_single_split():
@@ -74,7 +89,8 @@ def test_verify_large_shape_d128():
     c = workloads.verify_attention_batch(batch=6, q_len=9, num_qo_heads=32, num_kv_heads=8,
                                          head_dim=128, min_len=2048, max_len=4096,
                                          num_pages=1600, seed=3)
-    _check(c, 32, 8, 128)
+    plan = _check(c, 32, 8, 128)
+    assert plan.kv_groups == 2 and plan.max_splits > 1
 
 
 def test_decode_q1():

@@ -104,7 +104,8 @@ def bench_verify_attention(torch, w, dev, reps=160, pools=16, shape=None):
         flops += 4 * Hq * D * sum(L - ql + r + 1 for r in range(ql))
     del ks, vs
     return {"us": t, "bytes": nbytes, "gbs": nbytes / t / 1e3, "flops": flops,
-            "work_items": pi.num_work, "merge_items": pi.num_merge, "pools_rotated": pools}
+            "work_items": pi.num_work, "merge_items": pi.num_merge, "kv_groups": pi.kv_groups,
+            "row_tiles": pi.row_tiles, "pools_rotated": pools}
 
 
 def bench_acceptance(torch, dev, greedy, sets=3, reps=60, **kw):
@@ -129,6 +130,56 @@ def bench_acceptance(torch, dev, greedy, sets=3, reps=60, **kw):
     t = graph_time_us(torch, call, reps)
     nbytes = workloads.algorithmic_bytes_acceptance(B, k, V, greedy)
     return {"us": t, "bytes": nbytes, "gbs": nbytes / t / 1e3, "sets_rotated": sets}
+
+
+def pmc_probe(torch):
+    """Dispatches whose HBM counters calibrate and measure traffic: a plain
+    copy of COPY_BYTES (read COPY_BYTES, write COPY_BYTES), then the
+    verify-shape attention launches on rotated pools (as in the bench)."""
+    from nanosglang_amd import workloads
+    from nanosglang_amd.kernels import BatchPrefillWithPagedKVCacheWrapper
+    dev = torch.device("cuda", 0)
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    c = workloads.verify_attention_batch(seed=0)
+    k0 = torch.from_numpy(c["k"]).to(dev).bfloat16()
+    v0 = torch.from_numpy(c["v"]).to(dev).bfloat16()
+    pools = 16
+    ks = [k0] + [k0.clone() for _ in range(pools - 1)]
+    vs = [v0] + [v0.clone() for _ in range(pools - 1)]
+    q = torch.from_numpy(c["q"]).to(dev).bfloat16()
+    ws = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    wr = BatchPrefillWithPagedKVCacheWrapper(ws)
+    wr.plan(c["qo_indptr"], c["kv_indptr"], c["kv_indices"], c["kv_last_page_len"], 14, 2, 64,
+            c["page_size"])
+    out = torch.empty_like(q)
+    torch.cuda.synchronize()
+    for i in range(10):
+        wr.run(q, (ks[i % pools], vs[i % pools]), out=out)
+    torch.cuda.synchronize()
+    nbytes = workloads.algorithmic_bytes_verify_attention(
+        c["kv_lens"], c["qo_indptr"][-1], 14, 2, 64, len(c["kv_lens"]), c["kv_indptr"][-1])
+    print(json.dumps({"copy_bytes": COPY_BYTES, "attention_launches": 10,
+                      "attention_algorithmic_bytes": nbytes}), flush=True)
+
+
+COPY_BYTES = 256 << 20
+
+
+def traffic_bytes():
+    """HBM bytes per verify-attention launch at the verify shape, from the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes recorded in
+    profiles/verify_attention_traffic.json (each scaled by a plain copy kernel
+    of known size); None when that record is absent."""
+    p = os.path.join(ROOT, "profiles", "verify_attention_traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f).get("traffic_bytes_per_launch")
 
 
 def cpu_baseline(prompts, outs, n_tokens=48):
@@ -163,6 +214,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-kernels", action="store_true")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="only a 256 MiB device copy (3x) and 10 verify-attention launches at "
+                         "the verify shape, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the verify "
@@ -171,6 +225,9 @@ def main():
 
     import torch
     sys.path.insert(0, ROOT)
+    if args.pmc_probe:
+        pmc_probe(torch)
+        return
     from nanosglang_amd.engine.spec_engine import SpecEngine
     from nanosglang_amd.model.causal_lm import CausalLM, ModelConfig
 
@@ -223,11 +280,13 @@ def main():
     if not args.skip_kernels:
         va = bench_verify_attention(torch, None, dev)
         log(f"verify attention (verify shape): {va}")
+        launches = ("verify_attn_kernel" + (" + verify_merge_kernel" if va["merge_items"] else ""))
         result["roofline"] = {
             "bound": "hbm", "achieved": round(va["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(va["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "verify attention (verify_attn_kernel + verify_merge_kernel), batch 32, "
-                      "5 query tokens, 14/2 heads, D 64",
+            "frac": round(va["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic_bytes(),
+            "kernel": f"verify attention ({launches}; {va['work_items']} work items x 2 KV heads, "
+                      f"{va['kv_groups']} KV groups of {va['row_tiles']} waves per workgroup), "
+                      f"batch 32, 5 query tokens, 14/2 heads, D 64",
             "us_per_launch": round(va["us"], 2), "algorithmic_bytes": va["bytes"]}
         acc_s = bench_acceptance(torch, dev, greedy=False)
         log(f"acceptance stochastic: {acc_s}")

@@ -42,7 +42,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 4
+#define NSG_ABI_VERSION 5
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -94,16 +94,20 @@ int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
  * are empty and cost one early-exiting workgroup each), and the tile shape
  * follows max_q_len, so nsg_attn_run launches the same grid with the same
  * arguments for every such plan.  A plan that does not fit returns
- * NSG_ERR_WORKSPACE. */
+ * NSG_ERR_WORKSPACE.  With max_kv_len > 0 (at most 1022 pages) no request's
+ * KV range is split: the list holds one work item per query tile, no merge
+ * items, and nsg_attn_run launches no merge pass; a longer request is an
+ * argument error. */
 int32_t nsg_attn_fixed_capacity(int32_t batch, int32_t max_q_len, int32_t num_qo_heads,
-                                int32_t num_kv_heads, int32_t num_cus, int32_t* max_work,
-                                int32_t* max_merge);
+                                int32_t num_kv_heads, int32_t num_cus, int32_t max_kv_len,
+                                int32_t* max_work, int32_t* max_merge);
 int32_t nsg_attn_plan_fixed(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
                             const int32_t* kv_last_page_len_h, int32_t batch,
                             int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                             int32_t page_size, int32_t causal, int32_t num_cus,
-                            int32_t max_q_len, int32_t max_work, int32_t max_merge,
-                            int32_t* work_h, int32_t work_capacity, nsg_attn_plan_t* plan);
+                            int32_t max_q_len, int32_t max_kv_len, int32_t max_work,
+                            int32_t max_merge, int32_t* work_h, int32_t work_capacity,
+                            nsg_attn_plan_t* plan);
 
 /* Bytes of device workspace nsg_attn_run needs for this plan (split partials
  * and an error-flag word, which should start at zero). */

@@ -13,7 +13,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libnsg_spec.so")
 
 NSG_ATTN_WORK_INTS = 8
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 i32, i64, u32, u64, f32 = C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_float
 vp = C.c_void_p
@@ -34,9 +34,10 @@ SIGNATURES = {
     "nsg_abi_version": (i32, []),
     "nsg_attn_plan": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, i32,
                             C.POINTER(AttnPlan)]),
-    "nsg_attn_fixed_capacity": (i32, [i32, i32, i32, i32, i32, C.POINTER(i32), C.POINTER(i32)]),
+    "nsg_attn_fixed_capacity": (i32, [i32, i32, i32, i32, i32, i32, C.POINTER(i32),
+                                      C.POINTER(i32)]),
     "nsg_attn_plan_fixed": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, i32, i32,
-                                  vp, i32, C.POINTER(AttnPlan)]),
+                                  i32, vp, i32, C.POINTER(AttnPlan)]),
     "nsg_attn_workspace_bytes": (i64, [C.POINTER(AttnPlan)]),
     "nsg_linear_max_rows": (i32, []),
     "nsg_linear_preferred": (i32, [i32, i32, i32]),

@@ -547,10 +547,17 @@ long long target_items(int kv_groups, int num_cus, int num_kv_heads) {
 }
 
 // Graph-captured plans are decode / verify steps: the latency regime, fixed.
-void fixed_capacity(int batch, int max_ql, int G, int num_kv_heads, int num_cus,
+// With a KV-length bound (max_kv_len > 0) they never split a query tile's KV
+// range: one work item per tile and no merge launch at all.
+void fixed_capacity(int batch, int max_ql, int G, int num_kv_heads, int num_cus, int max_kv_len,
                     int* max_work, int* max_merge) {
   const int T = q_tile_tokens(G, max_ql);
   const int groups = batch * ((std::max(1, max_ql) + T - 1) / T);
+  if (max_kv_len > 0) {
+    *max_work = groups;
+    *max_merge = 0;
+    return;
+  }
   *max_work = (int)target_items(2, num_cus, num_kv_heads) + groups;
   *max_merge = groups;
 }
@@ -564,7 +571,8 @@ int32_t plan_impl(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
                   const int32_t* kv_last_page_len_h, int32_t batch, int32_t num_qo_heads,
                   int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int32_t causal,
                   int32_t num_cus, int32_t* work_h, int32_t work_capacity, int32_t fixed_work,
-                  int32_t fixed_merge, int32_t fixed_q_len, nsg_attn_plan_t* plan) {
+                  int32_t fixed_merge, int32_t fixed_q_len, int32_t fixed_kv_len,
+                  nsg_attn_plan_t* plan) {
   NSG_CHECK_ARG(plan && qo_indptr_h && kv_indptr_h && kv_last_page_len_h, "null argument");
   NSG_CHECK_ARG(batch >= 0, "batch %d < 0", batch);
   NSG_CHECK_ARG(num_kv_heads > 0 && num_qo_heads > 0 && num_qo_heads % num_kv_heads == 0,
@@ -614,6 +622,8 @@ int32_t plan_impl(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
     const int np = kv_indptr_h[b + 1] - kv_indptr_h[b];
     const int L = np > 0 ? (np - 1) * page_size + kv_last_page_len_h[b] : 0;
     NSG_CHECK_ARG(L >= 1, "request %d has %d query tokens but an empty KV range", b, ql);
+    NSG_CHECK_ARG(fixed_kv_len <= 0 || L <= fixed_kv_len,
+                  "request %d: kv length %d exceeds the fixed plan's bound %d", b, L, fixed_kv_len);
     NSG_CHECK_ARG(!causal || L >= ql, "request %d: kv length %d < query length %d", b, L, ql);
     for (int qb = 0; qb < ql; qb += T) {
       const int qn = std::min(T, ql - qb);
@@ -637,6 +647,7 @@ int32_t plan_impl(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
   const long long max_chunk_it =
       std::max<long long>(1, ((long long)(kMaxItemPages - 2) * page_size) / kTokIt);
   chunk_it = std::min(chunk_it, max_chunk_it);
+  if (fixed_kv_len > 0) chunk_it = std::max<long long>(chunk_it, (fixed_kv_len + kTokIt - 1) / kTokIt);
 
   int n = 0, max_splits = 0, n_merge = 0;
   std::vector<int> split_counts(groups.size());
@@ -718,13 +729,13 @@ extern "C" int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_i
                                  int32_t* work_h, int32_t work_capacity, nsg_attn_plan_t* plan) {
   return plan_impl(qo_indptr_h, kv_indptr_h, kv_last_page_len_h, batch, num_qo_heads,
                    num_kv_heads, head_dim, page_size, causal, num_cus, work_h, work_capacity,
-                   -1, 0, 0, plan);
+                   -1, 0, 0, 0, plan);
 }
 
 extern "C" int32_t nsg_attn_fixed_capacity(int32_t batch, int32_t max_q_len,
                                            int32_t num_qo_heads, int32_t num_kv_heads,
-                                           int32_t num_cus, int32_t* max_work,
-                                           int32_t* max_merge) {
+                                           int32_t num_cus, int32_t max_kv_len,
+                                           int32_t* max_work, int32_t* max_merge) {
   NSG_CHECK_ARG(max_work && max_merge, "null argument");
   NSG_CHECK_ARG(batch >= 1 && max_q_len >= 1, "batch %d and max_q_len %d must be >= 1", batch,
                 max_q_len);
@@ -732,8 +743,8 @@ extern "C" int32_t nsg_attn_fixed_capacity(int32_t batch, int32_t max_q_len,
                     num_qo_heads / num_kv_heads <= 64,
                 "num_qo_heads %d / num_kv_heads %d", num_qo_heads, num_kv_heads);
   if (num_cus <= 0) num_cus = 256;
-  fixed_capacity(batch, max_q_len, num_qo_heads / num_kv_heads, num_kv_heads, num_cus, max_work,
-                 max_merge);
+  fixed_capacity(batch, max_q_len, num_qo_heads / num_kv_heads, num_kv_heads, num_cus,
+                 max_kv_len, max_work, max_merge);
   clear_error();
   return NSG_OK;
 }
@@ -742,14 +753,17 @@ extern "C" int32_t nsg_attn_plan_fixed(const int32_t* qo_indptr_h, const int32_t
                                        const int32_t* kv_last_page_len_h, int32_t batch,
                                        int32_t num_qo_heads, int32_t num_kv_heads,
                                        int32_t head_dim, int32_t page_size, int32_t causal,
-                                       int32_t num_cus, int32_t max_q_len, int32_t max_work,
-                                       int32_t max_merge, int32_t* work_h,
+                                       int32_t num_cus, int32_t max_q_len, int32_t max_kv_len,
+                                       int32_t max_work, int32_t max_merge, int32_t* work_h,
                                        int32_t work_capacity, nsg_attn_plan_t* plan) {
   NSG_CHECK_ARG(max_q_len >= 1 && max_work >= 1 && max_merge >= 0,
                 "max_q_len %d, max_work %d, max_merge %d", max_q_len, max_work, max_merge);
+  NSG_CHECK_ARG(page_size > 0 && max_kv_len <= (kMaxItemPages - 2) * page_size,
+                "max_kv_len %d exceeds one work item's page list (%d tokens)", max_kv_len,
+                (kMaxItemPages - 2) * page_size);
   return plan_impl(qo_indptr_h, kv_indptr_h, kv_last_page_len_h, batch, num_qo_heads,
                    num_kv_heads, head_dim, page_size, causal, num_cus, work_h, work_capacity,
-                   max_work, max_merge, max_q_len, plan);
+                   max_work, max_merge, max_q_len, max_kv_len, plan);
 }
 
 extern "C" int32_t nsg_attn_run(const nsg_attn_plan_t* plan, const int32_t* work_d,

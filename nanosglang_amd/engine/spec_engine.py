@@ -115,7 +115,8 @@ class _StepGraph:
             ql = 1 if a < k else k + 1
             mw, mm = kernels.C.c_int32(0), kernels.C.c_int32(0)
             kernels.check(lib.nsg_attn_fixed_capacity(bs, ql, Hq, Hkv, kernels.MI355X_CUS,
-                                                      kernels.C.byref(mw), kernels.C.byref(mm)),
+                                                      eng.max_kv_len, kernels.C.byref(mw),
+                                                      kernels.C.byref(mm)),
                           "nsg_attn_fixed_capacity")
             nw = (mw.value + mm.value) * kernels.NSG_ATTN_WORK_INTS
             caps.append(ql)
@@ -131,7 +132,7 @@ class _StepGraph:
                 eng.attn_ws, "NHD", use_cuda_graph=True, qo_indptr_buf=A.d[f"qo{a}"],
                 paged_kv_indptr_buf=A.d[f"kvp{a}"], paged_kv_indices_buf=A.d[f"idx{a}"],
                 paged_kv_last_page_len_buf=A.d[f"last{a}"], work_buf=A.d[f"work{a}"],
-                host_bufs=hb, max_q_len=caps[a]))
+                host_bufs=hb, max_q_len=caps[a], max_kv_len=eng.max_kv_len))
         V = c.vocab_size
         self.drafts = torch.zeros(bs, k, dtype=torch.int64, device=dev)
         self.vids = torch.zeros(bs, k + 1, dtype=torch.int64, device=dev)
@@ -178,6 +179,9 @@ class SpecEngine:
         self._graphs: dict[int, _StepGraph] = {}
         self._accept_ws = kernels.AcceptWorkspace(self.device)
         self._dummy_block = None
+        # decode / verify contexts never exceed the position table: the
+        # captured attention plans need no KV split (and no merge launch)
+        self.max_kv_len = min(c.max_position_embeddings, 1022 * block_size)
 
     # ---- helpers ----
     def _uniforms(self, stream: int, n: int) -> torch.Tensor:

@@ -82,14 +82,17 @@ class BatchPrefillWithPagedKVCacheWrapper:
                  paged_kv_indices_buf: torch.Tensor | None = None,
                  paged_kv_last_page_len_buf: torch.Tensor | None = None,
                  num_cus: int = MI355X_CUS, work_buf: torch.Tensor | None = None,
-                 host_bufs: dict | None = None, max_q_len: int | None = None):
+                 host_bufs: dict | None = None, max_q_len: int | None = None,
+                 max_kv_len: int = 0):
         """``use_cuda_graph=True`` with the four ``*_buf`` int32 device tensors
         is the reference's graph mode (engine.py:121-133): ``plan`` rewrites
         those fixed-address buffers and a fixed-size work list (``work_buf``,
         allocated at the first plan if not given), so a graph captured around
         ``run`` replays correctly after each re-plan.  The batch is
         ``len(qo_indptr_buf) - 1``; the tile shape follows ``max_q_len``
-        (default: the first plan's longest query).  With ``host_bufs`` (numpy
+        (default: the first plan's longest query); ``max_kv_len`` > 0 bounds every
+        request's KV length so that plans never split it (no merge launch).
+        With ``host_bufs`` (numpy
         mirrors keyed qo_indptr / kv_indptr / kv_indices / kv_last / work),
         ``plan`` writes only the mirrors and the caller uploads them."""
         if kv_layout != "NHD":
@@ -124,6 +127,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
             self._gbufs = bufs
             self._host_bufs = host_bufs
             self._fixed_q = max_q_len
+            self._fixed_kv = int(max_kv_len)
             self._fixed = None          # (max_q_len, max_work, max_merge) from the first plan
             self._work_d = work_buf
 
@@ -135,7 +139,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
             mq = self._fixed_q or max(1, int(np.diff(qo_h).max(initial=1)))
             mw, mm = C.c_int32(0), C.c_int32(0)
             check(lib.nsg_attn_fixed_capacity(B, mq, num_qo_heads, num_kv_heads, self._num_cus,
-                                              C.byref(mw), C.byref(mm)), "nsg_attn_fixed_capacity")
+                                              self._fixed_kv, C.byref(mw), C.byref(mm)),
+                  "nsg_attn_fixed_capacity")
             need = (mw.value + mm.value) * NSG_ATTN_WORK_INTS
             if self._work_d is None:
                 self._work_d = torch.zeros(need, dtype=torch.int32, device=self._device)
@@ -152,7 +157,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
         pl = AttnPlan()
         check(lib.nsg_attn_plan_fixed(qo_h.ctypes.data, kvp_h.ctypes.data, last_h.ctypes.data, B,
                                       num_qo_heads, num_kv_heads, head_dim_qk, page_size,
-                                      1 if causal else 0, self._num_cus, mq, mw, mm,
+                                      1 if causal else 0, self._num_cus, mq, self._fixed_kv,
+                                      mw, mm,
                                       self._work_h.ctypes.data, self._work_h.shape[0],
                                       C.byref(pl)), "nsg_attn_plan_fixed")
         nnz = int(kvp_h[-1])

@@ -95,9 +95,10 @@ def test_planner_kv_groups_follow_the_work_size(lib):
     assert big.kv_groups == 1 and big.num_work >= 256
 
 
-def _plan_fixed(lib, q_lens, kv_lens, batch_cap, max_q, Hq=14, Hkv=2, D=64, P=16, cus=256):
+def _plan_fixed(lib, q_lens, kv_lens, batch_cap, max_q, Hq=14, Hkv=2, D=64, P=16, cus=256,
+                max_kv=0):
     mw, mm = C.c_int32(0), C.c_int32(0)
-    assert lib.nsg_attn_fixed_capacity(batch_cap, max_q, Hq, Hkv, cus, C.byref(mw),
+    assert lib.nsg_attn_fixed_capacity(batch_cap, max_q, Hq, Hkv, cus, max_kv, C.byref(mw),
                                        C.byref(mm)) == 0
     B = len(q_lens)
     qo = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
@@ -108,8 +109,8 @@ def _plan_fixed(lib, q_lens, kv_lens, batch_cap, max_q, Hq=14, Hkv=2, D=64, P=16
     work = np.full(cap * NSG_ATTN_WORK_INTS, 77, np.int32)    # garbage: padding must clear it
     pl = AttnPlan()
     rc = lib.nsg_attn_plan_fixed(qo.ctypes.data, kvp.ctypes.data, last.ctypes.data, B, Hq, Hkv,
-                                 D, P, 1, cus, max_q, mw.value, mm.value, work.ctypes.data, cap,
-                                 C.byref(pl))
+                                 D, P, 1, cus, max_q, max_kv, mw.value, mm.value,
+                                 work.ctypes.data, cap, C.byref(pl))
     return rc, pl, work.reshape(cap, NSG_ATTN_WORK_INTS), (mw.value, mm.value)
 
 
@@ -149,6 +150,20 @@ def test_fixed_plan_covers_long_contexts(lib):
     items = work[:mw][work[:mw, 1] > 0]
     merges = work[mw:][work[mw:, 3] > 1]
     _check_cover(pl, items, merges, [5] * 16, kv_lens, qo, kvp)
+
+
+def test_fixed_plan_with_kv_bound_never_splits(lib):
+    rng = np.random.default_rng(4)
+    for kv_lens in ([5] * 32, list(rng.integers(100, 641, 32)), [4096] * 32):
+        rc, pl, work, (mw, mm) = _plan_fixed(lib, [5] * 32, kv_lens, 32, 5, max_kv=4096)
+        assert rc == 0, lib.nsg_last_error()
+        assert (mw, mm) == (32, 0) and (pl.num_work, pl.num_merge) == (32, 0)
+        assert pl.max_splits == 1 and pl.kv_groups == 4
+        qo = np.concatenate([[0], np.cumsum([5] * 32)]).astype(np.int32)
+        kvp = np.concatenate([[0], np.cumsum([(L + 15) // 16 for L in kv_lens])]).astype(np.int32)
+        _check_cover(pl, work[:mw], work[mw:mw], [5] * 32, kv_lens, qo, kvp)
+    assert _plan_fixed(lib, [5] * 2, [4097, 10], 2, 5, max_kv=4096)[0] == 1   # over the bound
+    assert "bound" in lib.nsg_last_error().decode()
 
 
 def test_fixed_plan_keeps_tile_shape_and_rejects_longer_queries(lib):

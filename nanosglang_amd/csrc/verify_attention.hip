@@ -50,6 +50,8 @@ constexpr int kTargetWgPerCu = 8;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef short v8i16 __attribute__((ext_vector_type(8)));
 
 struct AttnParams {
   const bf16* q;
@@ -105,15 +107,21 @@ __device__ __forceinline__ void wait_steps(int later) {
 
 // LDS tile swizzles: 16-byte chunk c of token row t is stored at physical
 // chunk c ^ swz(t).  K fragments read one logical chunk of 16 consecutive
-// tokens (needs distinct banks across t); V^T fragments read two adjacent
-// chunks of 4 rows t = 4g + j (needs distinct chunk pairs across g, and a
-// per-lane constant swizzle so that read offsets stay affine).
+// tokens (needs distinct banks across t).  A V^T transposing read takes one
+// 32-byte chunk pair from each of 16 rows t = 4g + j (g, j < 4): the pair
+// index is XORed with a function of t that spreads those 16 rows over every
+// 32-byte bank window (with 256-byte bank rows: 2 rows per window, the
+// minimum).
 template <int D>
 __device__ __forceinline__ int swz_k(int t) {
   if constexpr (D == 64) return (t >> 1) & 7;  // 128-byte rows: two rows per bank cycle
   return t & 15;                               // 256-byte rows: one row per bank cycle
 }
-__device__ __forceinline__ int swz_v(int t) { return 2 * ((t >> 2) & 3); }
+template <int D>
+__device__ __forceinline__ int swz_v(int t) {
+  if constexpr (D == 64) return 2 * ((t >> 1) & 3);  // odd rows sit in the other half-row
+  return 2 * (t & 7);
+}
 
 constexpr float kLazyRescale = 8.f;  // rescale O only when a row max grows by > 2^8
 
@@ -222,10 +230,21 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
   int koff[KC];
 #pragma unroll
   for (int c = 0; c < KC; ++c) koff[c] = r16 * D + (((4 * c + g4) ^ swz_k<D>(r16)) * 8);
-  int voff[DT];
+  // V^T fragments come from ds_read_b64_tr_b16: within each 16-lane group,
+  // result element j of lane i is element i % 4 of the 8 bytes addressed by
+  // lane 4 j + i / 4.  So lane (r16, g4) addresses token row
+  // 4 g4 + r16 / 4 (+ 16 for elements 4..7), columns 16 dt + 4 (r16 % 4) ..
+  // + 3, and receives V[4 g4 + j][16 dt + r16], j = 0..3 -- the token order
+  // of the P^T operand.  Offsets are in bf16 elements, swizzle applied.
+  int vtr[DT][2];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
-    voff[dt] = 4 * g4 * D + (((2 * dt + (r16 >> 3)) ^ (2 * g4)) * 8) + (r16 & 7);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int t = 16 * hh + 4 * g4 + (r16 >> 2);
+      const int c = 16 * dt + 4 * (r16 & 3);
+      vtr[dt][hh] = t * D + (((c >> 3) ^ swz_v<D>(t)) << 3) + (c & 7);
+    }
 
   // Loop-invariant parts of this lane's DMA copies: token row inside the
   // step, source offset inside the token's head slice, and LDS destination.
@@ -240,26 +259,58 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
     const int jj = j - which * (NINST / 2);
     const int t = jj * TPI + lane / CPR;        // token row inside the step
     const int pc = lane % CPR;                   // physical chunk written by this lane
-    const int lc = pc ^ (which ? swz_v(t) : swz_k<D>(t));  // logical chunk it carries
+    const int lc = pc ^ (which ? swz_v<D>(t) : swz_k<D>(t));  // logical chunk it carries
     d_t[i] = t;
     d_off[i] = lc * 8;
     d_lds[i] = which * TILE + jj * TPI * D;
     d_v[i] = which != 0;
   }
+  // Pages of at least 16 tokens: a step (32 tokens from a multiple of 32)
+  // spans at most two pages, and each copy's offset inside its page is fixed,
+  // so a step needs two page ids and one multiply-add per copy.  Measured to
+  // pay only for single-wave groups (one wave issues all of a step's copies);
+  // with several waves per group the per-copy lookup is faster.
+  const bool big_pages = RT == 1 && P >= 16;
+  int d_pg[NI];          // which of the step's two pages (big pages)
+  int64_t d_inpage[NI];  // element offset of the copy inside its page (big pages)
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    d_pg[i] = P < kTokIt ? (d_t[i] >> p.log2P) : 0;
+    d_inpage[i] = (int64_t)(d_t[i] & (P - 1)) * (int64_t)tok_stride + (int64_t)head_off + d_off[i];
+  }
+  const int64_t page_elems = (int64_t)P * (int64_t)tok_stride;
   // Issue this wave's DMA instructions for step `it` into ring slot `slot`.
   auto issue = [&](int it, int slot) {
     const int t0 = gkvb + it * kTokIt;
+    const bool full = t0 + kTokIt <= kve;  // no token of the step past the range
+    int pg0 = 0, pg1 = 0;
+    int64_t shift = 0;
+    if (big_pages && full) {
+      const int pidx = (t0 >> p.log2P) - page0;
+      pg0 = s_pages[pidx];
+      pg1 = P < kTokIt ? s_pages[pidx + 1] : pg0;
+      shift = P > kTokIt ? (int64_t)(t0 & (P - 1)) * (int64_t)tok_stride : 0;
+    }
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int tok = t0 + d_t[i];
       const bf16* src = d_v[i] ? dummy_v : dummy_k;
-      if (tok < kve) {
-        const int page = s_pages[(tok >> p.log2P) - page0];
+      if (big_pages && full) {
+        const int page = d_pg[i] ? pg1 : pg0;
         if ((unsigned)page < (unsigned)p.num_pages) {
-          src = (d_v[i] ? p.vc : p.kc) + ((size_t)page * P + (tok & (P - 1))) * tok_stride +
-                head_off + d_off[i];
+          src = (d_v[i] ? p.vc : p.kc) + (int64_t)page * page_elems + shift + d_inpage[i];
         } else {
           bad_page = true;
+        }
+      } else {
+        const int tok = t0 + d_t[i];
+        if (tok < kve) {
+          const int page = s_pages[(tok >> p.log2P) - page0];
+          if ((unsigned)page < (unsigned)p.num_pages) {
+            src = (d_v[i] ? p.vc : p.kc) + ((size_t)page * P + (tok & (P - 1))) * tok_stride +
+                  head_off + d_off[i];
+          } else {
+            bad_page = true;
+          }
         }
       }
       // void* operands: with typed pointers the host pass silently drops the
@@ -298,7 +349,7 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
 
       const int t0 = gkvb + it * kTokIt;
       const bf16* Kt = ring[grp][slot][0];
-      const uint16_t* Vt = reinterpret_cast<const uint16_t*>(ring[grp][slot][1]);
+      const bf16* Vt = ring[grp][slot][1];
 
       // ---- S^T = K Q^T: lane holds tokens 16s + 4*g4 + i of query row r16 ----
       floatx4 sacc[2];
@@ -315,12 +366,21 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
 
       // ---- online softmax (base 2) with lazy rescaling ----
       float sv[8];
+      if (t0 + kTokIt - 1 <= lim0 && t0 + kTokIt <= kve) {
+        // every row of the tile sees every token of the step (lim0 is the
+        // tile's smallest causal limit): no mask
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
+        for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int j = t0 + 16 * s2 + 4 * g4 + i;
-          sv[4 * s2 + i] = (j <= lim && j < kve) ? sacc[s2][i] * p.scale_log2 : kMaskVal;
+          for (int i = 0; i < 4; ++i) sv[4 * s2 + i] = sacc[s2][i] * p.scale_log2;
+      } else {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int j = t0 + 16 * s2 + 4 * g4 + i;
+            sv[4 * s2 + i] = (j <= lim && j < kve) ? sacc[s2][i] * p.scale_log2 : kMaskVal;
+          }
         }
       }
       float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
@@ -354,12 +414,12 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
       //      4*g4 + e (e < 4) or 16 + 4*g4 + (e - 4), matching pf ----
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const uint16_t* vp = Vt + voff[dt];
-        const u32x4 w = {
-            (uint32_t)vp[0] | ((uint32_t)vp[D] << 16),
-            (uint32_t)vp[2 * D] | ((uint32_t)vp[3 * D] << 16),
-            (uint32_t)vp[16 * D] | ((uint32_t)vp[17 * D] << 16),
-            (uint32_t)vp[18 * D] | ((uint32_t)vp[19 * D] << 16)};
+        // (C-style casts: the only way to name the LDS address space here)
+        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4i16*)(Vt + vtr[dt][0]));
+        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4i16*)(Vt + vtr[dt][1]));
+        const v8i16 w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w), pf,
                                                            oacc[dt], 0, 0, 0);
       }

@@ -125,7 +125,13 @@ __device__ __forceinline__ int swz_v(int t) {
 
 constexpr float kLazyRescale = 8.f;  // rescale O only when a row max grows by > 2^8
 
-constexpr int kNBuf = 4;            // LDS ring depth (steps in flight: kNBuf - 1)
+// LDS ring depth (steps in flight: depth - 1).  With several KV groups a
+// workgroup fills the CU's LDS anyway; with one, a shallower ring lets more
+// workgroups (waves) share a CU, which hides more latency (measured: depth 3
+// beats 4 by ~8 % on the large shape).
+constexpr int kRingOne = 3;
+constexpr int kRingGroups = 4;
+constexpr int ring_depth(int KS) { return KS == 1 ? kRingOne : kRingGroups; }
 // KV groups per workgroup in the latency regime: as many 4-deep rings as
 // fit 128 KB of LDS (8 KB per step at head_dim 64, 16 KB at 128).
 constexpr int kv_groups_max(int D) { return D == 64 ? 4 : 2; }
@@ -140,7 +146,7 @@ constexpr int kMaxItemPages = 1024; // page ids one work item may span
 // launch nor more sequential steps per wave.
 // The item's page ids are staged in LDS once.  K and V rows of each step go
 // straight from HBM to a ring slot of the group with global_load_lds_dwordx4
-// (no staging registers), kNBuf - 1 steps ahead of the math; an explicit
+// (no staging registers), ring_depth - 1 steps ahead of the math; an explicit
 // vmcnt wait per step (plus a raw s_barrier when a group has several waves)
 // keeps the ring full (__syncthreads would drain it).  Every group iterates
 // the same number of steps (idle ones do nothing but the barrier), so the
@@ -157,6 +163,7 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
   constexpr int NI = (NINST + RT - 1) / RT;  // DMA instructions per wave per step
   constexpr int PSTRIDE = D + 4;          // partial row: O[D], m, l, 2 pad
   constexpr int NTHR = RT * KS * 64;
+  constexpr int kNBuf = ring_depth(KS);
   __shared__ __attribute__((aligned(16))) bf16 ring[KS][kNBuf][2][TILE];
   __shared__ int s_pages[kMaxItemPages];
 

@@ -9,7 +9,8 @@
 // throughput-bound for the small matrices (1.6 - 17 MB).  Library GEMMs tile
 // for large M; this kernel is shaped for the weight stream instead:
 //
-// * a workgroup owns 16 * NT rows of W (output columns) and all M rows of x;
+// * a workgroup owns 16 * NT rows of W (output columns) and up to 32 rows of
+//   x (more rows run as 32-row groups, see launch_epi);
 //   its NW waves split K in 64-element chunks (wave w takes chunks w, w + NW,
 //   ...), so every lane issues its loads for the next chunk while the MFMAs
 //   of the current one run, and the waves' partial sums meet in LDS;
@@ -43,7 +44,11 @@ struct LinParams {
   int64_t ldx, ldw, ldy;
   int M, N, K;     // N: output columns (SwiGLU: the intermediate size I)
   int w_rows;      // rows of W (N, or 2 I for SwiGLU)
+  int row_groups;  // > 1: M runs as groups of kRowGroup rows, one workgroup each
+  int col_tiles;   // column tiles (workgroups per row group)
 };
+
+constexpr int kRowGroup = 32;
 
 enum { kEpiBias = 0, kEpiSilu = 1 };
 
@@ -67,6 +72,24 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
   const int grp = wid / NW;
   const int r16 = lane & 15;
 
+  // Workgroup -> (column tile, row group).  With row groups, the groups of
+  // one column tile sit on the same XCD (workgroups go round-robin over the
+  // 8 XCDs), so its W rows come from HBM once and from that XCD's L2 for the
+  // other groups.
+  int tile = blockIdx.x;
+  int M = p.M;
+  const bf16* xg = p.x;
+  bf16* yg = p.y;
+  if (p.row_groups > 1) {
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    tile = xcd + 8 * (slot / p.row_groups);
+    if (tile >= p.col_tiles) return;
+    const int m0 = (slot % p.row_groups) * kRowGroup;
+    M = min(kRowGroup, p.M - m0);
+    xg += (int64_t)m0 * p.ldx;
+    yg += (int64_t)m0 * p.ldy;
+  }
+
   // Loads are coalesced: for a 16-row x 32-k fragment, lane l reads row
   // l / 4, 16-byte segment l % 4, so each lane quad covers one row's 64
   // contiguous bytes (the MFMA layout itself -- lane l = row l % 16 -- puts
@@ -82,10 +105,10 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
   for (int nt = 0; nt < NT; ++nt) {
     int row;
     if constexpr (EPI == kEpiSilu) {
-      const int col_tile = blockIdx.x * (NT / 2) + (nt >> 1);
+      const int col_tile = tile * (NT / 2) + (nt >> 1);
       row = ((nt & 1) ? p.N : 0) + col_tile * 16 + lrow;
     } else {
-      row = (blockIdx.x * NT + nt) * 16 + lrow;
+      row = (tile * NT + nt) * 16 + lrow;
     }
     row = min(row, p.w_rows - 1);
     wp[nt] = p.w + (int64_t)row * p.ldw + lseg;
@@ -93,7 +116,7 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
   const bf16* xp[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
-    xp[mt] = p.x + (int64_t)min((grp * MT + mt) * 16 + lrow, p.M - 1) * p.ldx + lseg;
+    xp[mt] = xg + (int64_t)min((grp * MT + mt) * 16 + lrow, M - 1) * p.ldx + lseg;
   auto to_mfma = [&](u32x4 v) {
     u32x4 r;
 #pragma unroll
@@ -110,7 +133,7 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
   const int nchunks = p.K / kChunk;
   // workgroups start their K sweep at different chunks: otherwise all of them
   // read the same x lines at the same moment, from the same L2 channels
-  const int rot = (int)(blockIdx.x % (unsigned)nchunks);
+  const int rot = (int)((unsigned)tile % (unsigned)nchunks);
   // two register stages: loads of chunk c + NW are in flight while chunk c
   // is multiplied
   u32x4 wa[NT][2], xa[MT][2], wb[NT][2], xb[MT][2];
@@ -197,10 +220,10 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
       }
       int n;
       if constexpr (EPI == kEpiSilu)
-        n = (blockIdx.x * (NT / 2) + t0 / 2) * 16 + 4 * (l >> 4);
+        n = (tile * (NT / 2) + t0 / 2) * 16 + 4 * (l >> 4);
       else
-        n = (blockIdx.x * NT + t0) * 16 + 4 * (l >> 4);
-      if (m >= p.M || n >= p.N) continue;
+        n = (tile * NT + t0) * 16 + 4 * (l >> 4);
+      if (m >= M || n >= p.N) continue;
       float v[4];
       if constexpr (EPI == kEpiSilu) {
 #pragma unroll
@@ -220,7 +243,7 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
           v[3] += bf16_bits_to_float(b[1] >> 16);
         }
       }
-      *reinterpret_cast<u32x2*>(p.y + (int64_t)m * p.ldy + n) =
+      *reinterpret_cast<u32x2*>(yg + (int64_t)m * p.ldy + n) =
           u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
     }
     __syncthreads();
@@ -230,32 +253,33 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
 // Tile shape per row count: more W rows per workgroup as M grows, so that x
 // (read from L2 once per workgroup) stays a small multiple of W's bytes.
 template <int MT, int MG, int NT, int NW, int EPI>
-int32_t launch_cfg(const LinParams& p, hipStream_t s) {
+int32_t launch_cfg(LinParams p, hipStream_t s) {
   const int cols_per_wg = 16 * (EPI == kEpiSilu ? NT / 2 : NT);
-  const int grid = (p.N + cols_per_wg - 1) / cols_per_wg;
+  p.col_tiles = (p.N + cols_per_wg - 1) / cols_per_wg;
+  int grid = p.col_tiles;
+  if (p.row_groups > 1) grid = p.row_groups * 8 * ((p.col_tiles + 7) / 8);
   hipLaunchKernelGGL((linear_kernel<MT, MG, NT, NW, EPI>), dim3(grid), dim3(MG * NW * 64), 0, s,
                      p);
   return launch_status("linear_kernel");
 }
 
+// Up to kRowGroup rows: one workgroup per column tile.  More rows run as
+// groups of kRowGroup rows, one workgroup per (column tile, group), with the
+// groups of a tile on one XCD.  Very wide outputs give a workgroup four
+// column tiles so that x is re-read no more than W.
+constexpr int kWideN = 65536;
+
 template <int EPI>
-int32_t launch_epi(const LinParams& p, hipStream_t s) {
-  constexpr int N1 = EPI == kEpiSilu ? 2 : 1;  // M <= 32: one column tile per workgroup
-  switch ((p.M + 15) / 16) {
-    case 1: return launch_cfg<1, 1, N1, 8, EPI>(p, s);
-    case 2: return launch_cfg<2, 1, N1, 8, EPI>(p, s);
-    case 3: return launch_cfg<3, 1, 2, 8, EPI>(p, s);
-    case 4: return launch_cfg<4, 1, 2, 8, EPI>(p, s);
-    case 5: return launch_cfg<5, 1, 2, 8, EPI>(p, s);
-    case 6: return launch_cfg<3, 2, 4, 4, EPI>(p, s);
-    case 7:
-    case 8: return launch_cfg<4, 2, 2, 4, EPI>(p, s);
-    case 9:
-    case 10: return launch_cfg<5, 2, 2, 4, EPI>(p, s);
-    default: break;
+int32_t launch_epi(LinParams p, hipStream_t s) {
+  constexpr int N1 = EPI == kEpiSilu ? 2 : 1;  // one column tile per workgroup
+  p.row_groups = 1;
+  if (p.M > kRowGroup) {
+    p.row_groups = (p.M + kRowGroup - 1) / kRowGroup;
+    if (EPI == kEpiBias && p.N >= kWideN) return launch_cfg<2, 1, 4, 8, EPI>(p, s);
+    return launch_cfg<2, 1, N1, 8, EPI>(p, s);
   }
-  set_error("M %d > %d rows", p.M, kMaxMT * 16);
-  return NSG_ERR_UNSUPPORTED;
+  if (p.M <= 16) return launch_cfg<1, 1, N1, 8, EPI>(p, s);
+  return launch_cfg<2, 1, N1, 8, EPI>(p, s);
 }
 
 }  // namespace
@@ -263,19 +287,20 @@ int32_t launch_epi(const LinParams& p, hipStream_t s) {
 
 using namespace nsg;
 
-// Where this kernel beats a library GEMM on MI355X (measured per shape, with
-// weights streamed from HBM): every x row re-read per workgroup costs L2
-// bandwidth, so the kernel serves few rows, and for very wide outputs (the
-// lm_head) only up to 16.
-constexpr int kFastRows = 64;
+// Where this kernel beats hipBLASLt on MI355X (measured per shape, weights
+// streamed from HBM): up to 160 rows for K <= 2048 (q/k/v, o_proj, gate/up),
+// up to 96 for long K (down_proj), up to 16 for very wide outputs (lm_head).
+constexpr int kFastRows = 160;
+constexpr int kFastRowsLongK = 96;
 constexpr int kFastRowsWide = 16;
-constexpr int kWideN = 65536;
+constexpr int kLongK = 4096;
 
 extern "C" int32_t nsg_linear_max_rows(void) { return kMaxMT * 16; }
 
 extern "C" int32_t nsg_linear_preferred(int32_t M, int32_t N, int32_t K) {
   if (M < 1 || K % kChunk != 0 || N % 4 != 0) return 0;
-  return M <= (N >= kWideN ? kFastRowsWide : kFastRows) ? 1 : 0;
+  const int rows = N >= kWideN ? kFastRowsWide : (K >= kLongK ? kFastRowsLongK : kFastRows);
+  return M <= rows ? 1 : 0;
 }
 
 extern "C" int32_t nsg_linear(const void* x, int64_t ldx, const void* w, int64_t ldw,

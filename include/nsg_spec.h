@@ -42,7 +42,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 5
+#define NSG_ABI_VERSION 6
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -241,6 +241,24 @@ int32_t nsg_linear_preferred(int32_t M, int32_t N, int32_t K);
 int32_t nsg_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias,
                    void* y, int64_t ldy, int32_t M, int32_t N, int32_t K, int32_t epilogue,
                    nsg_stream_t stream);
+
+/* The q/k/v projection with RoPE and the KV-slot write as its epilogue:
+ * nsg_linear (NSG_LINEAR_BIAS) of x (M x K) with the fused q/k/v weight w
+ * ((Hq + 2 Hkv) * head_dim rows) and bias, immediately followed by
+ * nsg_rope_kv_write on the bf16 result -- the same arithmetic (the
+ * projection is rounded to bf16 after the bias, then rotated with the
+ * bf16 rounding of causal_lm.py:167-206), without the projection ever
+ * reaching HBM.  Replaces the q/k/v calls of causal_lm.py:229-231 plus
+ * apply_rope (:300-301) and the KV scatter (:335-338).  head_dim 64 or 128;
+ * M <= nsg_linear_max_rows(); K % 64 == 0.  Arguments after K mean what
+ * they mean for nsg_rope_kv_write. */
+int32_t nsg_linear_rope_kv(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                           const void* bias, int32_t M, int32_t K, int32_t num_qo_heads,
+                           int32_t num_kv_heads, int32_t head_dim, const int64_t* positions,
+                           const float* cos_table, const float* sin_table,
+                           int32_t max_position, const int64_t* slots, void* q_out,
+                           void* k_cache, void* v_cache, int64_t num_slots, int32_t* flags,
+                           nsg_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Philox4x32-10 uniforms: out[i] = u(seed, stream_id, offset + i) with

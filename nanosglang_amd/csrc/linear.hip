@@ -46,11 +46,27 @@ struct LinParams {
   int w_rows;      // rows of W (N, or 2 I for SwiGLU)
   int row_groups;  // > 1: M runs as groups of kRowGroup rows, one workgroup each
   int col_tiles;   // column tiles (workgroups per row group)
+  // RoPE + KV-slot epilogue (q/k/v projection): one workgroup per head
+  const int64_t* pos;
+  const float* cos_t;
+  const float* sin_t;
+  int max_pos;
+  const int64_t* slots;
+  int Hq, Hkv, head_dim;
+  bf16* q_out;
+  bf16* kc;
+  bf16* vc;
+  int64_t num_slots;
+  int* flags;
 };
 
 constexpr int kRowGroup = 32;
 
-enum { kEpiBias = 0, kEpiSilu = 1 };
+enum { kEpiBias = 0, kEpiSilu = 1, kEpiRope = 2 };
+
+__device__ __forceinline__ float bf16_round(float x) {
+  return bf16_bits_to_float(float_to_bf16_bits(x));
+}
 
 __device__ __forceinline__ float silu_bf16(float g) {
   return bf16_bits_to_float(float_to_bf16_bits(g / (1.f + __expf(-g))));
@@ -78,13 +94,14 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
   // other groups.
   int tile = blockIdx.x;
   int M = p.M;
+  int m0 = 0;
   const bf16* xg = p.x;
   bf16* yg = p.y;
   if (p.row_groups > 1) {
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
     tile = xcd + 8 * (slot / p.row_groups);
     if (tile >= p.col_tiles) return;
-    const int m0 = (slot % p.row_groups) * kRowGroup;
+    m0 = (slot % p.row_groups) * kRowGroup;
     M = min(kRowGroup, p.M - m0);
     xg += (int64_t)m0 * p.ldx;
     yg += (int64_t)m0 * p.ldy;
@@ -107,6 +124,11 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
     if constexpr (EPI == kEpiSilu) {
       const int col_tile = tile * (NT / 2) + (nt >> 1);
       row = ((nt & 1) ? p.N : 0) + col_tile * 16 + lrow;
+    } else if constexpr (EPI == kEpiRope) {
+      // tile = (head, s): columns 16 s .. + 16 of the head and their RoPE
+      // partners head_dim / 2 further on
+      const int tph = p.head_dim / 32;  // tiles per half head
+      row = (tile / tph) * p.head_dim + nt * (p.head_dim / 2) + (tile % tph) * 16 + lrow;
     } else {
       row = (tile * NT + nt) * 16 + lrow;
     }
@@ -168,12 +190,58 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
               __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[nt], xf[mt], acc[nt][mt], 0, 0, 0);
     }
   };
+  // RoPE epilogue operands.  A workgroup owns the 16 rotation pairs
+  // (i, i + head_dim / 2), i = 16 s .. + 16, of one head: tile 0 holds the
+  // first members, tile 1 the partners.  Epilogue item idx = threadIdx.x +
+  // j * threads is row m = idx / 16, pair i = 16 s + idx % 16; rows past M
+  // are clamped and not stored.  The loads go before the K sweep, so that
+  // their latency (position, then cos / sin at that position) hides under it.
+  constexpr bool kRope = EPI == kEpiRope;
+  constexpr int kThreads = NW * 64;
+  constexpr int kItems = MT * 16 * 16;
+  constexpr int kIpt = kRope ? (kItems + kThreads - 1) / kThreads : 1;  // items per thread
+  constexpr int kRItems = 2 * MT * 64;  // reduction items: (tile, m tile, lane)
+  constexpr int kRpt = kRope ? (kRItems + kThreads - 1) / kThreads : 1;
+  static_assert(!kRope || NT == 2, "a first-half and a second-half tile");
+  static_assert(!kRope || (kItems % 64 == 0 && kRItems % 64 == 0), "whole waves of items");
+  const int half = p.head_dim / 2;
+  const int tph = kRope ? p.head_dim / 32 : 1;
+  const int head = tile / tph;
+  const int pair0 = (tile % tph) * 16;
+  int64_t e_pos[kIpt], e_slot[kIpt];
+  float e_cos[kIpt], e_sin[kIpt];
+  uint2 e_bias[kRpt];
+  if constexpr (kRope) {
+#pragma unroll
+    for (int j = 0; j < kIpt; ++j) {
+      const int idx = min((int)threadIdx.x + j * kThreads, kItems - 1);
+      const int t = m0 + min(idx / 16, M - 1);
+      e_pos[j] = p.pos[t];
+      e_slot[j] = p.slots ? p.slots[t] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kRpt; ++j) {
+      const int r = min((int)threadIdx.x + j * kThreads, kRItems - 1);
+      const int c = head * p.head_dim + (r / (MT * 64)) * half + pair0 + 4 * ((r & 63) >> 4);
+      e_bias[j] = p.bias ? *reinterpret_cast<const uint2*>(p.bias + c) : uint2{0u, 0u};
+    }
+  }
+
   // This wave's chunks are wave + NW i for i < n.  The loop body issues its
   // loads unconditionally: a load under a branch would make the wait-count
   // pass assume it might be outstanding and drain the next chunk's loads
   // before the current chunk's MFMAs.
   const int n = (nchunks - wave + NW - 1) / NW;
   if (n > 0) load(wave, wa, xa);
+  if constexpr (kRope) {
+#pragma unroll
+    for (int j = 0; j < kIpt; ++j) {
+      const int i = pair0 + ((int)threadIdx.x + j * kThreads) % 16;
+      const int64_t pc = min(max(e_pos[j], (int64_t)0), (int64_t)p.max_pos - 1);
+      e_cos[j] = p.cos_t[pc * half + i];
+      e_sin[j] = p.sin_t[pc * half + i];
+    }
+  }
   int i = 0;
   // sched_barrier(0): the machine scheduler would otherwise sink the next
   // chunk's loads next to their MFMAs (to shorten live ranges), which turns
@@ -195,6 +263,81 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
     mma(wb, xb);
   } else if (i < n) {
     mma(wa, xa);
+  }
+
+  if constexpr (EPI == kEpiRope) {
+    // ---- 16 rotation pairs of one head for this row group ----
+    // 1. partial sums to LDS; 2. reduce over the waves, add the bias, round
+    // to bf16 (the projection's output); 3. rotate q and k heads with
+    // bf16-rounded cos / sin and products (the arithmetic of bf16 tensors in
+    // causal_lm.py:181-206, as rope_kv_write_kernel), write q to q_out and k
+    // / v to the token's KV slot.
+    static_assert(MG == 1, "one row group per workgroup");
+    __shared__ floatx4 rred[2][NW][MT][64];
+    __shared__ float hv[MT * 16][33];  // [m][tile * 16 + column], padded
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) rred[q][wave][mt][lane] = acc[q][mt];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kRpt; ++j) {
+      const int r = threadIdx.x + j * kThreads;
+      if (kRItems % kThreads == 0 || r < kRItems) {
+        const int q = r / (MT * 64);
+        const int mt = (r >> 6) % MT;
+        const int l = r & 63;
+        floatx4 sum = rred[q][0][mt][l];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) sum += rred[q][w][mt][l];
+        const uint2 bb = e_bias[j];
+        const float b4[4] = {bf16_bits_to_float(bb.x & 0xffffu), bf16_bits_to_float(bb.x >> 16),
+                             bf16_bits_to_float(bb.y & 0xffffu), bf16_bits_to_float(bb.y >> 16)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          hv[mt * 16 + (l & 15)][q * 16 + 4 * (l >> 4) + i] = bf16_round(sum[i] + b4[i]);
+      }
+    }
+    __syncthreads();
+    // head: q heads, then k heads, then v heads
+    const bool rotate = head < p.Hq + p.Hkv;
+#pragma unroll
+    for (int j = 0; j < kIpt; ++j) {
+      const int idx = threadIdx.x + j * kThreads;
+      const int m = idx / 16;
+      if ((kItems % kThreads != 0 && idx >= kItems) || m >= M) continue;
+      const int il = idx % 16;
+      const int i = pair0 + il;
+      const int64_t t = m0 + m;
+      const float x1 = hv[m][il], x2 = hv[m][16 + il];
+      float y1 = x1, y2 = x2;
+      if (rotate) {
+        const bool pos_ok = e_pos[j] >= 0 && e_pos[j] < p.max_pos;
+        const float c = pos_ok ? bf16_round(e_cos[j]) : 0.f;
+        const float sn = pos_ok ? bf16_round(e_sin[j]) : 0.f;
+        y1 = bf16_round(x1 * c) + bf16_round(-x2 * sn);
+        y2 = bf16_round(x2 * c) + bf16_round(x1 * sn);
+        if (!pos_ok && i == 0 && p.flags) atomicOr(p.flags, 1);
+      }
+      uint16_t* dst = nullptr;
+      if (head < p.Hq) {
+        dst = reinterpret_cast<uint16_t*>(p.q_out) + (t * p.Hq + head) * p.head_dim;
+      } else {
+        const int64_t slot = e_slot[j];
+        if (slot >= 0 && slot < p.num_slots) {
+          const int kh = rotate ? head - p.Hq : head - p.Hq - p.Hkv;
+          dst = reinterpret_cast<uint16_t*>(rotate ? p.kc : p.vc) +
+                (slot * p.Hkv + kh) * p.head_dim;
+        } else if (slot >= p.num_slots && i == 0 && p.flags) {
+          atomicOr(p.flags, 1);
+        }
+      }
+      if (dst) {
+        dst[i] = float_to_bf16_bits(y1);
+        dst[i + half] = float_to_bf16_bits(y2);
+      }
+    }
+    return;
   }
 
   // cross-wave reduction and epilogue, NP physical tiles at a time.  Lane l
@@ -282,6 +425,14 @@ int32_t launch_epi(LinParams p, hipStream_t s) {
   return launch_cfg<2, 1, N1, 8, EPI>(p, s);
 }
 
+// RoPE epilogue: a workgroup per (head, 16 rotation pairs) -- two column
+// tiles -- and row group.
+int32_t launch_rope(LinParams p, hipStream_t s) {
+  p.row_groups = p.M > kRowGroup ? (p.M + kRowGroup - 1) / kRowGroup : 1;
+  if (p.M <= 16) return launch_cfg<1, 1, 2, 8, kEpiRope>(p, s);
+  return launch_cfg<2, 1, 2, 8, kEpiRope>(p, s);
+}
+
 }  // namespace
 }  // namespace nsg
 
@@ -342,4 +493,63 @@ extern "C" int32_t nsg_linear(const void* x, int64_t ldx, const void* w, int64_t
   p.w_rows = epilogue == NSG_LINEAR_SILU_MUL ? 2 * N : N;
   hipStream_t s = static_cast<hipStream_t>(stream);
   return epilogue == NSG_LINEAR_SILU_MUL ? launch_epi<kEpiSilu>(p, s) : launch_epi<kEpiBias>(p, s);
+}
+
+extern "C" int32_t nsg_linear_rope_kv(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                      const void* bias, int32_t M, int32_t K,
+                                      int32_t num_qo_heads, int32_t num_kv_heads,
+                                      int32_t head_dim, const int64_t* positions,
+                                      const float* cos_table, const float* sin_table,
+                                      int32_t max_position, const int64_t* slots, void* q_out,
+                                      void* k_cache, void* v_cache, int64_t num_slots,
+                                      int32_t* flags, nsg_stream_t stream) {
+  NSG_CHECK_ARG(M >= 0 && K > 0, "M %d, K %d", M, K);
+  if (M == 0) {
+    clear_error();
+    return NSG_OK;
+  }
+  NSG_CHECK_ARG(x && w && positions && cos_table && sin_table && q_out, "null pointer argument");
+  NSG_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0, "heads %d / %d", num_qo_heads, num_kv_heads);
+  NSG_CHECK_ARG(!slots || (k_cache && v_cache && num_slots > 0), "slots need both caches");
+  if (head_dim != 64 && head_dim != 128) {
+    set_error("head_dim %d not supported (64 or 128)", head_dim);
+    return NSG_ERR_UNSUPPORTED;
+  }
+  if (M > kMaxMT * 16 || K % kChunk != 0) {
+    set_error("M %d > %d or K %d not a multiple of %d", M, kMaxMT * 16, K, kChunk);
+    return NSG_ERR_UNSUPPORTED;
+  }
+  const int N = (num_qo_heads + 2 * num_kv_heads) * head_dim;
+  NSG_CHECK_ARG(ldx >= K && ldw >= K && ldx % 8 == 0 && ldw % 8 == 0 &&
+                    ((uintptr_t)x | (uintptr_t)w) % 16 == 0,
+                "x and w rows must be 16-byte aligned");
+  NSG_CHECK_ARG(max_position > 0, "max_position %d", max_position);
+  NSG_CHECK_ARG((uintptr_t)bias % 8 == 0, "bias must be 8-byte aligned");
+  LinParams p{};
+  p.x = static_cast<const bf16*>(x);
+  p.w = static_cast<const bf16*>(w);
+  p.bias = static_cast<const bf16*>(bias);
+  p.y = nullptr;
+  p.ldx = ldx;
+  p.ldw = ldw;
+  p.ldy = 0;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.w_rows = N;
+  p.pos = positions;
+  p.cos_t = cos_table;
+  p.sin_t = sin_table;
+  p.max_pos = max_position;
+  p.slots = slots;
+  p.Hq = num_qo_heads;
+  p.Hkv = num_kv_heads;
+  p.head_dim = head_dim;
+  p.q_out = static_cast<bf16*>(q_out);
+  p.kc = static_cast<bf16*>(k_cache);
+  p.vc = static_cast<bf16*>(v_cache);
+  p.num_slots = num_slots;
+  p.flags = flags;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return launch_rope(p, s);
 }

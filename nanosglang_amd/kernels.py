@@ -522,6 +522,50 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     return out
 
 
+def linear_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
+                   num_qo_heads: int, num_kv_heads: int, head_dim: int,
+                   positions: torch.Tensor, cos_table: torch.Tensor, sin_table: torch.Tensor,
+                   slots: torch.Tensor | None, k_cache: torch.Tensor | None,
+                   v_cache: torch.Tensor | None, q_out: torch.Tensor | None = None,
+                   force: bool = False) -> torch.Tensor:
+    """q/k/v projection + RoPE + KV-slot write (C ABI: nsg_linear_rope_kv).
+
+    Same result as ``rope_kv_write(linear(x, weight, bias), ...)``; at row
+    counts where the library GEMM is the faster projection (prefill), or for
+    shapes the fused kernel does not take, it runs exactly that pair.
+    Returns rotated q (M, Hq, D)."""
+    _require_gpu(x, "x")
+    M, K = x.shape
+    lib = _lib()
+    N = weight.shape[0]
+    fits = (M <= lib.nsg_linear_max_rows() and K % 64 == 0 and head_dim in (64, 128)
+            and N == (num_qo_heads + 2 * num_kv_heads) * head_dim and x.stride(1) == 1
+            and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0 and x.dtype == torch.bfloat16)
+    if not fits or not (force or lib.nsg_linear_preferred(M, N, K)):
+        qkv = linear(x, weight, bias)
+        return rope_kv_write(qkv, num_qo_heads, num_kv_heads, head_dim, positions, cos_table,
+                             sin_table, slots, k_cache, v_cache, q_out)
+    if weight.dtype != torch.bfloat16 or weight.stride(1) != 1 or weight.shape[1] != K:
+        raise ValueError("weight must be bf16 (N, K) with unit inner stride")
+    if bias is not None and (bias.dtype != torch.bfloat16 or not bias.is_contiguous()):
+        raise ValueError("bias must be contiguous bf16")
+    if q_out is None:
+        q_out = torch.empty(M, num_qo_heads, head_dim, dtype=torch.bfloat16, device=x.device)
+    positions = positions.to(torch.int64).contiguous()
+    if slots is not None:
+        slots = slots.to(torch.int64).contiguous()
+        num_slots = k_cache.numel() // (num_kv_heads * head_dim)
+    else:
+        num_slots = 0
+    check(lib.nsg_linear_rope_kv(
+        x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), _ptr(bias), M, K,
+        num_qo_heads, num_kv_heads, head_dim, positions.data_ptr(), cos_table.data_ptr(),
+        sin_table.data_ptr(), cos_table.shape[0], _ptr(slots), q_out.data_ptr(),
+        _ptr(k_cache), _ptr(v_cache), num_slots, None, _stream_ptr(x.device)),
+        "nsg_linear_rope_kv")
+    return q_out
+
+
 def philox_uniform(seed: int, stream_id: int, offset: int, n: int, device) -> torch.Tensor:
     """n float32 uniforms of Philox4x32-10 stream ``stream_id`` (see nsg_spec.h)."""
     out = torch.empty(n, dtype=torch.float32, device=device)

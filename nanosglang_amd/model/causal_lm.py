@@ -13,9 +13,12 @@ MI355X-side choices:
   epilogue); at decode / verify row counts (<= 160) every linear layer runs
   the HIP weight-streaming kernel ``kernels.linear``, at prefill sizes
   hipBLASLt;
-* RoPE + KV-slot write is one HIP kernel (``kernels.rope_kv_write``) with
-  the reference's bf16 rounding order; attention is the HIP verify-attention
-  kernel behind ``BatchPrefillWithPagedKVCacheWrapper``;
+* RoPE + KV-slot write (with the reference's bf16 rounding order) is the
+  epilogue of the q/k/v projection at decode / verify row counts
+  (``kernels.linear_rope_kv``: the projection never reaches HBM) and its own
+  HIP kernel (``kernels.rope_kv_write``) after a prefill GEMM; attention is
+  the HIP verify-attention kernel behind
+  ``BatchPrefillWithPagedKVCacheWrapper``;
 * RMSNorm (and residual add + RMSNorm) and the SwiGLU gate are HIP kernels
   with the reference's fp32-variance arithmetic (:142-154, :482);
 * a draft made of the first ``n`` layers plus the shared embedding, final
@@ -148,9 +151,9 @@ class CausalLM:
             # residual += x (causal_lm.py:505, 531), then RMSNorm -- one kernel
             h = kernels.rmsnorm(residual if x is None else x, L["ln1"], eps,
                                 residual=None if x is None else residual)
-            qkv = kernels.linear(h, L["qkv"], L["qkv_b"])
-            q = kernels.rope_kv_write(qkv, Hq, Hkv, D, positions, self.rope_cos, self.rope_sin,
-                                      write_indices, k_pool[li], v_pool[li])
+            q = kernels.linear_rope_kv(h, L["qkv"], L["qkv_b"], Hq, Hkv, D, positions,
+                                       self.rope_cos, self.rope_sin, write_indices,
+                                       k_pool[li], v_pool[li])
             attn = attn_wrapper.run(q, (k_pool[li], v_pool[li]))
             x = kernels.linear(attn.view(-1, Hq * D), L["o"])
             h = kernels.rmsnorm(x, L["ln2"], eps, residual=residual)   # causal_lm.py:147-154

@@ -408,21 +408,33 @@ int32_t launch_cfg(LinParams p, hipStream_t s) {
 
 // Up to kRowGroup rows: one workgroup per column tile.  More rows run as
 // groups of kRowGroup rows, one workgroup per (column tile, group), with the
-// groups of a tile on one XCD.  Very wide outputs give a workgroup four
-// column tiles so that x is re-read no more than W.
+// groups of a tile on one XCD.  Tile shape per row count, measured on MI355X
+// for the shapes of the verify forward (graph replay, weights cold): the
+// workgroup count against 256 CUs decides most of it, since each CU streams
+// its workgroups' W rows at a bounded rate.
 constexpr int kWideN = 65536;
 
 template <int EPI>
 int32_t launch_epi(LinParams p, hipStream_t s) {
-  constexpr int N1 = EPI == kEpiSilu ? 2 : 1;  // one column tile per workgroup
-  p.row_groups = 1;
-  if (p.M > kRowGroup) {
-    p.row_groups = (p.M + kRowGroup - 1) / kRowGroup;
-    if (EPI == kEpiBias && p.N >= kWideN) return launch_cfg<2, 1, 4, 8, EPI>(p, s);
-    return launch_cfg<2, 1, N1, 8, EPI>(p, s);
+  p.row_groups = p.M > kRowGroup ? (p.M + kRowGroup - 1) / kRowGroup : 1;
+  if constexpr (EPI == kEpiSilu) {
+    // NT counts gate and up tiles: NT = 2 is one output column tile
+    if (p.M <= 16) return launch_cfg<1, 1, 2, 2, EPI>(p, s);
+    if (p.M <= 32) return launch_cfg<2, 1, 2, 2, EPI>(p, s);
+    if (p.M <= 64) return launch_cfg<2, 1, 2, 4, EPI>(p, s);
+    if (p.M <= 96) return launch_cfg<2, 1, 4, 4, EPI>(p, s);
+    if (p.M <= 128) return launch_cfg<2, 1, 2, 4, EPI>(p, s);
+    return launch_cfg<2, 1, 4, 2, EPI>(p, s);
+  } else {
+    if (p.N >= kWideN) {  // lm_head
+      if (p.M == 1) return launch_cfg<1, 1, 1, 8, EPI>(p, s);
+      if (p.M <= 16) return launch_cfg<1, 1, 2, 8, EPI>(p, s);
+      return launch_cfg<2, 1, 2, 4, EPI>(p, s);
+    }
+    if (p.M <= 16) return launch_cfg<1, 1, 1, 8, EPI>(p, s);
+    if (p.M <= 128) return launch_cfg<2, 1, 1, 4, EPI>(p, s);
+    return launch_cfg<2, 1, 2, 4, EPI>(p, s);
   }
-  if (p.M <= 16) return launch_cfg<1, 1, N1, 8, EPI>(p, s);
-  return launch_cfg<2, 1, N1, 8, EPI>(p, s);
 }
 
 // RoPE epilogue: a workgroup per (head, 16 rotation pairs) -- two column
@@ -439,18 +451,16 @@ int32_t launch_rope(LinParams p, hipStream_t s) {
 using namespace nsg;
 
 // Where this kernel beats hipBLASLt on MI355X (measured per shape, weights
-// streamed from HBM): up to 160 rows for K <= 2048 (q/k/v, o_proj, gate/up),
-// up to 96 for long K (down_proj), up to 16 for very wide outputs (lm_head).
+// streamed from HBM): up to 160 rows for the q/k/v, o_proj, gate/up and
+// down_proj shapes, up to 32 for very wide outputs (lm_head).
 constexpr int kFastRows = 160;
-constexpr int kFastRowsLongK = 96;
-constexpr int kFastRowsWide = 16;
-constexpr int kLongK = 4096;
+constexpr int kFastRowsWide = 32;
 
 extern "C" int32_t nsg_linear_max_rows(void) { return kMaxMT * 16; }
 
 extern "C" int32_t nsg_linear_preferred(int32_t M, int32_t N, int32_t K) {
   if (M < 1 || K % kChunk != 0 || N % 4 != 0) return 0;
-  const int rows = N >= kWideN ? kFastRowsWide : (K >= kLongK ? kFastRowsLongK : kFastRows);
+  const int rows = N >= kWideN ? kFastRowsWide : kFastRows;
   return M <= rows ? 1 : 0;
 }
 

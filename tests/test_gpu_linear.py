@@ -37,7 +37,7 @@ def _check_bias(y, x, w, b):
     assert (err <= bound).all()
 
 
-@pytest.mark.parametrize("M", [1, 7, 16, 32, 33, 48, 80, 96, 100, 128, 160])
+@pytest.mark.parametrize("M", [1, 7, 16, 32, 33, 48, 80, 96, 100, 128, 129, 160])
 @pytest.mark.parametrize("N,K", [(1152, 896), (896, 4864), (1000, 896)])
 def test_linear_bias_matches_fp32_reference(M, N, K):
     from nanosglang_amd import kernels
@@ -49,6 +49,18 @@ def test_linear_bias_matches_fp32_reference(M, N, K):
     y0 = kernels.linear(x, w, None, force=True)
     torch.cuda.synchronize()
     _check_bias(y0, x, w, None)
+
+
+@pytest.mark.parametrize("M", [1, 2, 16, 17, 32])
+def test_linear_wide_output_matches_fp32_reference(M):
+    """Very wide outputs (lm_head: N >= 65536 columns) take their own tile
+    shapes; N is not a multiple of any workgroup's columns."""
+    from nanosglang_amd import kernels
+    print(f"case: linear wide M={M}", flush=True)
+    x, w, b = _data(M, 65540, 256, seed=40 + M)
+    y = kernels.linear(x, w, b, force=True)
+    torch.cuda.synchronize()
+    _check_bias(y, x, w, b)
 
 
 @pytest.mark.parametrize("M", [1, 32, 70, 160])
@@ -65,7 +77,7 @@ def test_linear_strided_rows_and_out_buffer(M):
     assert (base[:, 896:] == 7.0).all()                  # nothing written past N
 
 
-@pytest.mark.parametrize("M", [1, 32, 64, 96, 160])
+@pytest.mark.parametrize("M", [1, 16, 17, 32, 48, 64, 96, 100, 128, 129, 160])
 def test_linear_swiglu_matches_fp32_reference(M):
     from nanosglang_amd import kernels
     I, K = 4864, 896
@@ -88,7 +100,8 @@ def test_linear_large_m_uses_library_gemm_with_same_semantics():
     lib = load()
     assert lib.nsg_linear_preferred(32, 1152, 896) == 1
     assert lib.nsg_linear_preferred(300, 1152, 896) == 0
-    assert lib.nsg_linear_preferred(32, 151936, 896) == 0
+    assert lib.nsg_linear_preferred(32, 151936, 896) == 1
+    assert lib.nsg_linear_preferred(33, 151936, 896) == 0
     x, w, b = _data(300, 1152, 896, seed=3)
     _check_bias(kernels.linear(x, w, b), x, w, b)
     xs, ws, _ = _data(300, 4864, 896, seed=4, rows=2 * 4864)

@@ -15,79 +15,118 @@ namespace nsg {
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-constexpr int kNormThreads = 128;
+constexpr int kNormThreads = 256;  // four rows per workgroup
 
-__device__ __forceinline__ float block_sum(float v, float* sh) {
-  v = wave_sum(v);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) sh[wave] = v;
-  __syncthreads();
-  float t = 0.f;
-  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += sh[w];
-  __syncthreads();
-  return t;
-}
-
-// One workgroup per token row; each thread owns 8-element chunks (16 bytes).
-// H must be a multiple of 8 and at most kNormThreads * 8 * kMaxChunks.
-template <bool ADD>
-__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
-    const uint16_t* __restrict__ x, uint16_t* __restrict__ residual,
-    const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int H, float eps) {
-  constexpr int kMaxChunks = 8;  // H <= 128 * 8 * 8 = 8192
-  __shared__ float sh[kNormThreads / 64];
-  const int64_t row = blockIdx.x;
-  const int nch = H / 8;
-  float v[kMaxChunks][8];
-  float ss = 0.f;
+// Up to R rows of H bf16 values (H % 8 == 0, H <= 512 C), one wave: lane l
+// owns 16-byte chunks l + 64 c, c < C.  With ADD, s = bf16(x + residual) is
+// written back to residual first (a bf16 add, one rounding); otherwise s = x.
+// Then out = bf16(w * (s * rsqrt(mean(s^2) + eps))), products in fp32.  The
+// sum of squares runs per lane in chunk and element order (fused
+// multiply-adds), then over the wave by xor-butterfly: one fixed order.
+// row[0] must be a valid row; row[r] < 0 skips row r (r > 0).  Every load
+// of the batch is issued unconditionally (skipped rows and chunks past H
+// read row[0] and the last chunk instead; their values are never used) and
+// before the first use, so R rows cost one memory latency: a load under a
+// branch would make the wait-count pass wait for each load in turn.
+template <bool ADD, int R, int C>
+__device__ __forceinline__ void norm_rows(const uint16_t* x, int64_t ldx, uint16_t* residual,
+                                          int64_t ldr, const uint16_t* w, uint16_t* out,
+                                          int64_t ldo, const int (&row)[R], int H, float eps,
+                                          int lane) {
+  const int nch = H >> 3;
+  u32x4 a[R][C], b[R][C], wv[C];
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) {
-    const int ch = threadIdx.x + c * kNormThreads;
-    if (ch < nch) {
-      const u32x4 a = *reinterpret_cast<const u32x4*>(x + row * H + ch * 8);
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int64_t rl = row[r] >= 0 ? row[r] : row[0];
+      const int chl = min(lane + 64 * c, nch - 1);
+      a[r][c] = *reinterpret_cast<const u32x4*>(x + rl * ldx + chl * 8);
+      if constexpr (ADD) b[r][c] = *reinterpret_cast<const u32x4*>(residual + rl * ldr + chl * 8);
+    }
+#pragma unroll
+  for (int c = 0; c < C; ++c)
+    wv[c] = *reinterpret_cast<const u32x4*>(w + min(lane + 64 * c, nch - 1) * 8);
+  float ss[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    ss[r] = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int ch = lane + 64 * c;
+      if (row[r] < 0 || ch >= nch) continue;
       if constexpr (ADD) {
-        const u32x4 r = *reinterpret_cast<const u32x4*>(residual + row * H + ch * 8);
         u32x4 s;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float lo = bf16_bits_to_float(a[i] & 0xffff) + bf16_bits_to_float(r[i] & 0xffff);
-          const float hi = bf16_bits_to_float(a[i] >> 16) + bf16_bits_to_float(r[i] >> 16);
-          s[i] = pack_bf16x2(lo, hi);
-        }
-        *reinterpret_cast<u32x4*>(residual + row * H + ch * 8) = s;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[c][2 * i] = bf16_bits_to_float(s[i] & 0xffff);
-          v[c][2 * i + 1] = bf16_bits_to_float(s[i] >> 16);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[c][2 * i] = bf16_bits_to_float(a[i] & 0xffff);
-          v[c][2 * i + 1] = bf16_bits_to_float(a[i] >> 16);
-        }
+        for (int i = 0; i < 4; ++i)
+          s[i] = pack_bf16x2(
+              bf16_bits_to_float(a[r][c][i] & 0xffffu) + bf16_bits_to_float(b[r][c][i] & 0xffffu),
+              bf16_bits_to_float(a[r][c][i] >> 16) + bf16_bits_to_float(b[r][c][i] >> 16));
+        *reinterpret_cast<u32x4*>(residual + row[r] * ldr + ch * 8) = s;
+        a[r][c] = s;
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ss += v[c][i] * v[c][i];
+      for (int i = 0; i < 4; ++i) {
+        const float lo = bf16_bits_to_float(a[r][c][i] & 0xffffu);
+        const float hi = bf16_bits_to_float(a[r][c][i] >> 16);
+        ss[r] = __builtin_fmaf(lo, lo, ss[r]);
+        ss[r] = __builtin_fmaf(hi, hi, ss[r]);
+      }
     }
   }
-  const float var = block_sum(ss, sh) / (float)H;
-  const float r = 1.f / sqrtf(var + eps);
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) {
-    const int ch = threadIdx.x + c * kNormThreads;
-    if (ch < nch) {
-      const u32x4 wv = *reinterpret_cast<const u32x4*>(w + ch * 8);
+  for (int r = 0; r < R; ++r) ss[r] = wave_sum(ss[r]);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (row[r] < 0) continue;
+    const float rs = 1.f / sqrtf(ss[r] / (float)H + eps);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int ch = lane + 64 * c;
+      if (ch >= nch) continue;
       u32x4 o;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float lo = bf16_bits_to_float(wv[i] & 0xffff) * (v[c][2 * i] * r);
-        const float hi = bf16_bits_to_float(wv[i] >> 16) * (v[c][2 * i + 1] * r);
+        const float lo = bf16_bits_to_float(wv[c][i] & 0xffffu) *
+                         (bf16_bits_to_float(a[r][c][i] & 0xffffu) * rs);
+        const float hi = bf16_bits_to_float(wv[c][i] >> 16) *
+                         (bf16_bits_to_float(a[r][c][i] >> 16) * rs);
         o[i] = pack_bf16x2(lo, hi);
       }
-      *reinterpret_cast<u32x4*>(out + row * H + ch * 8) = o;
+      *reinterpret_cast<u32x4*>(out + row[r] * ldo + ch * 8) = o;
     }
   }
+}
+
+
+// One wave per token row; C 16-byte chunks per lane cover H <= 512 C.
+template <bool ADD, int C>
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
+    const uint16_t* __restrict__ x, uint16_t* __restrict__ residual,
+    const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int T, int H, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * (kNormThreads / 64) + (threadIdx.x >> 6);
+  if (t >= T) return;  // wave-uniform
+  const int row[1] = {t};
+  norm_rows<ADD, 1, C>(x, H, residual, H, w, out, H, row, H, eps, lane);
+}
+
+template <bool ADD>
+void launch_rmsnorm(const uint16_t* x, uint16_t* residual, const uint16_t* w, uint16_t* out,
+                    int T, int H, float eps, hipStream_t s) {
+  const dim3 grid((T + kNormThreads / 64 - 1) / (kNormThreads / 64));
+  if (H <= 1024)
+    hipLaunchKernelGGL((rmsnorm_kernel<ADD, 2>), grid, dim3(kNormThreads), 0, s, x, residual, w,
+                       out, T, H, eps);
+  else if (H <= 2048)
+    hipLaunchKernelGGL((rmsnorm_kernel<ADD, 4>), grid, dim3(kNormThreads), 0, s, x, residual, w,
+                       out, T, H, eps);
+  else if (H <= 4096)
+    hipLaunchKernelGGL((rmsnorm_kernel<ADD, 8>), grid, dim3(kNormThreads), 0, s, x, residual, w,
+                       out, T, H, eps);
+  else
+    hipLaunchKernelGGL((rmsnorm_kernel<ADD, 16>), grid, dim3(kNormThreads), 0, s, x, residual, w,
+                       out, T, H, eps);
 }
 
 // out[t, j] = bf16(bf16(silu(gu[t, j])) * gu[t, I + j]) for j < I.
@@ -127,22 +166,19 @@ extern "C" int32_t nsg_rmsnorm(const void* x, void* residual, const void* weight
     return NSG_OK;
   }
   NSG_CHECK_ARG(x && weight && out, "null pointer argument");
-  NSG_CHECK_ARG(hidden > 0 && hidden % 8 == 0 && hidden <= kNormThreads * 8 * 8,
+  NSG_CHECK_ARG(hidden > 0 && hidden % 8 == 0 && hidden <= 8192,
                 "hidden %d must be a multiple of 8 and at most 8192", hidden);
   NSG_CHECK_ARG(((uintptr_t)x | (uintptr_t)weight | (uintptr_t)out |
                  (uintptr_t)residual) % 16 == 0, "tensors must be 16-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (residual) {
-    hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(num_tokens), dim3(kNormThreads), 0, s,
-                       static_cast<const uint16_t*>(x), static_cast<uint16_t*>(residual),
-                       static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out),
-                       hidden, eps);
-  } else {
-    hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3(num_tokens), dim3(kNormThreads), 0, s,
-                       static_cast<const uint16_t*>(x), static_cast<uint16_t*>(nullptr),
-                       static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out),
-                       hidden, eps);
-  }
+  if (residual)
+    launch_rmsnorm<true>(static_cast<const uint16_t*>(x), static_cast<uint16_t*>(residual),
+                         static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out),
+                         num_tokens, hidden, eps, s);
+  else
+    launch_rmsnorm<false>(static_cast<const uint16_t*>(x), nullptr,
+                          static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out),
+                          num_tokens, hidden, eps, s);
   return launch_status("rmsnorm_kernel");
 }
 

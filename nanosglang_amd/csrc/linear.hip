@@ -489,7 +489,7 @@ extern "C" int32_t nsg_linear(const void* x, int64_t ldx, const void* w, int64_t
                     ((uintptr_t)x | (uintptr_t)w) % 16 == 0 && (uintptr_t)y % 8 == 0 &&
                     (uintptr_t)bias % 8 == 0,
                 "x and w rows must be 16-byte aligned, y rows and bias 8-byte aligned");
-  LinParams p;
+  LinParams p{};
   p.x = static_cast<const bf16*>(x);
   p.w = static_cast<const bf16*>(w);
   p.bias = static_cast<const bf16*>(bias);

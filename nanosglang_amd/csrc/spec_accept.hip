@@ -1042,7 +1042,7 @@ extern "C" int32_t nsg_spec_accept(const void* target_logits, int64_t target_req
               (long long)L.total);
     return NSG_ERR_WORKSPACE;
   }
-  AccParams p;
+  AccParams p{};
   p.tl = target_logits;
   p.t_req = target_req_stride;
   p.t_row = target_row_stride;

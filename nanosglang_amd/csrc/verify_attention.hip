@@ -856,7 +856,7 @@ extern "C" int32_t nsg_attn_run(const nsg_attn_plan_t* plan, const int32_t* work
               (long long)plan->workspace_bytes);
     return NSG_ERR_WORKSPACE;
   }
-  AttnParams prm;
+  AttnParams prm{};
   prm.q = static_cast<const bf16*>(q);
   prm.kc = static_cast<const bf16*>(k_cache);
   prm.vc = static_cast<const bf16*>(v_cache);

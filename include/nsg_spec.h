@@ -42,7 +42,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 6
+#define NSG_ABI_VERSION 7
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -241,6 +241,27 @@ int32_t nsg_linear_preferred(int32_t M, int32_t N, int32_t K);
 int32_t nsg_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias,
                    void* y, int64_t ldy, int32_t M, int32_t N, int32_t K, int32_t epilogue,
                    nsg_stream_t stream);
+
+/* FP8 weights (FP8Linear, nano_sglang/decode/quantization.py:24-75): w8 holds
+ * OCP e4m3fn bytes (row stride ldw8 bytes, rows 8-byte aligned) and w_scale
+ * one f32 per weight row (a per-tensor scale repeated over the tensor's rows;
+ * several tensors stacked -- q/k/v, gate/up -- keep their own scales).  Each
+ * weight is dequantised to bf16(float(w8) * w_scale[row]), the arithmetic of
+ * FP8Linear.forward's w8.to(bf16) * scale (:49-52), and the product then runs
+ * exactly as nsg_linear / nsg_linear_rope_kv on those bf16 weights (bf16 MFMA,
+ * fp32 accumulation), streaming half the weight bytes.  SwiGLU: w8 and
+ * w_scale have 2N rows.  Other arguments as in the bf16 entry points. */
+int32_t nsg_linear_fp8(const void* x, int64_t ldx, const void* w8, int64_t ldw8,
+                       const float* w_scale, const void* bias, void* y, int64_t ldy, int32_t M,
+                       int32_t N, int32_t K, int32_t epilogue, nsg_stream_t stream);
+int32_t nsg_linear_rope_kv_fp8(const void* x, int64_t ldx, const void* w8, int64_t ldw8,
+                               const float* w_scale, const void* bias, int32_t M, int32_t K,
+                               int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                               const int64_t* positions, const float* cos_table,
+                               const float* sin_table, int32_t max_position,
+                               const int64_t* slots, void* q_out, void* k_cache,
+                               void* v_cache, int64_t num_slots, int32_t* flags,
+                               nsg_stream_t stream);
 
 /* The q/k/v projection with RoPE and the KV-slot write as its epilogue:
  * nsg_linear (NSG_LINEAR_BIAS) of x (M x K) with the fused q/k/v weight w

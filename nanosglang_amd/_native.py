@@ -13,7 +13,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libnsg_spec.so")
 
 NSG_ATTN_WORK_INTS = 8
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 i32, i64, u32, u64, f32 = C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_float
 vp = C.c_void_p
@@ -42,6 +42,9 @@ SIGNATURES = {
     "nsg_linear_max_rows": (i32, []),
     "nsg_linear_preferred": (i32, [i32, i32, i32]),
     "nsg_linear": (i32, [vp, i64, vp, i64, vp, vp, i64, i32, i32, i32, i32, vp]),
+    "nsg_linear_fp8": (i32, [vp, i64, vp, i64, vp, vp, vp, i64, i32, i32, i32, i32, vp]),
+    "nsg_linear_rope_kv_fp8": (i32, [vp, i64, vp, i64, vp, vp, i32, i32, i32, i32, i32, vp, vp,
+                                     vp, i32, vp, vp, vp, vp, i64, vp, vp]),
     "nsg_linear_rope_kv": (i32, [vp, i64, vp, i64, vp, i32, i32, i32, i32, i32, vp, vp, vp,
                                  i32, vp, vp, vp, vp, i64, vp, vp]),
     "nsg_attn_run": (i32, [C.POINTER(AttnPlan), vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32,

@@ -24,6 +24,7 @@
 //   fused [gate; up] rows, and y = bf16(bf16(silu(bf16(g))) * bf16(u)), the
 //   rounding order of F.silu(gate) * up on bf16 tensors (causal_lm.py:482).
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -39,6 +40,10 @@ constexpr int kMaxMT = 10;  // up to 160 rows of x
 struct LinParams {
   const bf16* x;
   const bf16* w;
+  // FP8 weights (e4m3fn bytes, row stride ldw bytes) and one f32 scale per W
+  // row: W[n, k] = bf16(float(w8[n, k]) * w_scale[n])
+  const uint8_t* w8;
+  const float* w_scale;
   const bf16* bias;
   bf16* y;
   int64_t ldx, ldw, ldy;
@@ -77,7 +82,19 @@ __device__ __forceinline__ float silu_bf16(float g) {
 // MG * NW waves form MG groups of NW: group g owns m tiles [g MT, g MT + MT)
 // and its NW waves split K (more rows per wave would not fit the registers of
 // two load stages; the groups read the same W rows, the second from L2).
-template <int MT, int MG, int NT, int NW, int EPI>
+// One OCP e4m3fn byte pair -> two floats (gfx950's v_cvt_pk_f32_fp8, exact),
+// then the row scale and one bf16 rounding: the dequantisation
+// w8.to(bf16) * scale of FP8Linear.forward (quantization.py:49-52).
+__device__ __forceinline__ u32x4 dequant_fp8x8(u32x2 v, float s) {
+  const floatx2_t f0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)v[0], false);
+  const floatx2_t f1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)v[0], true);
+  const floatx2_t f2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)v[1], false);
+  const floatx2_t f3 = __builtin_amdgcn_cvt_pk_f32_fp8((int)v[1], true);
+  return u32x4{pack_bf16x2(f0[0] * s, f0[1] * s), pack_bf16x2(f1[0] * s, f1[1] * s),
+               pack_bf16x2(f2[0] * s, f2[1] * s), pack_bf16x2(f3[0] * s, f3[1] * s)};
+}
+
+template <int MT, int MG, int NT, int NW, int EPI, bool W8 = false>
 __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
   static_assert(EPI != kEpiSilu || NT % 2 == 0, "SwiGLU pairs gate and up tiles");
   constexpr int NP = EPI == kEpiSilu ? 2 : 1;  // physical tiles reduced together
@@ -118,6 +135,8 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
   const int lseg = (lane & 3) * 8;
   const int perm_src = 4 * (4 * r16 + (lane >> 4));  // byte address of the source lane
   const bf16* wp[NT];
+  const uint8_t* wp8[NT];
+  float wsc[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     int row;
@@ -133,7 +152,18 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
       row = (tile * NT + nt) * 16 + lrow;
     }
     row = min(row, p.w_rows - 1);
-    wp[nt] = p.w + (int64_t)row * p.ldw + lseg;
+    if constexpr (W8) {
+      // FP8: lane l reads the 8 bytes (k 8 (l % 4) .. + 8 of each 32-k half)
+      // that dequantise to exactly the 8 bf16 the bf16 path's 16-byte load
+      // gives it, so the MFMA lane mapping below is the same
+      wp8[nt] = p.w8 + (int64_t)row * p.ldw + lseg;
+      wsc[nt] = p.w_scale[row];
+      wp[nt] = nullptr;
+    } else {
+      wp[nt] = p.w + (int64_t)row * p.ldw + lseg;
+      wp8[nt] = nullptr;
+      wsc[nt] = 1.f;
+    }
   }
   const bf16* xp[MT];
 #pragma unroll
@@ -158,15 +188,22 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
   const int rot = (int)((unsigned)tile % (unsigned)nchunks);
   // two register stages: loads of chunk c + NW are in flight while chunk c
   // is multiplied
-  u32x4 wa[NT][2], xa[MT][2], wb[NT][2], xb[MT][2];
-  auto load = [&](int c, u32x4 (&wv)[NT][2], u32x4 (&xv)[MT][2]) {
+  using WReg = typename std::conditional<W8, u32x2, u32x4>::type;
+  WReg wa[NT][2], wb[NT][2];
+  u32x4 xa[MT][2], xb[MT][2];
+  auto load = [&](int c, WReg (&wv)[NT][2], u32x4 (&xv)[MT][2]) {
     int cr = c + rot;
     cr = cr >= nchunks ? cr - nchunks : cr;
     const int k0 = cr * kChunk;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      wv[nt][0] = *reinterpret_cast<const u32x4*>(wp[nt] + k0);
-      wv[nt][1] = *reinterpret_cast<const u32x4*>(wp[nt] + k0 + 32);
+      if constexpr (W8) {
+        wv[nt][0] = *reinterpret_cast<const u32x2*>(wp8[nt] + k0);
+        wv[nt][1] = *reinterpret_cast<const u32x2*>(wp8[nt] + k0 + 32);
+      } else {
+        wv[nt][0] = *reinterpret_cast<const u32x4*>(wp[nt] + k0);
+        wv[nt][1] = *reinterpret_cast<const u32x4*>(wp[nt] + k0 + 32);
+      }
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -174,12 +211,17 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
       xv[mt][1] = *reinterpret_cast<const u32x4*>(xp[mt] + k0 + 32);
     }
   };
-  auto mma = [&](const u32x4 (&wv)[NT][2], const u32x4 (&xv)[MT][2]) {
+  auto mma = [&](const WReg (&wv)[NT][2], const u32x4 (&xv)[MT][2]) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       bf16x8 wf[NT], xf[MT];
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) wf[nt] = to_mfma(wv[nt][h]);
+      for (int nt = 0; nt < NT; ++nt) {
+        if constexpr (W8)
+          wf[nt] = to_mfma(dequant_fp8x8(wv[nt][h], wsc[nt]));
+        else
+          wf[nt] = to_mfma(wv[nt][h]);
+      }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) xf[mt] = to_mfma(xv[mt][h]);
 #pragma unroll
@@ -397,6 +439,15 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
 // (read from L2 once per workgroup) stays a small multiple of W's bytes.
 template <int MT, int MG, int NT, int NW, int EPI>
 int32_t launch_cfg(LinParams p, hipStream_t s) {
+  if (p.w8) {
+    const int cols_per_wg = 16 * (EPI == kEpiSilu ? NT / 2 : NT);
+    p.col_tiles = (p.N + cols_per_wg - 1) / cols_per_wg;
+    int grid = p.col_tiles;
+    if (p.row_groups > 1) grid = p.row_groups * 8 * ((p.col_tiles + 7) / 8);
+    hipLaunchKernelGGL((linear_kernel<MT, MG, NT, NW, EPI, true>), dim3(grid), dim3(MG * NW * 64),
+                       0, s, p);
+    return launch_status("linear_kernel");
+  }
   const int cols_per_wg = 16 * (EPI == kEpiSilu ? NT / 2 : NT);
   p.col_tiles = (p.N + cols_per_wg - 1) / cols_per_wg;
   int grid = p.col_tiles;
@@ -451,28 +502,37 @@ int32_t launch_rope(LinParams p, hipStream_t s) {
 using namespace nsg;
 
 // Where this kernel beats hipBLASLt on MI355X (measured per shape, weights
-// streamed from HBM): up to 160 rows for the q/k/v, o_proj, gate/up and
-// down_proj shapes, up to 32 for very wide outputs (lm_head).
+// streamed from HBM): up to 160 rows for the 0.5B-class q/k/v, o_proj,
+// gate/up and down_proj shapes (weights up to 17 MB), up to 32 for very wide
+// outputs (lm_head) and for weights of 16 M elements or more (8B-class
+// layers, where the library's tiles win from about 64 rows).
 constexpr int kFastRows = 160;
 constexpr int kFastRowsWide = 32;
+constexpr int kFastRowsBig = 32;
+constexpr int64_t kBigWeight = 16ll << 20;
 
 extern "C" int32_t nsg_linear_max_rows(void) { return kMaxMT * 16; }
 
 extern "C" int32_t nsg_linear_preferred(int32_t M, int32_t N, int32_t K) {
   if (M < 1 || K % kChunk != 0 || N % 4 != 0) return 0;
-  const int rows = N >= kWideN ? kFastRowsWide : kFastRows;
+  const int rows = N >= kWideN ? kFastRowsWide
+                  : ((int64_t)N * K >= kBigWeight ? kFastRowsBig : kFastRows);
   return M <= rows ? 1 : 0;
 }
 
-extern "C" int32_t nsg_linear(const void* x, int64_t ldx, const void* w, int64_t ldw,
-                              const void* bias, void* y, int64_t ldy, int32_t M, int32_t N,
-                              int32_t K, int32_t epilogue, nsg_stream_t stream) {
+namespace {
+
+// Shared by the bf16 and FP8-weight entry points: exactly one of w / w8 is
+// given; w8 rows are ldw bytes apart and w_scale holds one f32 per W row.
+int32_t linear_impl(const void* x, int64_t ldx, const void* w, const void* w8, int64_t ldw,
+                    const float* w_scale, const void* bias, void* y, int64_t ldy, int32_t M,
+                    int32_t N, int32_t K, int32_t epilogue, nsg_stream_t stream) {
   NSG_CHECK_ARG(M >= 0 && N > 0 && K > 0, "M %d, N %d, K %d", M, N, K);
   if (M == 0) {
     clear_error();
     return NSG_OK;
   }
-  NSG_CHECK_ARG(x && w && y, "null pointer argument");
+  NSG_CHECK_ARG(x && (w || (w8 && w_scale)) && y, "null pointer argument");
   NSG_CHECK_ARG(epilogue == NSG_LINEAR_BIAS || epilogue == NSG_LINEAR_SILU_MUL,
                 "unknown epilogue %d", epilogue);
   NSG_CHECK_ARG(!(epilogue == NSG_LINEAR_SILU_MUL && bias), "SwiGLU epilogue takes no bias");
@@ -485,13 +545,15 @@ extern "C" int32_t nsg_linear(const void* x, int64_t ldx, const void* w, int64_t
     return NSG_ERR_UNSUPPORTED;
   }
   NSG_CHECK_ARG(ldx >= K && ldw >= K && ldy >= N, "leading dimensions too small");
-  NSG_CHECK_ARG(ldx % 8 == 0 && ldw % 8 == 0 && ldy % 4 == 0 &&
-                    ((uintptr_t)x | (uintptr_t)w) % 16 == 0 && (uintptr_t)y % 8 == 0 &&
+  NSG_CHECK_ARG(ldx % 8 == 0 && ldw % 8 == 0 && ldy % 4 == 0 && (uintptr_t)x % 16 == 0 &&
+                    (w ? (uintptr_t)w % 16 : (uintptr_t)w8 % 8) == 0 && (uintptr_t)y % 8 == 0 &&
                     (uintptr_t)bias % 8 == 0,
-                "x and w rows must be 16-byte aligned, y rows and bias 8-byte aligned");
+                "x and bf16 w rows must be 16-byte aligned, fp8 w rows, y rows and bias 8-byte");
   LinParams p{};
   p.x = static_cast<const bf16*>(x);
   p.w = static_cast<const bf16*>(w);
+  p.w8 = w ? nullptr : static_cast<const uint8_t*>(w8);
+  p.w_scale = w ? nullptr : w_scale;
   p.bias = static_cast<const bf16*>(bias);
   p.y = static_cast<bf16*>(y);
   p.ldx = ldx;
@@ -505,20 +567,19 @@ extern "C" int32_t nsg_linear(const void* x, int64_t ldx, const void* w, int64_t
   return epilogue == NSG_LINEAR_SILU_MUL ? launch_epi<kEpiSilu>(p, s) : launch_epi<kEpiBias>(p, s);
 }
 
-extern "C" int32_t nsg_linear_rope_kv(const void* x, int64_t ldx, const void* w, int64_t ldw,
-                                      const void* bias, int32_t M, int32_t K,
-                                      int32_t num_qo_heads, int32_t num_kv_heads,
-                                      int32_t head_dim, const int64_t* positions,
-                                      const float* cos_table, const float* sin_table,
-                                      int32_t max_position, const int64_t* slots, void* q_out,
-                                      void* k_cache, void* v_cache, int64_t num_slots,
-                                      int32_t* flags, nsg_stream_t stream) {
+int32_t rope_impl(const void* x, int64_t ldx, const void* w, const void* w8, int64_t ldw,
+                  const float* w_scale, const void* bias, int32_t M, int32_t K,
+                  int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                  const int64_t* positions, const float* cos_table, const float* sin_table,
+                  int32_t max_position, const int64_t* slots, void* q_out, void* k_cache,
+                  void* v_cache, int64_t num_slots, int32_t* flags, nsg_stream_t stream) {
   NSG_CHECK_ARG(M >= 0 && K > 0, "M %d, K %d", M, K);
   if (M == 0) {
     clear_error();
     return NSG_OK;
   }
-  NSG_CHECK_ARG(x && w && positions && cos_table && sin_table && q_out, "null pointer argument");
+  NSG_CHECK_ARG(x && (w || (w8 && w_scale)) && positions && cos_table && sin_table && q_out,
+                "null pointer argument");
   NSG_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0, "heads %d / %d", num_qo_heads, num_kv_heads);
   NSG_CHECK_ARG(!slots || (k_cache && v_cache && num_slots > 0), "slots need both caches");
   if (head_dim != 64 && head_dim != 128) {
@@ -530,14 +591,16 @@ extern "C" int32_t nsg_linear_rope_kv(const void* x, int64_t ldx, const void* w,
     return NSG_ERR_UNSUPPORTED;
   }
   const int N = (num_qo_heads + 2 * num_kv_heads) * head_dim;
-  NSG_CHECK_ARG(ldx >= K && ldw >= K && ldx % 8 == 0 && ldw % 8 == 0 &&
-                    ((uintptr_t)x | (uintptr_t)w) % 16 == 0,
-                "x and w rows must be 16-byte aligned");
+  NSG_CHECK_ARG(ldx >= K && ldw >= K && ldx % 8 == 0 && ldw % 8 == 0 && (uintptr_t)x % 16 == 0 &&
+                    (w ? (uintptr_t)w % 16 : (uintptr_t)w8 % 8) == 0,
+                "x and bf16 w rows must be 16-byte aligned, fp8 w rows 8-byte");
   NSG_CHECK_ARG(max_position > 0, "max_position %d", max_position);
   NSG_CHECK_ARG((uintptr_t)bias % 8 == 0, "bias must be 8-byte aligned");
   LinParams p{};
   p.x = static_cast<const bf16*>(x);
   p.w = static_cast<const bf16*>(w);
+  p.w8 = w ? nullptr : static_cast<const uint8_t*>(w8);
+  p.w_scale = w ? nullptr : w_scale;
   p.bias = static_cast<const bf16*>(bias);
   p.y = nullptr;
   p.ldx = ldx;
@@ -560,6 +623,51 @@ extern "C" int32_t nsg_linear_rope_kv(const void* x, int64_t ldx, const void* w,
   p.vc = static_cast<bf16*>(v_cache);
   p.num_slots = num_slots;
   p.flags = flags;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  return launch_rope(p, s);
+  return launch_rope(p, static_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+
+extern "C" int32_t nsg_linear(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                              const void* bias, void* y, int64_t ldy, int32_t M, int32_t N,
+                              int32_t K, int32_t epilogue, nsg_stream_t stream) {
+  NSG_CHECK_ARG(w, "null weight");
+  return linear_impl(x, ldx, w, nullptr, ldw, nullptr, bias, y, ldy, M, N, K, epilogue, stream);
+}
+
+extern "C" int32_t nsg_linear_fp8(const void* x, int64_t ldx, const void* w8, int64_t ldw8,
+                                  const float* w_scale, const void* bias, void* y, int64_t ldy,
+                                  int32_t M, int32_t N, int32_t K, int32_t epilogue,
+                                  nsg_stream_t stream) {
+  NSG_CHECK_ARG(w8 && w_scale, "null fp8 weight or scales");
+  return linear_impl(x, ldx, nullptr, w8, ldw8, w_scale, bias, y, ldy, M, N, K, epilogue, stream);
+}
+
+extern "C" int32_t nsg_linear_rope_kv(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                      const void* bias, int32_t M, int32_t K,
+                                      int32_t num_qo_heads, int32_t num_kv_heads,
+                                      int32_t head_dim, const int64_t* positions,
+                                      const float* cos_table, const float* sin_table,
+                                      int32_t max_position, const int64_t* slots, void* q_out,
+                                      void* k_cache, void* v_cache, int64_t num_slots,
+                                      int32_t* flags, nsg_stream_t stream) {
+  NSG_CHECK_ARG(w, "null weight");
+  return rope_impl(x, ldx, w, nullptr, ldw, nullptr, bias, M, K, num_qo_heads, num_kv_heads,
+                   head_dim, positions, cos_table, sin_table, max_position, slots, q_out, k_cache,
+                   v_cache, num_slots, flags, stream);
+}
+
+extern "C" int32_t nsg_linear_rope_kv_fp8(const void* x, int64_t ldx, const void* w8,
+                                          int64_t ldw8, const float* w_scale, const void* bias,
+                                          int32_t M, int32_t K, int32_t num_qo_heads,
+                                          int32_t num_kv_heads, int32_t head_dim,
+                                          const int64_t* positions, const float* cos_table,
+                                          const float* sin_table, int32_t max_position,
+                                          const int64_t* slots, void* q_out, void* k_cache,
+                                          void* v_cache, int64_t num_slots, int32_t* flags,
+                                          nsg_stream_t stream) {
+  NSG_CHECK_ARG(w8 && w_scale, "null fp8 weight or scales");
+  return rope_impl(x, ldx, nullptr, w8, ldw8, w_scale, bias, M, K, num_qo_heads, num_kv_heads,
+                   head_dim, positions, cos_table, sin_table, max_position, slots, q_out, k_cache,
+                   v_cache, num_slots, flags, stream);
 }

@@ -482,43 +482,77 @@ def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Te
 
 
 LINEAR_BIAS, LINEAR_SILU_MUL = 0, 1
+FP8 = torch.float8_e4m3fn
+
+
+def dequant_fp8(w8: torch.Tensor, w_scale: torch.Tensor) -> torch.Tensor:
+    """bf16(float(w8) * w_scale[row]): the weights the FP8 kernels multiply
+    (FP8Linear.forward's ``w8.to(bf16) * scale``, quantization.py:49-52)."""
+    return (w8.float() * w_scale.float()[:, None]).to(torch.bfloat16)
+
+
+def _check_fp8(weight, w_scale, K):
+    if weight.dtype != FP8:
+        if w_scale is not None:
+            raise ValueError("w_scale is only for float8_e4m3fn weights")
+        return False
+    if w_scale is None or w_scale.dtype != torch.float32 or not w_scale.is_contiguous() or \
+            w_scale.numel() != weight.shape[0] or w_scale.device != weight.device:
+        raise ValueError("float8_e4m3fn weights need an fp32 w_scale with one entry per row")
+    if weight.stride(1) != 1 or weight.shape[1] != K or weight.stride(0) % 8 or \
+            weight.data_ptr() % 8:
+        raise ValueError("fp8 weight must be (N, K) with unit inner stride, rows 8-byte aligned")
+    return True
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
            swiglu: bool = False, out: torch.Tensor | None = None,
-           force: bool = False) -> torch.Tensor:
+           force: bool = False, w_scale: torch.Tensor | None = None) -> torch.Tensor:
     """y = x @ weight.T (+ bias) for bf16 (M, K) rows (C ABI: nsg_linear).
 
     ``swiglu``: weight holds the fused [gate; up] rows (2I, K) and the
-    result is bf16(silu(gate)) * up, (M, I).  Shapes where the library is
-    faster (``nsg_linear_preferred``: many rows, prefill) go to hipBLASLt via
-    F.linear, plus the SwiGLU kernel; ``force`` runs nsg_linear whenever it
-    supports the shape (tests)."""
+    result is bf16(silu(gate)) * up, (M, I).  ``weight`` may be
+    float8_e4m3fn with fp32 per-row ``w_scale`` (C ABI: nsg_linear_fp8):
+    the weights are then ``dequant_fp8(weight, w_scale)``.  Shapes where the
+    library is faster (``nsg_linear_preferred``: many rows, prefill) go to
+    hipBLASLt via F.linear (on the dequantised weights), plus the SwiGLU
+    kernel; ``force`` runs the HIP kernel whenever it supports the shape
+    (tests)."""
     _require_gpu(x, "x")
     M, K = x.shape
     rows = weight.shape[0]
     N = rows // 2 if swiglu else rows
     lib = _lib()
+    fp8 = _check_fp8(weight, w_scale, K)
     fits = (M <= lib.nsg_linear_max_rows() and K % 64 == 0 and N % 4 == 0 and x.stride(1) == 1
             and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0 and x.dtype == torch.bfloat16)
-    if not fits or not (force or lib.nsg_linear_preferred(M, N, K)):
-        y = torch.nn.functional.linear(x, weight, bias)
+    # FP8 weights stay on the kernel whenever it fits: the library path would
+    # first write the dequantised bf16 weights (three times the FP8 bytes)
+    if not fits or not (force or fp8 or lib.nsg_linear_preferred(M, N, K)):
+        w = dequant_fp8(weight, w_scale) if fp8 else weight
+        y = torch.nn.functional.linear(x, w, bias)
         if swiglu:
             return silu_mul(y, out)
         if out is not None:
             out.copy_(y)
             return out
         return y
-    if weight.dtype != torch.bfloat16 or weight.stride(1) != 1 or weight.shape[1] != K:
+    if not fp8 and (weight.dtype != torch.bfloat16 or weight.stride(1) != 1
+                    or weight.shape[1] != K):
         raise ValueError("weight must be bf16 (N, K) with unit inner stride")
     if bias is not None and (bias.dtype != torch.bfloat16 or not bias.is_contiguous()):
         raise ValueError("bias must be contiguous bf16")
     if out is None:
         out = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
-    check(lib.nsg_linear(x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
-                         _ptr(bias), out.data_ptr(), out.stride(0), M, N, K,
-                         LINEAR_SILU_MUL if swiglu else LINEAR_BIAS, _stream_ptr(x.device)),
-          "nsg_linear")
+    epi = LINEAR_SILU_MUL if swiglu else LINEAR_BIAS
+    if fp8:
+        check(lib.nsg_linear_fp8(x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
+                                 w_scale.data_ptr(), _ptr(bias), out.data_ptr(), out.stride(0),
+                                 M, N, K, epi, _stream_ptr(x.device)), "nsg_linear_fp8")
+    else:
+        check(lib.nsg_linear(x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
+                             _ptr(bias), out.data_ptr(), out.stride(0), M, N, K, epi,
+                             _stream_ptr(x.device)), "nsg_linear")
     return out
 
 
@@ -527,8 +561,9 @@ def linear_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | N
                    positions: torch.Tensor, cos_table: torch.Tensor, sin_table: torch.Tensor,
                    slots: torch.Tensor | None, k_cache: torch.Tensor | None,
                    v_cache: torch.Tensor | None, q_out: torch.Tensor | None = None,
-                   force: bool = False) -> torch.Tensor:
-    """q/k/v projection + RoPE + KV-slot write (C ABI: nsg_linear_rope_kv).
+                   force: bool = False, w_scale: torch.Tensor | None = None) -> torch.Tensor:
+    """q/k/v projection + RoPE + KV-slot write (C ABI: nsg_linear_rope_kv, or
+    nsg_linear_rope_kv_fp8 for float8_e4m3fn weights with per-row w_scale).
 
     Same result as ``rope_kv_write(linear(x, weight, bias), ...)``; at row
     counts where the library GEMM is the faster projection (prefill), or for
@@ -538,14 +573,16 @@ def linear_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | N
     M, K = x.shape
     lib = _lib()
     N = weight.shape[0]
+    fp8 = _check_fp8(weight, w_scale, K)
     fits = (M <= lib.nsg_linear_max_rows() and K % 64 == 0 and head_dim in (64, 128)
             and N == (num_qo_heads + 2 * num_kv_heads) * head_dim and x.stride(1) == 1
             and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0 and x.dtype == torch.bfloat16)
-    if not fits or not (force or lib.nsg_linear_preferred(M, N, K)):
-        qkv = linear(x, weight, bias)
+    if not fits or not (force or fp8 or lib.nsg_linear_preferred(M, N, K)):
+        qkv = linear(x, weight, bias, w_scale=w_scale)
         return rope_kv_write(qkv, num_qo_heads, num_kv_heads, head_dim, positions, cos_table,
                              sin_table, slots, k_cache, v_cache, q_out)
-    if weight.dtype != torch.bfloat16 or weight.stride(1) != 1 or weight.shape[1] != K:
+    if not fp8 and (weight.dtype != torch.bfloat16 or weight.stride(1) != 1
+                    or weight.shape[1] != K):
         raise ValueError("weight must be bf16 (N, K) with unit inner stride")
     if bias is not None and (bias.dtype != torch.bfloat16 or not bias.is_contiguous()):
         raise ValueError("bias must be contiguous bf16")
@@ -557,12 +594,17 @@ def linear_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | N
         num_slots = k_cache.numel() // (num_kv_heads * head_dim)
     else:
         num_slots = 0
-    check(lib.nsg_linear_rope_kv(
-        x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), _ptr(bias), M, K,
-        num_qo_heads, num_kv_heads, head_dim, positions.data_ptr(), cos_table.data_ptr(),
-        sin_table.data_ptr(), cos_table.shape[0], _ptr(slots), q_out.data_ptr(),
-        _ptr(k_cache), _ptr(v_cache), num_slots, None, _stream_ptr(x.device)),
-        "nsg_linear_rope_kv")
+    tail = (num_qo_heads, num_kv_heads, head_dim, positions.data_ptr(), cos_table.data_ptr(),
+            sin_table.data_ptr(), cos_table.shape[0], _ptr(slots), q_out.data_ptr(),
+            _ptr(k_cache), _ptr(v_cache), num_slots, None, _stream_ptr(x.device))
+    if fp8:
+        check(lib.nsg_linear_rope_kv_fp8(x.data_ptr(), x.stride(0), weight.data_ptr(),
+                                         weight.stride(0), w_scale.data_ptr(), _ptr(bias), M, K,
+                                         *tail), "nsg_linear_rope_kv_fp8")
+    else:
+        check(lib.nsg_linear_rope_kv(x.data_ptr(), x.stride(0), weight.data_ptr(),
+                                     weight.stride(0), _ptr(bias), M, K, *tail),
+              "nsg_linear_rope_kv")
     return q_out
 
 

@@ -124,6 +124,25 @@ class CausalLM:
         self.lm_head = self.embed  # tie_word_embeddings
         self.rope_cos, self.rope_sin = rope_tables(c, self.device)
 
+    def quantize_fp8(self) -> "CausalLM":
+        """FP8 (E4M3) weights for every decoder layer's q/k/v, o_proj,
+        gate/up and down_proj, one per-tensor scale each (FP8Linear.from_linear,
+        nano_sglang/decode/quantization.py:54-75); embeddings, lm_head and
+        norms stay bf16, as the reference's default skip list keeps them
+        (:220-221).  In place; returns self."""
+        from .quantization import fp8_quantize_rows
+        c = self.config
+        Hq, Hkv, D, I = (c.num_attention_heads, c.num_key_value_heads, c.head_dim,
+                         c.intermediate_size)
+        for L in self.layers:
+            if "qkv_s" in L:
+                continue
+            L["qkv"], L["qkv_s"] = fp8_quantize_rows(L["qkv"], [Hq * D, Hkv * D, Hkv * D])
+            L["o"], L["o_s"] = fp8_quantize_rows(L["o"], [L["o"].shape[0]])
+            L["gate_up"], L["gate_up_s"] = fp8_quantize_rows(L["gate_up"], [I, I])
+            L["down"], L["down_s"] = fp8_quantize_rows(L["down"], [L["down"].shape[0]])
+        return self
+
     @property
     def num_layers(self) -> int:
         return self.config.num_hidden_layers
@@ -153,11 +172,13 @@ class CausalLM:
                                 residual=None if x is None else residual)
             q = kernels.linear_rope_kv(h, L["qkv"], L["qkv_b"], Hq, Hkv, D, positions,
                                        self.rope_cos, self.rope_sin, write_indices,
-                                       k_pool[li], v_pool[li])
+                                       k_pool[li], v_pool[li], w_scale=L.get("qkv_s"))
             attn = attn_wrapper.run(q, (k_pool[li], v_pool[li]))
-            x = kernels.linear(attn.view(-1, Hq * D), L["o"])
+            x = kernels.linear(attn.view(-1, Hq * D), L["o"], w_scale=L.get("o_s"))
             h = kernels.rmsnorm(x, L["ln2"], eps, residual=residual)   # causal_lm.py:147-154
-            x = kernels.linear(kernels.linear(h, L["gate_up"], swiglu=True), L["down"])
+            x = kernels.linear(kernels.linear(h, L["gate_up"], swiglu=True,
+                                              w_scale=L.get("gate_up_s")),
+                               L["down"], w_scale=L.get("down_s"))
         h = kernels.rmsnorm(x, self.norm, eps, residual=residual)
         if logit_indices is not None:
             h = h[logit_indices]

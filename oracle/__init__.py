@@ -17,6 +17,10 @@ Modules (each function cites the reference file:line it restates):
 * ``acceptance``       -- greedy and stochastic acceptance, textbook residual
                           resample, bonus token, KV-slot rollback
                           (nano_sglang/decode/speculative.py:130-196).
+* ``quantization``     -- FP8 (OCP E4M3FN) per-tensor weight quantisation and
+                          the dequantisation FP8Linear applies
+                          (nano_sglang/decode/quantization.py:24-75), pinned
+                          against torch's own float8_e4m3fn casts.
 * ``model``            -- fp32 PyTorch-CPU restatement of the Qwen2/Llama
                           decoder and the speculative loop
                           (nano_sglang/model/causal_lm.py, decode/speculative.py).

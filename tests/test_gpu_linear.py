@@ -102,6 +102,9 @@ def test_linear_large_m_uses_library_gemm_with_same_semantics():
     assert lib.nsg_linear_preferred(300, 1152, 896) == 0
     assert lib.nsg_linear_preferred(32, 151936, 896) == 1
     assert lib.nsg_linear_preferred(33, 151936, 896) == 0
+    assert lib.nsg_linear_preferred(160, 896, 4864) == 1       # 0.5B down_proj
+    assert lib.nsg_linear_preferred(64, 14336, 4096) == 0      # 8B-class weights
+    assert lib.nsg_linear_preferred(32, 14336, 4096) == 1
     x, w, b = _data(300, 1152, 896, seed=3)
     _check_bias(kernels.linear(x, w, b), x, w, b)
     xs, ws, _ = _data(300, 4864, 896, seed=4, rows=2 * 4864)
@@ -254,3 +257,136 @@ def test_linear_rope_kv_flags_bad_slot_and_position():
         assert rc == 0
         torch.cuda.synchronize()
         assert flags.item() == want
+
+
+# ---- FP8 weights (nsg_linear_fp8 / nsg_linear_rope_kv_fp8) ----
+
+def test_fp8_kernel_decodes_every_e4m3_code():
+    """One-hot x against a W8 whose row n holds code n: y[n] is the kernel's
+    dequantised weight, which must be the oracle's bf16(decode(n) * scale)
+    for all 256 codes (the OCP E4M3FN format, NaN codes included)."""
+    import numpy as np
+    from nanosglang_amd import kernels
+    from oracle.quantization import fp8_dequant_bf16
+    print("case: fp8 decode of all codes", flush=True)
+    K = 64
+    codes = torch.arange(256, dtype=torch.uint8)
+    w8 = torch.zeros(256, K, dtype=torch.uint8)
+    w8[:, 0] = codes
+    w8 = w8.view(torch.float8_e4m3fn).cuda()
+    x = torch.zeros(1, K, dtype=torch.bfloat16, device="cuda")
+    x[0, 0] = 1.0
+    for s in (1.0, 0.375, 3.0517578125e-05):       # bf16-exact scales (as applied)
+        scale = torch.full((256,), s, dtype=torch.float32, device="cuda")
+        y = kernels.linear(x, w8, None, w_scale=scale, force=True)
+        torch.cuda.synchronize()
+        got = y.float().cpu().numpy()[0]
+        want = fp8_dequant_bf16(codes.numpy(), np.float32(s))
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        assert np.array_equal(got[~np.isnan(got)], want[~np.isnan(want)])
+
+
+def test_fp8_dequant_matches_torch_on_the_gpu():
+    """FP8Linear.forward's w8.to(bf16) * scale (0-dim fp32 scale) computed by
+    torch on the GPU, the oracle's GPU form bf16(float(w8) * bf16(scale)) and
+    the kernels' dequantisation with applied_scale agree bit for bit; the
+    CPU form (scale kept in fp32) differs for most scales, so the check has
+    teeth."""
+    import numpy as np
+    from nanosglang_amd import kernels
+    from nanosglang_amd.model.quantization import applied_scale, fp8_quantize
+    from oracle.quantization import fp8_dequant_bf16
+    g = torch.Generator(device="cuda").manual_seed(3)
+    cpu_form_differs = 0
+    for t in range(40):
+        w = torch.randn(64, 128, generator=g, device="cuda") * (0.001 + 0.37 * t)
+        w8, s = fp8_quantize(w)
+        ref = (w8.to(torch.bfloat16) * s).float().cpu().numpy()
+        codes = w8.view(torch.uint8).cpu().numpy()
+        assert np.array_equal(ref, fp8_dequant_bf16(codes, s.item(), scale_in_bf16=True)), t
+        cpu_form_differs += not np.array_equal(ref, fp8_dequant_bf16(codes, s.item(), False))
+        mine = kernels.dequant_fp8(w8, applied_scale(s).expand(64).contiguous())
+        assert np.array_equal(mine.float().cpu().numpy(), ref), t
+    assert cpu_form_differs >= 20
+
+
+def _fp8_weights(rows_blocks, K, seed):
+    from nanosglang_amd.model.quantization import fp8_quantize_rows
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w = torch.randn(sum(rows_blocks), K, generator=g, device="cuda") * K ** -0.5
+    for i, n in enumerate(rows_blocks):           # blocks of different magnitude
+        w[sum(rows_blocks[:i]):sum(rows_blocks[:i]) + n] *= (1 + 3 * i)
+    return fp8_quantize_rows(w, rows_blocks)
+
+
+@pytest.mark.parametrize("M", [1, 16, 17, 32, 33, 64, 100, 160])
+def test_fp8_linear_bit_exact_vs_bf16_kernel_on_dequantized_weights(M):
+    """The FP8 kernels compute exactly what the bf16 kernels compute on the
+    dequantised weights (bias, SwiGLU and RoPE + KV-write epilogues), and
+    stay within bf16 rounding of an fp32 product."""
+    from nanosglang_amd import kernels
+    print(f"case: fp8 linear M={M}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(M)
+    x = torch.randn(M, 896, generator=g, device="cuda").bfloat16()
+    b = torch.randn(1152, generator=g, device="cuda").bfloat16()
+    w8, s = _fp8_weights([896, 128, 128], 896, seed=M)
+    wd = kernels.dequant_fp8(w8, s)
+    y8 = kernels.linear(x, w8, b, w_scale=s, force=True)
+    yb = kernels.linear(x, wd, b, force=True)
+    torch.cuda.synchronize()
+    assert torch.equal(y8, yb)
+    _check_bias(y8, x, wd, b)
+    # SwiGLU with separate gate / up scales
+    g8, gs = _fp8_weights([512, 512], 896, seed=M + 1)
+    ys8 = kernels.linear(x, g8, swiglu=True, w_scale=gs, force=True)
+    ysb = kernels.linear(x, kernels.dequant_fp8(g8, gs), swiglu=True, force=True)
+    torch.cuda.synchronize()
+    assert torch.equal(ys8, ysb)
+    # RoPE + KV write (q, k, v blocks with their own scales)
+    from nanosglang_amd.model.causal_lm import ModelConfig, rope_tables
+    cfg = ModelConfig(vocab_size=1000, hidden_size=896, intermediate_size=512,
+                      num_hidden_layers=1, num_attention_heads=14, num_key_value_heads=2,
+                      max_position_embeddings=2048)
+    cos, sin = (t.cuda() for t in rope_tables(cfg, "cpu"))
+    pos = (torch.arange(M, device="cuda") * 13) % 2048
+    slots = torch.arange(M, device="cuda") * 2
+    kc = torch.zeros(2 * M, 1, 2, 64, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    kc2, vc2 = torch.zeros_like(kc), torch.zeros_like(vc)
+    q8 = kernels.linear_rope_kv(x, w8, b, 14, 2, 64, pos, cos, sin, slots, kc, vc, w_scale=s,
+                                force=True)
+    qb = kernels.linear_rope_kv(x, wd, b, 14, 2, 64, pos, cos, sin, slots, kc2, vc2, force=True)
+    torch.cuda.synchronize()
+    assert torch.equal(q8, qb) and torch.equal(kc, kc2) and torch.equal(vc, vc2)
+
+
+def test_fp8_linear_library_path_for_prefill_rows():
+    from nanosglang_amd import kernels
+    print("case: fp8 linear M=300 (library path)", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(300, 896, generator=g, device="cuda").bfloat16()
+    w8, s = _fp8_weights([1152], 896, seed=5)
+    y = kernels.linear(x, w8, None, w_scale=s)
+    torch.cuda.synchronize()
+    _check_bias(y, x, kernels.dequant_fp8(w8, s), None)
+
+
+def test_fp8linear_module_matches_reference_arithmetic():
+    """FP8Linear (the reference's module interface) on the GPU: from_linear,
+    then forward == F.linear(x, w8.to(bf16) * scale, bias) within bf16 rounding,
+    and quantize_model swaps every nn.Linear outside the skip list."""
+    from nanosglang_amd.model.quantization import FP8Linear, quantize_model
+    print("case: FP8Linear module", flush=True)
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(896, 1152, bias=True).cuda().to(torch.bfloat16)
+    m = FP8Linear.from_linear(lin)
+    x = torch.randn(3, 7, 896, device="cuda").bfloat16()
+    y = m(x)
+    ref = torch.nn.functional.linear(x.float(), (m.weight_fp8.to(torch.bfloat16)
+                                                 * m.weight_scale).float(), m.bias.float())
+    torch.cuda.synchronize()
+    assert y.shape == (3, 7, 1152)
+    assert ((y.float() - ref).abs() <= 2.0 ** -8 * ref.abs() + 3e-3).all()
+    net = torch.nn.ModuleDict({"mlp": torch.nn.Linear(64, 64), "lm_head": torch.nn.Linear(64, 10)})
+    quantize_model(net)
+    assert isinstance(net["mlp"], FP8Linear) and isinstance(net["lm_head"], torch.nn.Linear)

@@ -138,6 +138,61 @@ def test_spec_engine_greedy_equals_plain_greedy_and_oracle(graphs):
         print(f"  prompt {len(p)}: first divergence from CPU oracle at {first}/{m}", flush=True)
 
 
+def test_spec_engine_fp8_weights_greedy_equals_plain_greedy():
+    """FP8 decoder weights (CausalLM.quantize_fp8, the reference's per-tensor
+    FP8Linear rule): greedy speculative decoding still reproduces plain
+    greedy decoding of the same quantised model, in graph mode, and the
+    packed forward stays within bf16 tolerance of the CPU oracle run on the
+    dequantised weights."""
+    from nanosglang_amd import kernels
+    from nanosglang_amd.engine.spec_engine import SpecEngine
+    print("case: spec engine greedy with fp8 weights", flush=True)
+    cpu, gpu = _tiny_models()
+    gpu.quantize_fp8()
+    assert gpu.layers[0]["qkv"].dtype == torch.float8_e4m3fn
+    rng = np.random.default_rng(2)
+    prompts = [rng.integers(0, 1000, n).tolist() for n in (20, 33, 5, 64)]
+    max_new = [20, 12, 25, 8]
+    spec = SpecEngine(gpu, draft_layers=2, num_speculative=4, num_blocks=64, max_batch=4)
+    plain = SpecEngine(gpu, draft_layers=2, num_speculative=0, num_blocks=64, max_batch=4)
+    out_spec, out_plain = spec.generate(prompts, max_new), plain.generate(prompts, max_new)
+    assert out_spec == out_plain
+    # packed forward (init-scale weights) vs the CPU fp32 oracle on the
+    # dequantised weights: the bf16 tolerance of the bf16 model's test
+    from nanosglang_amd.engine.paged_kv_cache import BlockManager, PagedKVCache
+    from nanosglang_amd.kernels import BatchPrefillWithPagedKVCacheWrapper
+    cpu1, gpu1 = _tiny_models(scale=1.0)
+    gpu1.quantize_fp8()
+    c = gpu1.config
+    Hq, Hkv, D, I = c.num_attention_heads, c.num_key_value_heads, c.head_dim, c.intermediate_size
+    deq = {"embed": cpu1.w["embed"], "norm": cpu1.w["norm"], "layers": []}
+    for L, Lc in zip(gpu1.layers, cpu1.w["layers"]):
+        qkv = kernels.dequant_fp8(L["qkv"], L["qkv_s"]).float().cpu()
+        gu = kernels.dequant_fp8(L["gate_up"], L["gate_up_s"]).float().cpu()
+        deq["layers"].append(dict(Lc, q=qkv[:Hq * D], k=qkv[Hq * D:(Hq + Hkv) * D],
+                                  v=qkv[(Hq + Hkv) * D:], gate=gu[:I], up=gu[I:],
+                                  o=kernels.dequant_fp8(L["o"], L["o_s"]).float().cpu(),
+                                  down=kernels.dequant_fp8(L["down"], L["down_s"]).float().cpu()))
+    ref_model = CPUCausalLM(cpu1.cfg, deq)
+    S = 40
+    prompt = rng.integers(0, 1000, S).tolist()
+    bm = BlockManager(64, 16, 4, 2, 64, torch.bfloat16, "cuda")
+    kv = PagedKVCache(bm)
+    t = kv.allocate_for_request(S)
+    w = BatchPrefillWithPagedKVCacheWrapper(torch.empty(32 << 20, dtype=torch.uint8, device="cuda"))
+    w.plan(np.array([0, S], np.int32), np.array([0, t.num_blocks], np.int32),
+           np.asarray(t.block_indices, np.int32), np.array([(S % 16) or 16], np.int32),
+           4, 2, 64, 16, causal=True)
+    got = gpu1.forward_packed(torch.tensor(prompt, device="cuda"), torch.arange(S, device="cuda"),
+                              (bm.k_cache, bm.v_cache), w,
+                              torch.tensor(kv.slots(t, 0, S), device="cuda")).float().cpu()
+    ref = ref_model.forward(torch.tensor([prompt]), torch.arange(S)[None],
+                            ref_model.new_cache(1, S), 0, causal_mask(S, S))[0].float()
+    rel = ((got - ref).norm(dim=-1) / ref.norm(dim=-1)).max().item()
+    print(f"  fp8 packed forward vs oracle on dequantised weights: max rel err {rel:.3e}", flush=True)
+    assert rel < 2e-2
+
+
 def test_spec_engine_graph_equals_eager_stochastic():
     """Stochastic speculative decoding (T = 0.8): with one request per graph
     size (no padding rows) the captured step consumes the same Philox words

@@ -42,7 +42,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 7
+#define NSG_ABI_VERSION 8
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -128,6 +128,50 @@ int32_t nsg_attn_run(const nsg_attn_plan_t* plan, const int32_t* work_d,
 /* Copies the workspace's error flags (bit 0: page id out of range) to
  * *flags_h after synchronising the stream, and clears them. */
 int32_t nsg_attn_check_flags(void* workspace, int32_t* flags_h, nsg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Host-side inputs of one captured speculative step (host only; no GPU call).
+ *
+ * Replaces the per-step preparation of the reference's graph decode path
+ * (engine.py:357-410: page-table CSR, last-page lengths, write slots, padding
+ * rows on a dummy page, wrapper.plan before g.replay), widened to the k
+ * one-token draft calls and the (k+1)-token verify call of a speculative step
+ * (speculative.py:76-128).  Request j of `batch` owns row rows[j] of
+ * page_table (num_pages[j] valid page ids; the step needs
+ * ceil((start_pos[j] + k + 1) / page_size) of them) and its last emitted
+ * token last_token[j] sits at position start_pos[j], not yet in the cache.
+ * Rows batch .. padded_batch-1 are padding: start 0, token 0, every page
+ * dummy_page.  Attention call a < k (draft a) has one query per row over
+ * start + a + 1 keys; call k (verify) has k + 1 queries over start + k + 1
+ * keys; each is planned by nsg_attn_plan_fixed with max_q_len = its query
+ * count and the given max_kv_len, into plans[a].  k may be 0 (no draft
+ * calls: plain decode).  Arrays with a stride hold
+ * one block per attention call (k + 1 blocks). */
+typedef struct {
+  int64_t* token0;            /* [padded_batch] last emitted token            */
+  int32_t* start;             /* [padded_batch] start position                */
+  int64_t* draft_pos;         /* [k][padded_batch] position of draft call a   */
+  int64_t* draft_slot;        /* [k][padded_batch] KV slot of draft call a
+                                 (both may be NULL when k = 0)               */
+  int64_t* verify_pos;        /* [padded_batch][k+1]                          */
+  int64_t* verify_slot;       /* [padded_batch][k+1]                          */
+  int32_t* qo_indptr;         /* [k+1][indptr_stride], padded_batch+1 used    */
+  int32_t* kv_indptr;         /* [k+1][indptr_stride], padded_batch+1 used    */
+  int32_t* kv_last_page_len;  /* [k+1][indptr_stride], padded_batch used      */
+  int32_t* kv_indices;        /* [k+1][indices_stride]                        */
+  int32_t* work;              /* [k+1][work_stride] work lists                */
+  int32_t indptr_stride;
+  int32_t indices_stride;
+  int32_t work_stride;
+} nsg_spec_step_bufs_t;
+
+int32_t nsg_spec_step_fill(const int32_t* page_table, int64_t page_table_stride,
+                           const int32_t* rows, const int32_t* num_pages,
+                           const int64_t* start_pos, const int64_t* last_token, int32_t batch,
+                           int32_t padded_batch, int32_t k, int32_t page_size,
+                           int32_t dummy_page, int32_t num_qo_heads, int32_t num_kv_heads,
+                           int32_t head_dim, int32_t num_cus, int32_t max_kv_len,
+                           const nsg_spec_step_bufs_t* bufs, nsg_attn_plan_t* plans);
 
 /* ------------------------------------------------------------------------
  * Fused acceptance: ratio test, residual resample, bonus token and rollback

@@ -13,7 +13,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libnsg_spec.so")
 
 NSG_ATTN_WORK_INTS = 8
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 i32, i64, u32, u64, f32 = C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_float
 vp = C.c_void_p
@@ -25,6 +25,16 @@ class AttnPlan(C.Structure):
         ("num_work", i32), ("num_merge", i32), ("num_groups", i32), ("row_tiles", i32), ("q_tile_tokens", i32),
         ("max_splits", i32), ("head_dim", i32), ("num_qo_heads", i32), ("num_kv_heads", i32),
         ("kv_groups", i32), ("workspace_bytes", i64),
+    ]
+
+
+class StepBufs(C.Structure):
+    """Mirror of nsg_spec_step_bufs_t (host staging pointers of one step)."""
+    _fields_ = [
+        ("token0", vp), ("start", vp), ("draft_pos", vp), ("draft_slot", vp),
+        ("verify_pos", vp), ("verify_slot", vp), ("qo_indptr", vp), ("kv_indptr", vp),
+        ("kv_last_page_len", vp), ("kv_indices", vp), ("work", vp),
+        ("indptr_stride", i32), ("indices_stride", i32), ("work_stride", i32),
     ]
 
 
@@ -60,6 +70,8 @@ SIGNATURES = {
     "nsg_rmsnorm": (i32, [vp, vp, vp, vp, i32, i32, f32, vp]),
     "nsg_silu_mul": (i32, [vp, vp, i64, i32, vp]),
     "nsg_philox_uniform": (i32, [u64, u32, u64, i64, vp, vp]),
+    "nsg_spec_step_fill": (i32, [vp, i64, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32,
+                                 i32, i32, i32, C.POINTER(StepBufs), C.POINTER(AttnPlan)]),
 }
 
 _lib = None

@@ -50,7 +50,7 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
-from .. import kernels
+from .. import _native, kernels
 from ..kernels import BatchPrefillWithPagedKVCacheWrapper
 from .paged_kv_cache import BlockManager, BlockTable, PagedKVCache
 
@@ -63,6 +63,8 @@ class _Req:
     table: BlockTable = field(default_factory=BlockTable)
     out: list[int] = field(default_factory=list)
     start: int = 0          # position of out[-1]; KV holds positions < start
+    row: int = -1           # row of the engine's page-table mirror (graph mode)
+    synced: int = 0         # pages of `table` mirrored into that row
 
 
 def graph_batch_sizes(max_bs: int) -> list[int]:
@@ -96,21 +98,27 @@ class _Arena:
         self.dev.copy_(self.host, non_blocking=True)
 
 
+def _round_up(n: int, m: int = 64) -> int:
+    return (n + m - 1) // m * m
+
+
 class _StepGraph:
     """Static buffers, attention wrappers and the captured graph of one
-    speculative step at padded batch size ``bs``."""
+    speculative step at padded batch size ``bs``.
 
-    def __init__(self, eng: "SpecEngine", bs: int, max_pages: int):
+    Staging layout (one pinned host buffer, one device buffer, same offsets):
+    token0 / start [bs]; draft positions and slots [k][bs]; verify positions
+    and slots [bs][k+1]; then, per attention call a (k drafts, then the
+    verify call), a block of qo / kv indptr and last-page lengths, page ids
+    and the fixed-size work list, each block at a 256-byte aligned stride."""
+
+    def __init__(self, eng: "SpecEngine", bs: int, max_page_ids: int):
         c = eng.model.config
         k, dev = eng.k, eng.device
         Hq, Hkv = c.num_attention_heads, c.num_key_value_heads
         self.bs = bs
         lib = kernels._lib()
-        specs = [("tok0", torch.int64, bs), ("start", torch.int32, bs),
-                 ("vpos", torch.int64, bs * (k + 1)), ("vslot", torch.int64, bs * (k + 1))]
-        for i in range(k):
-            specs += [(f"pos{i}", torch.int64, bs), (f"slot{i}", torch.int64, bs)]
-        caps = []
+        nw = 0
         for a in range(k + 1):                       # attention calls: k drafts, 1 verify
             ql = 1 if a < k else k + 1
             mw, mm = kernels.C.c_int32(0), kernels.C.c_int32(0)
@@ -118,21 +126,35 @@ class _StepGraph:
                                                       eng.max_kv_len, kernels.C.byref(mw),
                                                       kernels.C.byref(mm)),
                           "nsg_attn_fixed_capacity")
-            nw = (mw.value + mm.value) * kernels.NSG_ATTN_WORK_INTS
-            caps.append(ql)
-            specs += [(f"qo{a}", torch.int32, bs + 1), (f"kvp{a}", torch.int32, bs + 1),
-                      (f"last{a}", torch.int32, bs), (f"idx{a}", torch.int32, bs * max_pages),
-                      (f"work{a}", torch.int32, nw)]
+            nw = max(nw, (mw.value + mm.value) * kernels.NSG_ATTN_WORK_INTS)
+        si, sx, sw = _round_up(bs + 1), _round_up(max_page_ids), _round_up(nw)
+        self.strides = (si, sx, sw)
+        specs = [("tok0", torch.int64, bs), ("start", torch.int32, bs),
+                 ("pos", torch.int64, k * bs), ("slot", torch.int64, k * bs),
+                 ("vpos", torch.int64, bs * (k + 1)), ("vslot", torch.int64, bs * (k + 1)),
+                 ("qo", torch.int32, (k + 1) * si), ("kvp", torch.int32, (k + 1) * si),
+                 ("last", torch.int32, (k + 1) * si), ("work", torch.int32, (k + 1) * sw),
+                 ("idx", torch.int32, (k + 1) * sx)]
         self.arena = A = _Arena(specs, dev)
+        H = A.h
+        self.bufs = _native.StepBufs(
+            *[H[n].ctypes.data for n in ("tok0", "start", "pos", "slot", "vpos", "vslot", "qo",
+                                         "kvp", "last", "idx", "work")], si, sx, sw)
+        self.plans = (_native.AttnPlan * (k + 1))()
+        D = A.d
+        self.pos = [D["pos"][i * bs:(i + 1) * bs] for i in range(k)]
+        self.slot = [D["slot"][i * bs:(i + 1) * bs] for i in range(k)]
+        self.kvp = [D["kvp"][a * si:a * si + bs + 1] for a in range(k + 1)]
+        self.idx = [D["idx"][a * sx:(a + 1) * sx] for a in range(k + 1)]
         self.attn = []
         for a in range(k + 1):
-            hb = {"qo_indptr": A.h[f"qo{a}"], "kv_indptr": A.h[f"kvp{a}"],
-                  "kv_indices": A.h[f"idx{a}"], "kv_last": A.h[f"last{a}"], "work": A.h[f"work{a}"]}
             self.attn.append(BatchPrefillWithPagedKVCacheWrapper(
-                eng.attn_ws, "NHD", use_cuda_graph=True, qo_indptr_buf=A.d[f"qo{a}"],
-                paged_kv_indptr_buf=A.d[f"kvp{a}"], paged_kv_indices_buf=A.d[f"idx{a}"],
-                paged_kv_last_page_len_buf=A.d[f"last{a}"], work_buf=A.d[f"work{a}"],
-                host_bufs=hb, max_q_len=caps[a], max_kv_len=eng.max_kv_len))
+                eng.attn_ws, "NHD", use_cuda_graph=True,
+                qo_indptr_buf=D["qo"][a * si:a * si + bs + 1], paged_kv_indptr_buf=self.kvp[a],
+                paged_kv_indices_buf=self.idx[a],
+                paged_kv_last_page_len_buf=D["last"][a * si:a * si + bs],
+                work_buf=D["work"][a * sw:(a + 1) * sw],
+                max_q_len=1 if a < k else k + 1, max_kv_len=eng.max_kv_len))
         V = c.vocab_size
         self.drafts = torch.zeros(bs, k, dtype=torch.int64, device=dev)
         self.vids = torch.zeros(bs, k + 1, dtype=torch.int64, device=dev)
@@ -179,6 +201,7 @@ class SpecEngine:
         self._graphs: dict[int, _StepGraph] = {}
         self._accept_ws = kernels.AcceptWorkspace(self.device)
         self._dummy_block = None
+        self._tab = np.zeros((0, 0), np.int32)     # page-table mirror of graph mode
         # decode / verify contexts never exceed the position table: the
         # captured attention plans need no KV split (and no merge launch)
         self.max_kv_len = min(c.max_position_embeddings, 1022 * block_size)
@@ -260,8 +283,16 @@ class SpecEngine:
         for bs in graph_batch_sizes(self.max_batch):
             if bs in self._graphs:
                 continue
-            g = _StepGraph(self, bs, self._max_pages())
+            # page ids per attention call: every pool page at most once (no
+            # table shares a page) plus the padding rows' dummy pages
+            ids = min(bs * self._max_pages(),
+                      self.bm.num_blocks + bs * ((self.k + self.P) // self.P))
+            g = _StepGraph(self, bs, ids)
             self._fill_step(g, [])                       # all rows on the dummy page
+            for a, w in enumerate(g.attn):
+                ql = 1 if a < self.k else self.k + 1
+                w.adopt_plan(g.plans[a], bs * ql, c.num_attention_heads,
+                             c.num_key_value_heads, c.head_dim, self.P, causal=True)
             g.arena.upload()
             for _ in range(2):                           # warm-up (allocator, GEMM heuristics)
                 self._graph_body(g)
@@ -281,7 +312,7 @@ class SpecEngine:
         pool = self._pool()
         tok = A["tok0"]
         for i in range(k):
-            lg = m.forward_packed(tok, A[f"pos{i}"], pool, g.attn[i], A[f"slot{i}"], None,
+            lg = m.forward_packed(tok, g.pos[i], pool, g.attn[i], g.slot[i], None,
                                   self.draft_layers)
             if g.dlog is not None:
                 g.dlog[:, i].copy_(lg)
@@ -294,47 +325,40 @@ class SpecEngine:
         g.vids[:, 1:].copy_(g.drafts)
         tl = m.forward_packed(g.vids.view(-1), A["vpos"], pool, g.attn[k], A["vslot"])
         kernels.spec_accept(tl.view(bs, k + 1, -1), g.dlog, g.drafts, g.u, self.temperature,
-                            A[f"kvp{k}"], A[f"idx{k}"], A["start"], page_size=self.P,
+                            g.kvp[k], g.idx[k], A["start"], page_size=self.P,
                             workspace=self._accept_ws, out=(g.n_out, g.emitted, g.rollback))
 
     def _fill_step(self, g: _StepGraph, active: list) -> None:
-        """Host side of one step: page tables, slots, positions and the k + 1
-        attention plans, written into the graph's pinned staging views."""
+        """Host side of one step, one native call (``nsg_spec_step_fill``):
+        tokens, positions, KV slots, the k + 1 page tables and attention plans,
+        written into the graph's pinned staging buffer.  Request rows come
+        from the engine's page-table mirror (``_sync_table``)."""
         c = self.model.config
-        k, P, bs = self.k, self.P, g.bs
-        H = g.arena.h
         B = len(active)
-        maxp = max([len(r.table.block_indices) for r in active] + [(k + P) // P])
-        tab = np.full((bs, maxp), self._dummy_block, np.int32)
-        for j, r in enumerate(active):
-            bt = r.table.block_indices
-            tab[j, :len(bt)] = bt
-        starts = np.zeros(bs, np.int64)
-        starts[:B] = [r.start for r in active]
-        H["tok0"][:B] = [r.out[-1] for r in active]
-        H["tok0"][B:] = 0
-        H["start"][:] = starts
-        rows = np.arange(bs)
-        cols = np.arange(maxp)[None, :]
-        Hq, Hkv, D = c.num_attention_heads, c.num_key_value_heads, c.head_dim
-        for a in range(k + 1):
-            ql = 1 if a < k else k + 1
-            L = starts + (a + 1 if a < k else k + 1)
-            npg = (L + P - 1) // P
-            kvp = np.zeros(bs + 1, np.int32)
-            np.cumsum(npg, out=kvp[1:])
-            idx = tab[cols < npg[:, None]]
-            last = (L - (npg - 1) * P).astype(np.int32)
-            qo = (np.arange(bs + 1) * ql).astype(np.int32)
-            g.attn[a].plan(qo, kvp, idx, last, Hq, Hkv, D, P, causal=True)
-            if a < k:
-                pos = starts + a
-                H[f"pos{a}"][:] = pos
-                H[f"slot{a}"][:] = tab[rows, pos // P].astype(np.int64) * P + pos % P
-        vpos = (starts[:, None] + np.arange(k + 1)[None, :])
-        H["vpos"][:] = vpos.reshape(-1)
-        H["vslot"][:] = (tab[rows[:, None], vpos // P].astype(np.int64) * P
-                         + vpos % P).reshape(-1)
+        if B:
+            tab = self._tab
+            rows = np.fromiter((r.row for r in active), np.int32, B)
+            npg = np.fromiter((r.synced for r in active), np.int32, B)
+            starts = np.fromiter((r.start for r in active), np.int64, B)
+            last = np.fromiter((r.out[-1] for r in active), np.int64, B)
+            ptrs = (tab.ctypes.data, tab.shape[1], rows.ctypes.data, npg.ctypes.data,
+                    starts.ctypes.data, last.ctypes.data)
+        else:
+            ptrs = (None, 0, None, None, None, None)
+        kernels.check(kernels._lib().nsg_spec_step_fill(
+            *ptrs, B, g.bs, self.k, self.P, self._dummy_block, c.num_attention_heads,
+            c.num_key_value_heads, c.head_dim, kernels.MI355X_CUS, self.max_kv_len,
+            kernels.C.byref(g.bufs), g.plans), "nsg_spec_step_fill")
+
+    def _sync_table(self, r: _Req) -> None:
+        """Mirror request r's block table into its row of the int32 page table
+        the native step fill reads (only pages added since the last sync are
+        copied; a rollback only shortens the row)."""
+        bt = r.table.block_indices
+        n = len(bt)
+        if n > r.synced:
+            self._tab[r.row, r.synced:n] = bt[r.synced:]
+        r.synced = n
 
     def _step_graph(self, active: list):
         B = len(active)
@@ -407,6 +431,10 @@ class SpecEngine:
         # 1. admission
         for r in reqs:
             r.table = self.kv.allocate_for_request(len(r.prompt))
+        if self.use_graphs:
+            self._tab = np.zeros((len(reqs), self._max_pages()), np.int32)
+            for i, r in enumerate(reqs):
+                r.row = i
         # 2. prefill (one ragged packed forward)
         lens = [len(r.prompt) for r in reqs]
         self._plan(reqs, lens, lens)
@@ -430,6 +458,8 @@ class SpecEngine:
             B = len(active)
             for r in active:
                 self.kv.reserve(r.table, r.start + k + 1)
+                if self.use_graphs:
+                    self._sync_table(r)
             if self.use_graphs:
                 n_h, em_h = self._step_graph(active)
             else:
@@ -444,6 +474,7 @@ class SpecEngine:
                 r.out.extend(em_h[j, :n].tolist())
                 r.start += n
                 self.kv.truncate(r.table, r.start)        # rollback of rejected pages
+                r.synced = min(r.synced, len(r.table.block_indices))
                 if len(r.out) >= r.max_new:
                     del r.out[r.max_new:]
                     self.kv.free_request(r.table)

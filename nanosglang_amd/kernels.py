@@ -198,6 +198,16 @@ class BatchPrefillWithPagedKVCacheWrapper:
         else:
             pl = self._plan_dynamic(lib, qo_h, kvp_h, last_h, B, num_qo_heads, num_kv_heads,
                                     head_dim_qk, page_size, causal)
+        if not self._graph:
+            self._qo_indptr = _dev_i32(qo_indptr, self._device)
+            self._kv_indptr = _dev_i32(paged_kv_indptr, self._device)
+            self._kv_indices = _dev_i32(paged_kv_indices, self._device)
+            self._kv_last = _dev_i32(paged_kv_last_page_len, self._device)
+        self._set_plan(pl, int(qo_h[-1]), num_qo_heads, num_kv_heads, head_dim_qk, page_size,
+                       causal, sm_scale)
+
+    def _set_plan(self, pl, total_q, num_qo_heads, num_kv_heads, head_dim_qk, page_size,
+                  causal, sm_scale):
         if pl.workspace_bytes > self._ws.numel() * self._ws.element_size():
             raise RuntimeError(
                 f"attention workspace too small: plan needs {pl.workspace_bytes} bytes, "
@@ -207,16 +217,41 @@ class BatchPrefillWithPagedKVCacheWrapper:
             g = self._gbufs
             self._qo_indptr, self._kv_indptr = g["qo_indptr"], g["kv_indptr"]
             self._kv_indices, self._kv_last = g["kv_indices"], g["kv_last"]
-        else:
-            self._qo_indptr = _dev_i32(qo_indptr, self._device)
-            self._kv_indptr = _dev_i32(paged_kv_indptr, self._device)
-            self._kv_indices = _dev_i32(paged_kv_indices, self._device)
-            self._kv_last = _dev_i32(paged_kv_last_page_len, self._device)
-        self._total_q = int(qo_h[-1])
+        self._total_q = int(total_q)
         self._page_size = page_size
         self._causal = causal
         self._sm_scale = (1.0 / math.sqrt(head_dim_qk)) if sm_scale is None else float(sm_scale)
         self._dims = (num_qo_heads, num_kv_heads, head_dim_qk)
+
+    def adopt_plan(self, plan: AttnPlan, total_q: int, num_qo_heads: int, num_kv_heads: int,
+                   head_dim_qk: int, page_size: int, causal: bool = True,
+                   sm_scale: float | None = None) -> None:
+        """Graph mode: take a plan whose metadata and work list a host routine
+        (``nsg_spec_step_fill``) already wrote into this wrapper's buffers --
+        the state ``plan`` leaves, without re-planning.  The plan must have the
+        fixed shape of this wrapper's graph buffers (``max_q_len``,
+        ``max_kv_len``), so that a graph captured around ``run`` replays it."""
+        if not self._graph:
+            raise ValueError("adopt_plan is for use_cuda_graph=True wrappers")
+        if self._fixed is None:
+            if not self._fixed_q:
+                raise ValueError("adopt_plan needs a wrapper built with max_q_len")
+            lib = _lib()
+            mq = self._fixed_q
+            mw, mm = C.c_int32(0), C.c_int32(0)
+            check(lib.nsg_attn_fixed_capacity(self._batch, mq, num_qo_heads, num_kv_heads,
+                                              self._num_cus, self._fixed_kv, C.byref(mw),
+                                              C.byref(mm)), "nsg_attn_fixed_capacity")
+            if self._work_d is None or self._work_d.numel() < (mw.value + mm.value) * \
+                    NSG_ATTN_WORK_INTS:
+                raise ValueError("adopt_plan needs a work_buf of the fixed capacity")
+            self._fixed = (mq, mw.value, mm.value)
+        mq, mw, mm = self._fixed
+        if (plan.num_work, plan.num_merge) != (mw, mm):
+            raise ValueError(f"plan holds {plan.num_work} + {plan.num_merge} work items, the "
+                             f"fixed list {mw} + {mm}")
+        self._set_plan(plan, total_q, num_qo_heads, num_kv_heads, head_dim_qk, page_size, causal,
+                       sm_scale)
 
     def _plan_dynamic(self, lib, qo_h, kvp_h, last_h, B, num_qo_heads, num_kv_heads,
                       head_dim_qk, page_size, causal) -> AttnPlan:

@@ -42,7 +42,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 8
+#define NSG_ABI_VERSION 9
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -187,6 +187,10 @@ int32_t nsg_spec_step_fill(const int32_t* page_table, int64_t page_table_stride,
  *   element b*req_stride + r*row_stride; logits_dtype 0 = bf16, 1 = fp32.
  * draft_tokens int64 [B, k]; uniforms fp32 [B, k+1] (columns 0..k-1 for the
  *   ratio tests, column k for the residual / bonus draw).
+ * bonus_tokens int64 [B] (may be NULL; ignored when greedy): when every draft
+ *   of request b is accepted, emitted[b][k] = bonus_tokens[b] instead of a
+ *   draw from target row k -- the reference's bonus is sample_token with
+ *   top-k / top-p (speculative.py:174-182), which nsg_sample computes.
  * Page table (may be NULL, then no rollback slots): kv_indptr / kv_indices
  *   as in the attention entry points, start_pos int32 [B] = position of the
  *   first verify token (the cache length before verify).
@@ -195,7 +199,7 @@ int32_t nsg_spec_step_fill(const int32_t* page_table, int64_t page_table_stride,
  *   block*P + offset of positions start+n .. start+k.
  * k may be 0: the call then samples one token per request from row 0
  *   (argmax when greedy), which is the reference's sample_token
- *   (sampling.py:25-50) without top-k / top-p.
+ *   (sampling.py:25-50) without top-k / top-p (nsg_sample has them).
  * ---------------------------------------------------------------------- */
 int64_t nsg_spec_accept_workspace_bytes(int32_t batch, int32_t k, int32_t vocab);
 
@@ -203,12 +207,34 @@ int32_t nsg_spec_accept(const void* target_logits, int64_t target_req_stride,
                         int64_t target_row_stride, const void* draft_logits,
                         int64_t draft_req_stride, int64_t draft_row_stride,
                         int32_t logits_dtype, const int64_t* draft_tokens,
-                        const float* uniforms, int32_t batch, int32_t k, int32_t vocab,
+                        const float* uniforms, const int64_t* bonus_tokens, int32_t batch,
+                        int32_t k, int32_t vocab,
                         float temperature, const int32_t* kv_indptr,
                         const int32_t* kv_indices, const int32_t* start_pos,
                         int32_t page_size, int32_t* num_emitted, int64_t* emitted,
                         int64_t* rollback_slots, void* workspace, int64_t workspace_bytes,
                         nsg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Sampling with temperature, top-k and top-p: one token per logits row.
+ *
+ * Replaces sample_token (nano_sglang/engine/sampling.py:25-50) and its
+ * filters (_sample_pytorch, :71-88): argmax (first index) when
+ * temperature < 1e-6; otherwise logits / T, top-k keeps every logit >= the
+ * k-th largest (top_k <= 0 or >= vocab: off), top-p drops a token when the
+ * probability mass of the tokens before it in descending order reaches top_p
+ * (top_p in (0, 1]; 1 = off; equal logits ordered by index), then an inverse-
+ * CDF draw in vocabulary order with uniforms[r * uniform_stride].  Masses are
+ * exact 2^-40 fixed-point sums, so the result does not depend on the order
+ * of summation.  logits: rows of `vocab` values, row r at r * row_stride
+ * elements; logits_dtype 0 = bf16, 1 = fp32 (no NaN).  tokens int64 [rows]
+ * (-1 for a row of -inf).  The workspace needs no initialisation.
+ * ---------------------------------------------------------------------- */
+int64_t nsg_sample_workspace_bytes(int32_t rows, int32_t vocab);
+int32_t nsg_sample(const void* logits, int64_t row_stride, int32_t logits_dtype, int32_t rows,
+                   int32_t vocab, float temperature, int32_t top_k, float top_p,
+                   const float* uniforms, int64_t uniform_stride, int64_t* tokens,
+                   void* workspace, int64_t workspace_bytes, nsg_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * KV slot writes and rollback.

@@ -11,7 +11,9 @@
 //     argmax(target row k);
 //   stochastic: p = softmax(logits / T); accept iff u_i < min(1, pt/pd)
 //     (pd == 0 accepts); on rejection sample max(0, pt - pd) (falls back to pt
-//     if that sums to 0) by inverse CDF with u_k; else the bonus from pt_k.
+//     if that sums to 0) by inverse CDF with u_k; else the bonus from pt_k,
+//     or the caller's bonus token when one is given (a top-k / top-p draw
+//     from target row k, speculative.py:174-182).
 //
 // Launches (no workgroup waits on another inside a launch: on gfx950 that
 // handshake needs agent-scope fences, which write back and invalidate the
@@ -59,6 +61,7 @@ struct AccParams {
   int64_t d_req, d_row;
   const int64_t* dtok;
   const float* u;
+  const int64_t* bonus;  // optional precomputed bonus tokens [B] (stochastic)
   int B, k, V;
   float c;  // log2(e) / T
   int greedy;
@@ -588,6 +591,10 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(AccParams p) {
   const float* dd = p.dec + (int64_t)b * 8;
   const int j = __float_as_int(dd[0]);
   int mode = __float_as_int(dd[1]);
+  if (mode == 1 && p.bonus) {  // all accepted: the caller's filtered bonus draw
+    if (tid == 0) p.emitted[(int64_t)b * (p.k + 1) + j] = p.bonus[b];
+    return;
+  }
   const float Mt = dd[2], iZt = dd[3], Md = dd[4], iZd = dd[5];
   const int64_t to = trow(p, b, j);
   const int64_t dof = mode == 0 ? drow(p, b, j) : 0;
@@ -817,6 +824,7 @@ __global__ __launch_bounds__(kRsThreads) void resolve_kernel(AccParams p) {
   }
   __syncthreads();
   const Decision d = s_d;
+  if (d.mode == 1 && p.bonus) return;  // the bonus comes from the caller
   const int64_t to = trow(p, b, d.j);
   const int64_t dof = d.mode == 0 ? drow(p, b, d.j) : 0;
   const int ns = rs_steps(p.V);
@@ -846,6 +854,10 @@ __global__ __launch_bounds__(64) void select_kernel2(AccParams p) {
   const int b = blockIdx.x;
   const int lane = threadIdx.x;
   const Decision d = load_decision(p.dec + (int64_t)b * 8);
+  if (d.mode == 1 && p.bonus) {  // all accepted: the caller's filtered bonus draw
+    if (lane == 0) p.emitted[(int64_t)b * (p.k + 1) + d.j] = p.bonus[b];
+    return;
+  }
   const int64_t to = trow(p, b, d.j);
   const int64_t dof = d.mode == 0 ? drow(p, b, d.j) : 0;
   const float u = p.u[(int64_t)b * (p.k + 1) + p.k];
@@ -1003,7 +1015,8 @@ extern "C" int32_t nsg_spec_accept(const void* target_logits, int64_t target_req
                                    int64_t target_row_stride, const void* draft_logits,
                                    int64_t draft_req_stride, int64_t draft_row_stride,
                                    int32_t logits_dtype, const int64_t* draft_tokens,
-                                   const float* uniforms, int32_t batch, int32_t k,
+                                   const float* uniforms, const int64_t* bonus_tokens,
+                                   int32_t batch, int32_t k,
                                    int32_t vocab, float temperature, const int32_t* kv_indptr,
                                    const int32_t* kv_indices, const int32_t* start_pos,
                                    int32_t page_size, int32_t* num_emitted, int64_t* emitted,
@@ -1051,6 +1064,7 @@ extern "C" int32_t nsg_spec_accept(const void* target_logits, int64_t target_req
   p.d_row = draft_row_stride;
   p.dtok = draft_tokens;
   p.u = uniforms;
+  p.bonus = greedy ? nullptr : bonus_tokens;
   p.B = batch;
   p.k = k;
   p.V = vocab;

@@ -21,8 +21,16 @@ Philox4x32-10 (``seed``) instead of ``torch.rand``; ``make_mask_fn`` must be
 bottom-right causal (use :func:`causal_mask`; the reference engine's
 ``_make_causal_mask``, engine.py:704-710, is not causal for S != full); and the
 draft-cache hole after full acceptance (the draft never consumed d_{k-1}) is
-filled on the next call unless ``fill_draft_hole=False``.  ``top_k`` /
-``top_p`` draft filtering is not implemented (raises).
+filled on the next call unless ``fill_draft_hole=False``.
+
+``top_k`` / ``top_p`` apply where the reference calls ``sample_token``: the
+draft tokens (:95-100) and the bonus token (:174-182), through the HIP sampler
+(``kernels.sample``, engine/sampling.py:71-88).  The ratio test uses the
+unfiltered ``softmax(logits / T)`` of both models, as the reference does
+(:89-92, 104, 134-148); the residual is the textbook one over those
+distributions (the reference's filtered fallback, :163-169, is only reached
+when the residual is empty, which the textbook residual never is after a
+rejection).
 
 ``generate_batch`` is additive API: batched speculative decoding on the paged
 KV cache (``engine.spec_engine.SpecEngine``) for a target built by
@@ -47,8 +55,8 @@ class SpeculativeDecoder:
     def __init__(self, draft_model, target_model, num_speculative: int = 5,
                  temperature: float = 1.0, top_p: float = 1.0, top_k: int = 0, seed: int = 0,
                  fill_draft_hole: bool = True):
-        if top_k > 0 or top_p < 1.0:
-            raise NotImplementedError("top-k / top-p draft filtering is not implemented")
+        if not 0.0 < top_p or top_p != top_p:
+            raise ValueError(f"top_p {top_p} must be in (0, 1] (1 = off)")
         self.draft_model = draft_model
         self.target_model = target_model
         self.num_speculative = num_speculative
@@ -69,12 +77,18 @@ class SpeculativeDecoder:
     def _logits_dtype(x: torch.Tensor) -> torch.Tensor:
         return x if x.dtype in (torch.bfloat16, torch.float32) else x.float()
 
+    def _filtered(self) -> bool:
+        return self.temperature >= 1e-6 and (self.top_k > 0 or self.top_p < 1.0)
+
     def _sample(self, row: torch.Tensor) -> torch.Tensor:
-        """One token from a (1, V) logits row: argmax or inverse CDF of
-        softmax(row / T) (the acceptance kernel with k = 0)."""
+        """One token from a (1, V) logits row (sample_token, sampling.py:25-50):
+        argmax, or an inverse-CDF draw from softmax(row / T) after top-k / top-p."""
         row = self._logits_dtype(row)
         greedy = self.temperature < 1e-6
         u = None if greedy else self._uniforms(1, 1, row.device).view(1, 1)
+        if self._filtered():
+            return kernels.sample(row.reshape(1, -1), self.temperature, self.top_k, self.top_p,
+                                  u.view(1))
         _, em, _ = kernels.spec_accept(row.view(1, 1, -1).contiguous(), None, None, u,
                                        self.temperature)
         return em[:, 0]
@@ -117,7 +131,11 @@ class SpeculativeDecoder:
         tl = self._logits_dtype(tl).contiguous()
         dl = None if greedy else torch.stack(dlogits, 1).to(tl.dtype).contiguous()
         u = None if greedy else self._uniforms(0, k + 1, dev).view(1, k + 1)
-        n, emitted, _ = kernels.spec_accept(tl, dl, torch.stack(drafts, 1), u, self.temperature)
+        bonus = None
+        if self._filtered():    # speculative.py:174-182: sample_token with the filters
+            bonus = kernels.sample(tl[:, k], self.temperature, self.top_k, self.top_p, u[:, k])
+        n, emitted, _ = kernels.spec_accept(tl, dl, torch.stack(drafts, 1), u, self.temperature,
+                                            bonus_tokens=bonus)
         n = int(n.item())
         out = emitted[0, :n].tolist()
         if n == k + 1:
@@ -136,7 +154,8 @@ class SpeculativeDecoder:
         from ..engine.spec_engine import SpecEngine
         eng = SpecEngine(self.target_model, draft_layers=draft_layers,
                          num_speculative=self.num_speculative, num_blocks=num_blocks,
-                         block_size=block_size, temperature=self.temperature, seed=self.seed)
+                         block_size=block_size, temperature=self.temperature, seed=self.seed,
+                         top_k=self.top_k, top_p=self.top_p)
         out = eng.generate(prompts, max_new_tokens)
         self.last_stats = eng.stats
         return out

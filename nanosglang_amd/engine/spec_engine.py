@@ -162,6 +162,7 @@ class _StepGraph:
         self.emitted = torch.zeros(bs, k + 1, dtype=torch.int64, device=dev)
         self.rollback = torch.zeros(bs, k, dtype=torch.int64, device=dev)
         self.n1 = torch.zeros(bs, dtype=torch.int32, device=dev)
+        self.bonus = torch.zeros(bs, dtype=torch.int64, device=dev)
         self.em1 = torch.zeros(bs, 1, dtype=torch.int64, device=dev)
         self.rb1 = torch.zeros(bs, 0, dtype=torch.int64, device=dev)
         if not eng.greedy:
@@ -179,13 +180,18 @@ class SpecEngine:
     def __init__(self, model, draft_layers: int, num_speculative: int, num_blocks: int,
                  block_size: int = 16, temperature: float = 0.0, seed: int = 0,
                  workspace_bytes: int = 256 << 20, use_graphs: bool = True,
-                 max_batch: int = 32):
+                 max_batch: int = 32, top_k: int = 0, top_p: float = 1.0):
         c = model.config
         self.model = model
         self.k = num_speculative
         self.draft_layers = draft_layers
         self.temperature = float(temperature)
         self.greedy = self.temperature < 1e-6
+        if not 0.0 < top_p or top_p != top_p:
+            raise ValueError(f"top_p {top_p} must be in (0, 1] (1 = off)")
+        self.top_k, self.top_p = int(top_k), float(top_p)
+        # top-k / top-p at the reference's sample_token sites: drafts and bonus
+        self.filtered = not self.greedy and (self.top_k > 0 or self.top_p < 1.0)
         self.seed = seed
         self.device = model.device
         self.bm = BlockManager(num_blocks, block_size, model.num_layers, c.num_key_value_heads,
@@ -252,11 +258,24 @@ class SpecEngine:
 
     def _sample_rows(self, logits: torch.Tensor) -> torch.Tensor:
         """One token per row: argmax if greedy, else inverse CDF of
-        softmax(logits / T) with Philox stream 1 (spec_accept with k = 0)."""
+        softmax(logits / T) -- after top-k / top-p when set -- with Philox
+        stream 1 (spec_accept with k = 0, or the sampler)."""
         B = logits.shape[0]
         u = None if self.greedy else self._uniforms(1, B).view(B, 1)
+        if self.filtered:
+            return kernels.sample(logits.view(B, -1), self.temperature, self.top_k, self.top_p,
+                                  u.view(B))
         _, em, _ = kernels.spec_accept(logits.view(B, 1, -1), None, None, u, self.temperature)
         return em[:, 0]
+
+    def _bonus(self, tl: torch.Tensor, u: torch.Tensor | None, workspace=None, out=None):
+        """speculative.py:174-182: the bonus after k accepted drafts is
+        sample_token(target row k) with top-k / top-p; None without filters
+        (the acceptance kernel draws it itself)."""
+        if not self.filtered:
+            return None
+        return kernels.sample(tl[:, self.k], self.temperature, self.top_k, self.top_p,
+                              u[:, self.k], workspace=workspace, out=out)
 
     # ---- graph mode ----
     def _max_pages(self) -> int:
@@ -277,7 +296,8 @@ class SpecEngine:
         V = c.vocab_size
         # every accept call of every graph shares one workspace, sized once
         need = max(kernels._lib().nsg_spec_accept_workspace_bytes(self.max_batch, self.k, V),
-                   kernels._lib().nsg_spec_accept_workspace_bytes(self.max_batch, 0, V))
+                   kernels._lib().nsg_spec_accept_workspace_bytes(self.max_batch, 0, V),
+                   kernels._lib().nsg_sample_workspace_bytes(self.max_batch, V))
         self._accept_ws.get(need)
         pool = torch.cuda.graph_pool_handle()
         for bs in graph_batch_sizes(self.max_batch):
@@ -317,16 +337,23 @@ class SpecEngine:
             if g.dlog is not None:
                 g.dlog[:, i].copy_(lg)
             u = None if g.ud is None else g.ud[i].view(bs, 1)
-            kernels.spec_accept(lg.view(bs, 1, -1), None, None, u, self.temperature,
-                                workspace=self._accept_ws, out=(g.n1, g.em1, g.rb1))
+            if self.filtered:
+                kernels.sample(lg.view(bs, -1), self.temperature, self.top_k, self.top_p,
+                               u.view(bs), workspace=self._accept_ws, out=g.em1[:, 0])
+            else:
+                kernels.spec_accept(lg.view(bs, 1, -1), None, None, u, self.temperature,
+                                    workspace=self._accept_ws, out=(g.n1, g.em1, g.rb1))
             g.drafts[:, i].copy_(g.em1[:, 0])
             tok = g.em1[:, 0]
         g.vids[:, 0].copy_(A["tok0"])
         g.vids[:, 1:].copy_(g.drafts)
         tl = m.forward_packed(g.vids.view(-1), A["vpos"], pool, g.attn[k], A["vslot"])
+        bonus = self._bonus(tl.view(bs, k + 1, -1), g.u, workspace=self._accept_ws,
+                            out=g.bonus)
         kernels.spec_accept(tl.view(bs, k + 1, -1), g.dlog, g.drafts, g.u, self.temperature,
                             g.kvp[k], g.idx[k], A["start"], page_size=self.P,
-                            workspace=self._accept_ws, out=(g.n_out, g.emitted, g.rollback))
+                            workspace=self._accept_ws, out=(g.n_out, g.emitted, g.rollback),
+                            bonus_tokens=bonus)
 
     def _fill_step(self, g: _StepGraph, active: list) -> None:
         """Host side of one step, one native call (``nsg_spec_step_fill``):
@@ -415,7 +442,7 @@ class SpecEngine:
         n_out, emitted, _ = kernels.spec_accept(
             tl.view(B, k + 1, -1), dlog, drafts, u, self.temperature,
             self._to_dev(kvp), self._to_dev(idx), self._to_dev(start_pos, torch.int32),
-            page_size=self.P)
+            page_size=self.P, bonus_tokens=self._bonus(tl.view(B, k + 1, -1), u))
         return n_out.cpu().numpy(), emitted.cpu().numpy()
 
     # ---- main entry ----

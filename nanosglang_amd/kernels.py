@@ -351,12 +351,15 @@ def spec_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor | None,
                 temperature: float, kv_indptr: torch.Tensor | None = None,
                 kv_indices: torch.Tensor | None = None, start_pos: torch.Tensor | None = None,
                 page_size: int = 16, workspace: AcceptWorkspace | None = None,
-                out: tuple | None = None):
+                out: tuple | None = None, bonus_tokens: torch.Tensor | None = None):
     """Fused verify-step acceptance for B requests (C ABI: nsg_spec_accept).
 
     target_logits (B, k+1, V) and draft_logits (B, k, V) in bf16 or fp32 with a
     unit stride along V; draft_tokens int64 (B, k); uniforms fp32 (B, k+1).
     Greedy when ``temperature < 1e-6`` (draft_logits / uniforms may be None).
+    ``bonus_tokens`` int64 (B,) (stochastic only): the token emitted after k
+    accepted drafts, e.g. a top-k / top-p draw from target row k
+    (:func:`sample`); without it that bonus is drawn from softmax(row k / T).
     Returns (num_emitted int32 (B,), emitted int64 (B, k+1) padded -1,
     rollback_slots int64 (B, k) padded -1).
     """
@@ -393,6 +396,13 @@ def spec_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor | None,
             raise ValueError("uniforms must be (B, k+1) float32")
         _require_gpu(uniforms, "uniforms")
         uniforms = uniforms.to(torch.float32).contiguous()
+    if bonus_tokens is not None and not greedy:
+        _require_gpu(bonus_tokens, "bonus_tokens")
+        if tuple(bonus_tokens.shape) != (B,) or bonus_tokens.dtype != torch.int64 \
+                or not bonus_tokens.is_contiguous():
+            raise ValueError("bonus_tokens must be contiguous int64 (B,)")
+    else:
+        bonus_tokens = None
     rb_ok = kv_indptr is not None and k > 0
     if rb_ok:
         for name, t in (("kv_indptr", kv_indptr), ("kv_indices", kv_indices),
@@ -415,12 +425,50 @@ def spec_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor | None,
     rc = lib.nsg_spec_accept(
         target_logits.data_ptr(), target_logits.stride(0), target_logits.stride(1),
         _ptr(draft_logits), d_req, d_row, dt, _ptr(draft_tokens) if k > 0 else None,
-        _ptr(uniforms) if not greedy else None, B, k, V, float(temperature),
+        _ptr(uniforms) if not greedy else None, _ptr(bonus_tokens), B, k, V, float(temperature),
         _ptr(kv_indptr) if rb_ok else None, _ptr(kv_indices) if rb_ok else None,
         _ptr(start_pos) if rb_ok else None, page_size, n_out.data_ptr(), emitted.data_ptr(),
         rollback.data_ptr() if rb_ok else None, ws.data_ptr(), ws.numel(), _stream_ptr(dev))
     check(rc, "nsg_spec_accept")
     return n_out, emitted, rollback
+
+
+def sample(logits: torch.Tensor, temperature: float, top_k: int = 0, top_p: float = 1.0,
+           uniforms: torch.Tensor | None = None, workspace: AcceptWorkspace | None = None,
+           out: torch.Tensor | None = None) -> torch.Tensor:
+    """One token per row of ``logits`` (R, V) -- the reference's
+    ``sample_token(logits, temperature, top_p, top_k)`` (engine/sampling.py:
+    25-50, 71-88) with the draw taken by inverse CDF from ``uniforms`` (R,)
+    (C ABI: nsg_sample).  Argmax when ``temperature < 1e-6``.  Rows may be a
+    strided view with unit stride along V; bf16 or fp32.  Returns int64 (R,)."""
+    _require_gpu(logits, "logits")
+    if logits.dim() != 2:
+        raise ValueError("logits must be (rows, V)")
+    R, V = logits.shape
+    dt = {torch.bfloat16: 0, torch.float32: 1}.get(logits.dtype)
+    if dt is None:
+        raise TypeError(f"logits dtype {logits.dtype}: bf16 or fp32")
+    if logits.stride(1) != 1 and R > 0:
+        raise ValueError("logits must be contiguous along the vocabulary")
+    greedy = temperature < 1e-6
+    if not greedy:
+        if uniforms is None or uniforms.numel() != R:
+            raise ValueError("uniforms (R,) float32 required when temperature > 0")
+        _require_gpu(uniforms, "uniforms")
+        uniforms = uniforms.reshape(R).to(torch.float32).contiguous()
+    dev = logits.device
+    if out is None:
+        out = torch.empty(R, dtype=torch.int64, device=dev)
+    elif out.dtype != torch.int64 or out.numel() != R or (R > 1 and out.stride(0) != 1):
+        raise ValueError("out must be a contiguous int64 (R,) tensor")
+    lib = _lib()
+    need = lib.nsg_sample_workspace_bytes(R, V)
+    ws = (workspace or _accept_ws(dev)).get(need)
+    check(lib.nsg_sample(logits.data_ptr(), logits.stride(0) if R > 1 else V, dt, R, V,
+                         float(temperature), int(top_k), float(top_p),
+                         _ptr(uniforms) if not greedy else None, 1, out.data_ptr(),
+                         ws.data_ptr(), ws.numel(), _stream_ptr(dev)), "nsg_sample")
+    return out
 
 
 def kv_write(k: torch.Tensor, v: torch.Tensor, slots: torch.Tensor, k_cache: torch.Tensor,

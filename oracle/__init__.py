@@ -17,6 +17,9 @@ Modules (each function cites the reference file:line it restates):
 * ``acceptance``       -- greedy and stochastic acceptance, textbook residual
                           resample, bonus token, KV-slot rollback
                           (nano_sglang/decode/speculative.py:130-196).
+* ``sampling``         -- temperature / top-k / top-p sampling in exact
+                          fixed-point arithmetic
+                          (nano_sglang/engine/sampling.py:25-50, 71-88).
 * ``quantization``     -- FP8 (OCP E4M3FN) per-tensor weight quantisation and
                           the dequantisation FP8Linear applies
                           (nano_sglang/decode/quantization.py:24-75), pinned

@@ -190,6 +190,17 @@ def test_accept_workspace_and_argument_checks(lib):
     assert lib.nsg_spec_accept_workspace_bytes(64, 4, 151936) > 64 * 9 * 4 * 8
     assert lib.nsg_spec_accept_workspace_bytes(-1, 4, 10) == -1
     # k beyond the kernel's limit is an argument error before any GPU work
-    rc = lib.nsg_spec_accept(None, 0, 0, None, 0, 0, 0, None, None, 1, 99, 10, 0.0, None,
+    rc = lib.nsg_spec_accept(None, 0, 0, None, 0, 0, 0, None, None, None, 1, 99, 10, 0.0, None,
                              None, None, 16, None, None, None, None, 0, None)
     assert rc == 1 and "k 99" in lib.nsg_last_error().decode()
+
+
+def test_sample_workspace_and_argument_checks(lib):
+    assert lib.nsg_sample_workspace_bytes(64, 151936) > 64 * 8 * 256 * 12
+    assert lib.nsg_sample_workspace_bytes(-1, 10) == -1
+    # argument errors before any GPU work: top_p outside (0, 1], missing uniforms
+    rc = lib.nsg_sample(None, 10, 0, 1, 10, 1.0, 0, 0.0, None, 1, None, None, 0, None)
+    assert rc == 1 and "top_p" in lib.nsg_last_error().decode()
+    rc = lib.nsg_sample(None, 10, 2, 1, 10, 1.0, 0, 1.0, None, 1, None, None, 0, None)
+    assert rc == 1 and "logits_dtype" in lib.nsg_last_error().decode()
+    assert lib.nsg_sample(None, 10, 0, 0, 10, 1.0, 5, 0.5, None, 1, None, None, 0, None) == 0

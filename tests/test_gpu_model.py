@@ -219,6 +219,27 @@ def test_spec_engine_graph_equals_eager_stochastic():
     assert first >= 20
 
 
+@pytest.mark.parametrize("top_k,top_p", [(20, 1.0), (0, 0.8), (50, 0.9)])
+def test_spec_engine_top_k_top_p_graph_equals_eager(top_k, top_p):
+    """Top-k / top-p drafts and bonus (the sampler) inside the captured step:
+    graph and eager runs consume the same Philox words, so they agree."""
+    from nanosglang_amd.engine.spec_engine import SpecEngine
+    print(f"case: spec engine top_k {top_k} top_p {top_p} graph vs eager", flush=True)
+    _, gpu = _tiny_models(scale=1.0)
+    rng = np.random.default_rng(4)
+    prompts = [rng.integers(0, 1000, 33).tolist()]
+    outs = []
+    for graphs in (True, False):
+        eng = SpecEngine(gpu, draft_layers=2, num_speculative=3, num_blocks=64, temperature=0.9,
+                         seed=9, use_graphs=graphs, max_batch=1, top_k=top_k, top_p=top_p)
+        outs.append(eng.generate(prompts, [36])[0])
+    assert len(outs[0]) == len(outs[1]) == 36
+    assert all(0 <= t < 1000 for t in outs[0])
+    first = next((i for i, (a, b) in enumerate(zip(*outs)) if a != b), 36)
+    print(f"  first graph/eager difference at {first}/36", flush=True)
+    assert first >= 18
+
+
 def test_rmsnorm_and_silu_kernels_match_reference_arithmetic():
     """Against the reference's bf16 torch expressions (causal_lm.py:142-154,
     482) evaluated on the GPU: within one bf16 rounding step."""

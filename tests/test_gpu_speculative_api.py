@@ -88,3 +88,24 @@ def test_speculative_step_stochastic_runs():
     draft(ids, torch.arange(5, device="cuda")[None], dc, 0, causal_mask(5, 5))
     acc = spec.speculative_step(torch.tensor([[9]], device="cuda"), 5, dc, tc, causal_mask)
     assert 1 <= len(acc) <= 4 and all(0 <= t < 500 for t in acc)
+
+
+def test_speculative_step_top_k_top_p():
+    """top_k / top_p reach the draft and bonus draws (sample_token sites,
+    speculative.py:95-100, 174-182); top_k = 1 makes each draft the argmax."""
+    from nanosglang_amd.decode.speculative import SpeculativeDecoder, causal_mask
+    target, draft = _GPUModel(4), _GPUModel(2)
+    for top_k, top_p in ((5, 0.8), (0, 0.5), (1, 1.0)):
+        spec = SpeculativeDecoder(draft, target, num_speculative=3, temperature=0.9, seed=3,
+                                  top_k=top_k, top_p=top_p)
+        tc, dc = target.new_cache(64), draft.new_cache(64)
+        ids = torch.tensor([[3, 1, 4, 1, 5]], device="cuda")
+        target(ids, torch.arange(5, device="cuda")[None], tc, 0, causal_mask(5, 5))
+        draft(ids, torch.arange(5, device="cuda")[None], dc, 0, causal_mask(5, 5))
+        acc = spec.speculative_step(torch.tensor([[9]], device="cuda"), 5, dc, tc, causal_mask)
+        assert 1 <= len(acc) <= 4 and all(0 <= t < 500 for t in acc)
+        row = torch.randn(1, 500, device="cuda")
+        if top_k == 1:
+            assert int(spec._sample(row)) == int(row.argmax())
+    with pytest.raises(ValueError):
+        SpeculativeDecoder(draft, target, top_p=0.0)

@@ -23,6 +23,17 @@ three rotated buffer sets) and the large verify shape (Llama-3-8B heads,
 k 8, batch 64, KV U[2048, 8192]).  ``cpu_baseline`` times the oracle's fp32
 PyTorch CPU speculative loop (batch 1, the reference's own algorithm) on a
 bounded sample of the same workload.
+
+    python bench.py --workload large-shape [--steps K] [--warmup W]
+
+measures the large shape end to end instead (not the default line): a
+random-init Llama-3-8B-shape target (32 layers, hidden 4096, 32 q / 8 kv
+heads, head dim 128, FFN 14336, vocab 128256, RoPE theta 5e5) with FP8 E4M3
+per-tensor-scaled decoder weights and bf16 KV, a draft of its first 4
+layers, k = 8, 64 requests with contexts U[2048, 8192], 32 output tokens
+each, stochastic verification at T = 1.0 (Philox uniforms).  The contexts'
+K/V are seeded pool noise instead of a prefill (decoding alone is timed);
+long KV ranges are split over workgroups and merged inside the captured step.
 """
 
 from __future__ import annotations
@@ -207,6 +218,64 @@ def cpu_baseline(prompts, outs, n_tokens=48):
             "torch": torch.__version__}
 
 
+def large_shape(args, torch):
+    """The large shape end to end (decoding only): 8B-shape FP8 target, k 8,
+    batch 64, contexts U[2048, 8192], T 1.0."""
+    from nanosglang_amd.engine.spec_engine import SpecEngine
+    from nanosglang_amd.model.causal_lm import CausalLM, ModelConfig
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, k, n_out, P = 64, 8, 32, 16
+    rng = np.random.default_rng(0)
+    ctx = rng.integers(2048, 8193, B)
+    cfg = ModelConfig(model_type="llama", vocab_size=128256, hidden_size=4096,
+                      intermediate_size=14336, num_hidden_layers=32, num_attention_heads=32,
+                      num_key_value_heads=8, max_position_embeddings=8192 + 256,
+                      rms_norm_eps=1e-5, rope_theta=5e5, tie_word_embeddings=False,
+                      attention_bias=False)
+    t0 = time.perf_counter()
+    model = CausalLM(cfg, device=dev, seed=0).quantize_fp8()
+    torch.cuda.empty_cache()
+    log(f"8B-shape FP8 model built in {time.perf_counter() - t0:.1f} s")
+    blocks = int(sum((int(L) + n_out + k + 1 + P - 1) // P for L in ctx)) + B + 8
+    engine = SpecEngine(model, draft_layers=4, num_speculative=k, num_blocks=blocks,
+                        block_size=P, temperature=1.0, seed=0, max_batch=B, kv_split=True)
+    prompts = [[int(t)] * int(L) for t, L in zip(rng.integers(0, cfg.vocab_size, B), ctx)]
+    outs = [n_out] * B
+    t_cap = time.perf_counter()
+    sizes = engine.capture()
+    log(f"captured spec-step graphs for batch sizes {sizes} in "
+        f"{time.perf_counter() - t_cap:.1f} s")
+    for w in range(args.warmup):
+        engine.generate(prompts, outs, synthetic_context=True)
+        log(f"warmup {w}: {engine.stats}")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n_tok, steps, stats = 0, 0, []
+    for s in range(args.steps):
+        res = engine.generate(prompts, outs, synthetic_context=True)
+        n_tok += sum(len(r) - 1 for r in res)       # the first token is the prompt's last
+        stats.append(dict(engine.stats))
+        steps += engine.stats["steps"]
+        log(f"step {s}: {engine.stats}")
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    result = {
+        "metric": "spec-decode tok/s, decoding only (8B-shape FP8, k=8, bs=64, ctx 2-8K, T=1)",
+        "value": round(n_tok / elapsed, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 2),
+        "ms_per_spec_step": round(elapsed / max(1, steps) * 1e3, 2),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp8 weights / bf16", "data": "synthetic (random-init weights, noise KV context)",
+        "config": {"workload": "8B-shape spec decode: 32-layer FP8 target / 4-layer draft, k=8, "
+                               "64 requests, contexts U[2048,8192], 32 outputs, T=1.0",
+                   "batch": B, "k": k, "page_size": P, "num_blocks": blocks},
+        "acceptance_rate": round(float(np.mean([s["acceptance_rate"] for s in stats])), 4),
+        "tokens_per_step": round(float(np.mean([s["tokens_per_step"] for s in stats])), 3),
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -214,6 +283,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-kernels", action="store_true")
+    ap.add_argument("--workload", default="0.5b", choices=["0.5b", "large-shape"],
+                    help="large-shape: the 8B-shape FP8 end-to-end line instead of the default")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only a 256 MiB device copy (3x) and 10 verify-attention launches at "
                          "the verify shape, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
@@ -227,6 +298,9 @@ def main():
     sys.path.insert(0, ROOT)
     if args.pmc_probe:
         pmc_probe(torch)
+        return
+    if args.workload == "large-shape":
+        large_shape(args, torch)
         return
     from nanosglang_amd.engine.spec_engine import SpecEngine
     from nanosglang_amd.model.causal_lm import CausalLM, ModelConfig

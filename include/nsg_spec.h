@@ -42,7 +42,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 9
+#define NSG_ABI_VERSION 10
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -343,6 +343,14 @@ int32_t nsg_linear_rope_kv_fp8(const void* x, int64_t ldx, const void* w8, int64
  * apply_rope (:300-301) and the KV scatter (:335-338).  head_dim 64 or 128;
  * M <= nsg_linear_max_rows(); K % 64 == 0.  Arguments after K mean what
  * they mean for nsg_rope_kv_write. */
+/* bf16 copy of FP8 weights for a library GEMM (row counts past the
+ * weight-streaming kernel, prefill): out[r][c] = bf16(float(w8[r][c]) *
+ * w_scale[r]), the dequantisation of FP8Linear.forward (w8.to(bf16) * scale,
+ * nano_sglang/decode/quantization.py:49-52) in one pass.  w8: rows x cols
+ * float8_e4m3fn, rows ld8 bytes apart; out: bf16 rows ldo elements apart. */
+int32_t nsg_dequant_fp8(const void* w8, int64_t ld8, const float* w_scale, void* out,
+                        int64_t ldo, int32_t rows, int32_t cols, nsg_stream_t stream);
+
 int32_t nsg_linear_rope_kv(const void* x, int64_t ldx, const void* w, int64_t ldw,
                            const void* bias, int32_t M, int32_t K, int32_t num_qo_heads,
                            int32_t num_kv_heads, int32_t head_dim, const int64_t* positions,

@@ -49,7 +49,7 @@ struct LinParams {
   int64_t ldx, ldw, ldy;
   int M, N, K;     // N: output columns (SwiGLU: the intermediate size I)
   int w_rows;      // rows of W (N, or 2 I for SwiGLU)
-  int row_groups;  // > 1: M runs as groups of kRowGroup rows, one workgroup each
+  int row_groups;  // > 1: M runs as groups of MG * MT * 16 rows, one workgroup each
   int col_tiles;   // column tiles (workgroups per row group)
   // RoPE + KV-slot epilogue (q/k/v projection): one workgroup per head
   const int64_t* pos;
@@ -65,7 +65,6 @@ struct LinParams {
   int* flags;
 };
 
-constexpr int kRowGroup = 32;
 
 enum { kEpiBias = 0, kEpiSilu = 1, kEpiRope = 2 };
 
@@ -118,8 +117,8 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
     tile = xcd + 8 * (slot / p.row_groups);
     if (tile >= p.col_tiles) return;
-    m0 = (slot % p.row_groups) * kRowGroup;
-    M = min(kRowGroup, p.M - m0);
+    m0 = (slot % p.row_groups) * (MG * MT * 16);
+    M = min(MG * MT * 16, p.M - m0);
     xg += (int64_t)m0 * p.ldx;
     yg += (int64_t)m0 * p.ldy;
   }
@@ -439,6 +438,8 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
 // (read from L2 once per workgroup) stays a small multiple of W's bytes.
 template <int MT, int MG, int NT, int NW, int EPI>
 int32_t launch_cfg(LinParams p, hipStream_t s) {
+  constexpr int kRows = MG * MT * 16;  // rows per workgroup
+  p.row_groups = p.M > kRows ? (p.M + kRows - 1) / kRows : 1;
   if (p.w8) {
     const int cols_per_wg = 16 * (EPI == kEpiSilu ? NT / 2 : NT);
     p.col_tiles = (p.N + cols_per_wg - 1) / cols_per_wg;
@@ -457,8 +458,8 @@ int32_t launch_cfg(LinParams p, hipStream_t s) {
   return launch_status("linear_kernel");
 }
 
-// Up to kRowGroup rows: one workgroup per column tile.  More rows run as
-// groups of kRowGroup rows, one workgroup per (column tile, group), with the
+// Up to MG * MT * 16 rows: one workgroup per column tile.  More rows run as
+// groups of that many rows, one workgroup per (column tile, group), with the
 // groups of a tile on one XCD.  Tile shape per row count, measured on MI355X
 // for the shapes of the verify forward (graph replay, weights cold): the
 // workgroup count against 256 CUs decides most of it, since each CU streams
@@ -467,7 +468,6 @@ constexpr int kWideN = 65536;
 
 template <int EPI>
 int32_t launch_epi(LinParams p, hipStream_t s) {
-  p.row_groups = p.M > kRowGroup ? (p.M + kRowGroup - 1) / kRowGroup : 1;
   if constexpr (EPI == kEpiSilu) {
     // NT counts gate and up tiles: NT = 2 is one output column tile
     if (p.M <= 16) return launch_cfg<1, 1, 2, 2, EPI>(p, s);
@@ -491,7 +491,6 @@ int32_t launch_epi(LinParams p, hipStream_t s) {
 // RoPE epilogue: a workgroup per (head, 16 rotation pairs) -- two column
 // tiles -- and row group.
 int32_t launch_rope(LinParams p, hipStream_t s) {
-  p.row_groups = p.M > kRowGroup ? (p.M + kRowGroup - 1) / kRowGroup : 1;
   if (p.M <= 16) return launch_cfg<1, 1, 2, 8, kEpiRope>(p, s);
   return launch_cfg<2, 1, 2, 8, kEpiRope>(p, s);
 }
@@ -670,4 +669,61 @@ extern "C" int32_t nsg_linear_rope_kv_fp8(const void* x, int64_t ldx, const void
   return rope_impl(x, ldx, nullptr, w8, ldw8, w_scale, bias, M, K, num_qo_heads, num_kv_heads,
                    head_dim, positions, cos_table, sin_table, max_position, slots, q_out, k_cache,
                    v_cache, num_slots, flags, stream);
+}
+
+// ---- FP8 weights for a library GEMM (many rows, prefill) ----
+// The dequantisation of FP8Linear.forward (w8.to(bf16) * scale,
+// quantization.py:49-52) in one pass: 16 weight bytes per thread in, 32
+// bytes of bf16 out, the same per-value arithmetic as the in-register path
+// (exact e4m3 -> f32, times the row scale, one round to nearest even).
+namespace nsg {
+namespace {
+
+__global__ __launch_bounds__(256) void dequant_fp8_kernel(const uint8_t* w8, int64_t ld8,
+                                                          const float* scale, uint16_t* out,
+                                                          int64_t ldo, int rows, int cols,
+                                                          bool vec) {
+  const int64_t gpr = (cols + 15) / 16;  // 16-value groups per row
+  const int64_t total = (int64_t)rows * gpr;
+  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < total;
+       g += (int64_t)gridDim.x * blockDim.x) {
+    const int row = (int)(g / gpr);
+    const int c0 = (int)(g % gpr) * 16;
+    const float s = scale[row];
+    const uint8_t* src = w8 + (int64_t)row * ld8 + c0;
+    uint16_t* dst = out + (int64_t)row * ldo + c0;
+    if (vec && c0 + 16 <= cols) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(src);
+      *reinterpret_cast<u32x4*>(dst) = dequant_fp8x8(u32x2{v[0], v[1]}, s);
+      *reinterpret_cast<u32x4*>(dst + 8) = dequant_fp8x8(u32x2{v[2], v[3]}, s);
+    } else {
+      for (int c = 0; c < 16 && c0 + c < cols; ++c) {
+        const floatx2_t f = __builtin_amdgcn_cvt_pk_f32_fp8((int)src[c], false);
+        dst[c] = float_to_bf16_bits(f[0] * s);
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace nsg
+
+extern "C" int32_t nsg_dequant_fp8(const void* w8, int64_t ld8, const float* w_scale, void* out,
+                                   int64_t ldo, int32_t rows, int32_t cols, nsg_stream_t stream) {
+  NSG_CHECK_ARG(rows >= 0 && cols >= 0, "rows %d, cols %d", rows, cols);
+  if (rows == 0 || cols == 0) {
+    clear_error();
+    return NSG_OK;
+  }
+  NSG_CHECK_ARG(w8 && w_scale && out, "null pointer argument");
+  NSG_CHECK_ARG(ld8 >= cols && ldo >= cols, "ld8 %lld / ldo %lld < cols %d", (long long)ld8,
+                (long long)ldo, cols);
+  const bool vec = reinterpret_cast<uintptr_t>(w8) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(out) % 16 == 0 && ld8 % 16 == 0 && ldo % 8 == 0;
+  const int64_t groups = (int64_t)rows * ((cols + 15) / 16);
+  const int grid = (int)std::min<int64_t>((groups + 255) / 256, 8192);
+  hipLaunchKernelGGL(dequant_fp8_kernel, dim3(grid), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(w8), ld8,
+                     w_scale, static_cast<uint16_t*>(out), ldo, rows, cols, vec);
+  return launch_status("dequant_fp8_kernel");
 }

@@ -180,7 +180,8 @@ class SpecEngine:
     def __init__(self, model, draft_layers: int, num_speculative: int, num_blocks: int,
                  block_size: int = 16, temperature: float = 0.0, seed: int = 0,
                  workspace_bytes: int = 256 << 20, use_graphs: bool = True,
-                 max_batch: int = 32, top_k: int = 0, top_p: float = 1.0):
+                 max_batch: int = 32, top_k: int = 0, top_p: float = 1.0,
+                 kv_split: bool = False):
         c = model.config
         self.model = model
         self.k = num_speculative
@@ -209,8 +210,11 @@ class SpecEngine:
         self._dummy_block = None
         self._tab = np.zeros((0, 0), np.int32)     # page-table mirror of graph mode
         # decode / verify contexts never exceed the position table: the
-        # captured attention plans need no KV split (and no merge launch)
-        self.max_kv_len = min(c.max_position_embeddings, 1022 * block_size)
+        # captured attention plans need no KV split (and no merge launch).
+        # kv_split: long contexts (thousands of tokens) are split over more
+        # workgroups instead, with the merge launch captured as well.
+        self.max_kv_len = 0 if kv_split else min(c.max_position_embeddings, 1022 * block_size)
+        self._noise = False
 
     # ---- helpers ----
     def _uniforms(self, stream: int, n: int) -> torch.Tensor:
@@ -447,7 +451,13 @@ class SpecEngine:
 
     # ---- main entry ----
     @torch.inference_mode()
-    def generate(self, prompts: list[list[int]], max_new_tokens: list[int]):
+    def generate(self, prompts: list[list[int]], max_new_tokens: list[int],
+                 synthetic_context: bool = False):
+        """Serve ``prompts`` to ``max_new_tokens`` tokens each (EOS ignored).
+
+        ``synthetic_context``: measure decoding alone -- the prompt positions'
+        K/V are the pool's seeded noise instead of a prefill forward, and the
+        first output token is the prompt's last id."""
         k = self.k
         reqs = [_Req(i, list(p), int(m)) for i, (p, m) in enumerate(zip(prompts, max_new_tokens))]
         if self.use_graphs and len(reqs) > self.max_batch:
@@ -464,13 +474,23 @@ class SpecEngine:
                 r.row = i
         # 2. prefill (one ragged packed forward)
         lens = [len(r.prompt) for r in reqs]
-        self._plan(reqs, lens, lens)
-        ids = self._to_dev(np.concatenate([np.asarray(r.prompt, np.int64) for r in reqs]))
-        pos = self._to_dev(np.concatenate([np.arange(n, dtype=np.int64) for n in lens]))
-        slots = self._to_dev(self._slots(reqs, [0] * len(reqs), lens))
-        last_idx = self._to_dev(np.cumsum(lens) - 1)
-        logits = self.model.forward_packed(ids, pos, self._pool(), self.attn, slots, last_idx)
-        first = self._sample_rows(logits).cpu().tolist()
+        if synthetic_context:
+            if not self._noise:
+                g = torch.Generator(device=self.device).manual_seed(self.seed)
+                for pool in self._pool():
+                    for layer in pool:
+                        layer.normal_(generator=g)
+                self._noise = True
+            first = [r.prompt[-1] for r in reqs]
+        else:
+            self._plan(reqs, lens, lens)
+            ids = self._to_dev(np.concatenate([np.asarray(r.prompt, np.int64) for r in reqs]))
+            pos = self._to_dev(np.concatenate([np.arange(n, dtype=np.int64) for n in lens]))
+            slots = self._to_dev(self._slots(reqs, [0] * len(reqs), lens))
+            last_idx = self._to_dev(np.cumsum(lens) - 1)
+            logits = self.model.forward_packed(ids, pos, self._pool(), self.attn, slots,
+                                               last_idx)
+            first = self._sample_rows(logits).cpu().tolist()
         for r, f in zip(reqs, first):
             r.out.append(f)
             r.start = len(r.prompt)

@@ -570,8 +570,19 @@ FP8 = torch.float8_e4m3fn
 
 def dequant_fp8(w8: torch.Tensor, w_scale: torch.Tensor) -> torch.Tensor:
     """bf16(float(w8) * w_scale[row]): the weights the FP8 kernels multiply
-    (FP8Linear.forward's ``w8.to(bf16) * scale``, quantization.py:49-52)."""
-    return (w8.float() * w_scale.float()[:, None]).to(torch.bfloat16)
+    (FP8Linear.forward's ``w8.to(bf16) * scale``, quantization.py:49-52), in
+    one HIP pass (C ABI: nsg_dequant_fp8)."""
+    _require_gpu(w8, "w8")
+    if w8.dtype != FP8 or w8.dim() != 2 or w8.stride(1) != 1:
+        raise ValueError("w8 must be float8_e4m3fn (rows, cols) with unit inner stride")
+    rows, cols = w8.shape
+    w_scale = w_scale.to(torch.float32).contiguous()
+    if w_scale.numel() != rows:
+        raise ValueError(f"w_scale must hold one f32 per row ({rows})")
+    out = torch.empty(rows, cols, dtype=torch.bfloat16, device=w8.device)
+    check(_lib().nsg_dequant_fp8(w8.data_ptr(), w8.stride(0), w_scale.data_ptr(), out.data_ptr(),
+                                 cols, rows, cols, _stream_ptr(w8.device)), "nsg_dequant_fp8")
+    return out
 
 
 def _check_fp8(weight, w_scale, K):

@@ -310,6 +310,26 @@ def test_fp8_dequant_matches_torch_on_the_gpu():
     assert cpu_form_differs >= 20
 
 
+def test_fp8_dequant_kernel_all_codes_tails_and_strides():
+    """nsg_dequant_fp8 (one pass, 16 bytes per thread) = torch's
+    (float(w8) * row_scale).to(bf16) bit for bit: every e4m3 code, per-row
+    scales, a column count with a scalar tail and rows wider than the copy."""
+    from nanosglang_amd import kernels
+    g = torch.Generator(device="cuda").manual_seed(7)
+    for rows, cols, ld in ((256, 256, 256), (37, 1000, 1000), (9, 77, 96)):
+        codes = torch.randint(0, 256, (rows, ld), generator=g, device="cuda", dtype=torch.int32)
+        codes[:, :256 if cols >= 256 else cols] = torch.arange(256 if cols >= 256 else cols,
+                                                                 device="cuda", dtype=torch.int32)
+        base = codes.to(torch.uint8).view(torch.float8_e4m3fn)
+        w8 = base[:, :cols]
+        sc = torch.rand(rows, generator=g, device="cuda") * 3e-3 + 1e-5
+        ref = (w8.float() * sc[:, None]).to(torch.bfloat16)
+        got = kernels.dequant_fp8(w8, sc)
+        nan = torch.isnan(ref)
+        assert torch.equal(torch.isnan(got), nan)
+        assert torch.equal(got[~nan].view(torch.int16), ref[~nan].view(torch.int16)), (rows, cols)
+
+
 def _fp8_weights(rows_blocks, K, seed):
     from nanosglang_amd.model.quantization import fp8_quantize_rows
     g = torch.Generator(device="cuda").manual_seed(seed)

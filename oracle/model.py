@@ -32,12 +32,14 @@ with ``seed``, drawn in a fixed order (embed, then per layer q, k, v, o, gate,
 up, down), RMSNorm weights 1, q/k/v biases 0; lm_head tied to the embedding
 (Qwen2.5-0.5B ties them).
 
-Pinning: incremental decoding with the KV cache must equal a full-sequence
-forward (catches RoPE position, cache and mask errors), and greedy
-speculative decoding must equal plain greedy decoding of the target for any
-draft (the speculative-sampling invariant) -- tests/test_oracle_model.py.
-Bitwise agreement with the reference's own forward is parity unpinned (it
-would need the reference imported).
+Pinning: the forward reproduces, bit for bit, fp32 logits that the
+reference's own CausalLM.forward wrote (tests/golden/make_model_golden.py ->
+tests/golden/model_forward_golden.npz: a tiny Qwen2-style config with random
+biases and norm weights, a full forward and a cached prefill + verify-style
+call; tests/test_oracle_model_golden.py).  Besides, incremental decoding with
+the KV cache must equal a full-sequence forward, and greedy speculative
+decoding must equal plain greedy decoding of the target for any draft (the
+speculative-sampling invariant) -- tests/test_oracle_model.py.
 """
 
 from __future__ import annotations

@@ -450,29 +450,19 @@ class SpecEngine:
         return n_out.cpu().numpy(), emitted.cpu().numpy()
 
     # ---- main entry ----
-    @torch.inference_mode()
-    def generate(self, prompts: list[list[int]], max_new_tokens: list[int],
-                 synthetic_context: bool = False):
-        """Serve ``prompts`` to ``max_new_tokens`` tokens each (EOS ignored).
-
-        ``synthetic_context``: measure decoding alone -- the prompt positions'
-        K/V are the pool's seeded noise instead of a prefill forward, and the
-        first output token is the prompt's last id."""
-        k = self.k
-        reqs = [_Req(i, list(p), int(m)) for i, (p, m) in enumerate(zip(prompts, max_new_tokens))]
-        if self.use_graphs and len(reqs) > self.max_batch:
-            raise ValueError(f"{len(reqs)} requests > max_batch {self.max_batch} of the graphs")
-        if self.use_graphs and not self._graphs:
-            self.capture()
-        t0 = time.perf_counter()
-        # 1. admission
+    def _admit(self, reqs: list, synthetic_context: bool = False) -> None:
+        """Admission and prefill: a block table per request
+        (paged_kv_cache.py:113-120), one ragged packed forward over every
+        prompt (engine.py:298-472), the first token of each request.
+        ``synthetic_context``: the prompt positions' K/V are the pool's seeded
+        noise instead (decoding measured alone); the first token is then the
+        prompt's last id."""
         for r in reqs:
             r.table = self.kv.allocate_for_request(len(r.prompt))
         if self.use_graphs:
             self._tab = np.zeros((len(reqs), self._max_pages()), np.int32)
             for i, r in enumerate(reqs):
                 r.row = i
-        # 2. prefill (one ragged packed forward)
         lens = [len(r.prompt) for r in reqs]
         if synthetic_context:
             if not self._noise:
@@ -494,6 +484,94 @@ class SpecEngine:
         for r, f in zip(reqs, first):
             r.out.append(f)
             r.start = len(r.prompt)
+
+    def _step(self, active: list):
+        """One speculative step for the active requests: reserve the verify
+        window's pages (scheduler.py:221-232 applied to k + 1 positions),
+        draft, verify and accept (graph or eager), append the emitted tokens,
+        advance the positions and roll back pages past them.  Returns the
+        per-request emitted counts."""
+        k = self.k
+        for r in active:
+            self.kv.reserve(r.table, r.start + k + 1)
+            if self.use_graphs:
+                self._sync_table(r)
+        if self.use_graphs:
+            n_h, em_h = self._step_graph(active)
+        else:
+            n_h, em_h = self._step_eager(active)
+        for j, r in enumerate(active):
+            n = int(n_h[j])
+            r.out.extend(em_h[j, :n].tolist())
+            r.start += n
+            self.kv.truncate(r.table, r.start)        # rollback of rejected pages
+            r.synced = min(r.synced, len(r.table.block_indices))
+        return n_h
+
+    def _check_batch(self, n: int) -> None:
+        if self.use_graphs and n > self.max_batch:
+            raise ValueError(f"{n} requests > max_batch {self.max_batch} of the graphs")
+        if self.use_graphs and not self._graphs:
+            self.capture()
+
+    @torch.inference_mode()
+    def prefill(self, prompts: list[list[int]]):
+        """Admit and prefill ``prompts`` (additive API, with
+        :meth:`speculative_step_batch`).  Returns (first tokens, block
+        tables): request b's KV cache holds positions < len(prompts[b]) in
+        block_tables[b]; its first token sits at position len(prompts[b])."""
+        self._check_batch(len(prompts))
+        reqs = [_Req(i, list(p), 1) for i, p in enumerate(prompts)]
+        self._admit(reqs)
+        return [r.out[0] for r in reqs], [r.table for r in reqs]
+
+    @torch.inference_mode()
+    def speculative_step_batch(self, last_tokens: list[int], start_pos: list[int],
+                               block_tables: list[BlockTable]) -> list[list[int]]:
+        """One batched speculative step on the paged cache (additive API: the
+        reference's ``speculative_step``, speculative.py:50-184, is batch-1).
+
+        Request b's last emitted token ``last_tokens[b]`` sits at position
+        ``start_pos[b]``; its KV cache holds positions < start_pos[b] in
+        ``block_tables[b]``.  Drafts k tokens, verifies them in one target
+        forward, accepts, and returns the 1..k+1 emitted tokens per request.
+        The tables are grown for the verify window and rolled back past the
+        kept positions (the next call's start is start_pos[b] + len(result[b]),
+        its last token result[b][-1])."""
+        B = len(last_tokens)
+        if len(start_pos) != B or len(block_tables) != B:
+            raise ValueError("last_tokens, start_pos and block_tables disagree on the batch")
+        if B == 0:
+            return []
+        self._check_batch(B)
+        reqs = []
+        for i, (t, s, bt) in enumerate(zip(last_tokens, start_pos, block_tables)):
+            r = _Req(i, [], 1 << 30, table=bt, out=[int(t)], start=int(s))
+            if r.start < 0 or len(bt.block_indices) * self.P < r.start:
+                raise ValueError(f"request {i}: start {r.start} beyond its block table")
+            reqs.append(r)
+        if self.use_graphs:
+            self._tab = np.zeros((B, self._max_pages()), np.int32)
+            for i, r in enumerate(reqs):
+                r.row = i
+        self._step(reqs)
+        return [r.out[1:] for r in reqs]
+
+    @torch.inference_mode()
+    def generate(self, prompts: list[list[int]], max_new_tokens: list[int],
+                 synthetic_context: bool = False):
+        """Serve ``prompts`` to ``max_new_tokens`` tokens each (EOS ignored).
+
+        ``synthetic_context``: measure decoding alone -- the prompt positions'
+        K/V are the pool's seeded noise instead of a prefill forward, and the
+        first output token is the prompt's last id."""
+        k = self.k
+        reqs = [_Req(i, list(p), int(m)) for i, (p, m) in enumerate(zip(prompts, max_new_tokens))]
+        self._check_batch(len(reqs))
+        t0 = time.perf_counter()
+        # 1-2. admission and prefill
+        self._admit(reqs, synthetic_context)
+        lens = [len(r.prompt) for r in reqs]
         t_prefill = time.perf_counter() - t0
         steps = proposed = accepted = req_steps = 0
         active = [r for r in reqs if len(r.out) < r.max_new]
@@ -503,25 +581,13 @@ class SpecEngine:
         # 3. speculative steps
         while active:
             B = len(active)
-            for r in active:
-                self.kv.reserve(r.table, r.start + k + 1)
-                if self.use_graphs:
-                    self._sync_table(r)
-            if self.use_graphs:
-                n_h, em_h = self._step_graph(active)
-            else:
-                n_h, em_h = self._step_eager(active)
+            n_h = self._step(active)
             steps += 1
             req_steps += B
             proposed += B * k
             accepted += int(n_h.sum()) - B
             still = []
-            for j, r in enumerate(active):
-                n = int(n_h[j])
-                r.out.extend(em_h[j, :n].tolist())
-                r.start += n
-                self.kv.truncate(r.table, r.start)        # rollback of rejected pages
-                r.synced = min(r.synced, len(r.table.block_indices))
+            for r in active:
                 if len(r.out) >= r.max_new:
                     del r.out[r.max_new:]
                     self.kv.free_request(r.table)

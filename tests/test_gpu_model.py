@@ -219,6 +219,43 @@ def test_spec_engine_graph_equals_eager_stochastic():
     assert first >= 20
 
 
+@pytest.mark.parametrize("graphs", [True, False])
+def test_spec_engine_step_api_equals_generate(graphs):
+    """prefill + speculative_step_batch, driven by hand, emit exactly what
+    generate does (greedy), and leave the pool as generate leaves it."""
+    from nanosglang_amd.engine.spec_engine import SpecEngine
+    print(f"case: spec engine step API, graphs={graphs}", flush=True)
+    _, gpu = _tiny_models()
+    rng = np.random.default_rng(6)
+    prompts = [rng.integers(0, 1000, n).tolist() for n in (12, 40, 7)]
+    max_new = [21, 9, 30]
+    mk = lambda: SpecEngine(gpu, draft_layers=2, num_speculative=3, num_blocks=64,
+                            use_graphs=graphs, max_batch=4)
+    ref = mk().generate(prompts, max_new)
+    eng = mk()
+    first, tables = eng.prefill(prompts)
+    outs = [[f] for f in first]
+    starts = [len(p) for p in prompts]
+    active = [i for i in range(len(prompts)) if len(outs[i]) < max_new[i]]
+    while active:
+        res = eng.speculative_step_batch([outs[i][-1] for i in active],
+                                         [starts[i] for i in active],
+                                         [tables[i] for i in active])
+        assert all(1 <= len(r) <= 4 for r in res)
+        for i, r in zip(active, res):
+            outs[i].extend(r)
+            starts[i] += len(r)
+        done = [i for i in active if len(outs[i]) >= max_new[i]]
+        for i in done:
+            del outs[i][max_new[i]:]
+            eng.kv.free_request(tables[i])
+        active = [i for i in active if i not in done]
+    assert outs == ref
+    assert eng.bm.num_free_blocks == 64 - (1 if graphs else 0)
+    with pytest.raises(ValueError):
+        eng.speculative_step_batch([1], [40], [tables[0]])   # start beyond the table
+
+
 @pytest.mark.parametrize("top_k,top_p", [(20, 1.0), (0, 0.8), (50, 0.9)])
 def test_spec_engine_top_k_top_p_graph_equals_eager(top_k, top_p):
     """Top-k / top-p drafts and bonus (the sampler) inside the captured step:

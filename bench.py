@@ -291,7 +291,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the verify "
-              f"step runs on a single MI355X in this build.", file=sys.stderr)
+              f"step runs on a single MI355X.", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -11,7 +11,7 @@ Mirrors nano_sglang/decode/quantization.py's FP8 path:
   the HIP weight-streaming kernel reading the FP8 bytes directly
   (``kernels.linear``, C ABI ``nsg_linear_fp8``);
 * ``quantize_model`` -- the reference's module walk (:202-243) for FP8
-  (AWQ/INT4 is not part of this build).
+  (AWQ/INT4 is not implemented here).
 
 ``CausalLM.quantize_fp8()`` applies the same per-tensor rule to the packed
 decoder weights (q, k and v, and gate and up, keep separate scales, as the

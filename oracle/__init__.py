@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product path (``nanosglang_amd``)
 imports this package; only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` use it, and only as the checker or as the
+``cpu_baseline`` leg of ``bench.py`` use it, and only to check results or as the
 timed CPU baseline -- never as a fallback for the HIP kernels.
 
 Modules (each function cites the reference file:line it restates):

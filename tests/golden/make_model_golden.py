@@ -3,8 +3,8 @@ reference's own CausalLM.forward (nano_sglang/model/causal_lm.py:564-583) on a
 tiny random-init Qwen2-style config, the vectors that pin the oracle's model
 restatement (oracle/model.py) to the reference bit for bit.
 
-Runs only in the build container (it imports the reference from
-/root/reference; the GPU box has no copy):
+Runs only where the reference sources are present (it imports them from
+/root/reference); the tests read the committed .npz alone:
 
     python tests/golden/make_model_golden.py
 

@@ -51,13 +51,15 @@ def test_linear_bias_matches_fp32_reference(M, N, K):
     _check_bias(y0, x, w, None)
 
 
-@pytest.mark.parametrize("M", [1, 2, 16, 17, 32])
-def test_linear_wide_output_matches_fp32_reference(M):
+@pytest.mark.parametrize("M,K", [(1, 256), (2, 256), (8, 256), (9, 256), (16, 256), (17, 256),
+                                 (32, 256), (16, 2048), (24, 2048), (32, 4096)])
+def test_linear_wide_output_matches_fp32_reference(M, K):
     """Very wide outputs (lm_head: N >= 65536 columns) take their own tile
-    shapes; N is not a multiple of any workgroup's columns."""
+    shapes, by row count and row length; N is not a multiple of any
+    workgroup's columns."""
     from nanosglang_amd import kernels
-    print(f"case: linear wide M={M}", flush=True)
-    x, w, b = _data(M, 65540, 256, seed=40 + M)
+    print(f"case: linear wide M={M} K={K}", flush=True)
+    x, w, b = _data(M, 65540, K, seed=40 + M)
     y = kernels.linear(x, w, b, force=True)
     torch.cuda.synchronize()
     _check_bias(y, x, w, b)

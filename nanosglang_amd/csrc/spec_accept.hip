@@ -78,6 +78,7 @@ struct AccParams {
   float* dec;     // [B][8]
   float* psum;    // [B][nch2]
   float2* rsum;   // [B][kRsRanges][kRsMaxSteps] step sums (residual, target)
+  float* xlog;    // [rows] logit at the row's draft token (stochastic rows i < k)
   int* flags;
 };
 
@@ -211,6 +212,17 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
   const int v1 = min(p.V, v0 + p.cs);
   const int tid = threadIdx.x;
   const bool vec = ((roff % Logit<T>::kAlign) == 0);
+  // stochastic rows i < k: the chunk holding the draft token records that
+  // logit, so the decision needs no second read of the logits
+  int xt = -1;
+  float xval = 0.f;
+  bool xhit = false;
+  if constexpr (!GREEDY) {
+    if (i < p.k) {
+      const int64_t x = p.dtok[(int64_t)b * p.k + i];
+      if (x >= v0 && x < v1) xt = (int)x;
+    }
+  }
 
   // stochastic: running reference m and sum of 2^(x c - m).  m starts finite
   // (-FLT_MAX): an all -inf chunk then sums exact zeros instead of NaN.
@@ -222,6 +234,10 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
     if constexpr (GREEDY) {
       am_merge(bv, bi, x, v);
     } else {
+      if (v == xt) {
+        xval = x;
+        xhit = true;
+      }
       const float y = x * p.c;
       if (y > m) {
         s = s * exp2f(m - y);
@@ -248,6 +264,12 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
         }
       }
     } else {
+      if (__builtin_expect(vv == (xt & ~7), 0)) {  // never for xt = -1
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (e == (xt & 7)) xval = x[e];
+        xhit = true;
+      }
       // lazy rescale: the reference m moves only when a logit exceeds it by
       // more than kSlack (terms stay <= 2^kSlack), so the common path is one
       // compare per 8 logits and fma + exp + add per logit
@@ -314,6 +336,9 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
   // scalar, in increasing index per thread
   for (int vv = (vec ? vfull : v0) + tid; vv < v1; vv += kThreads) take(Logit<T>::at(base, roff + vv), vv);
 
+  if constexpr (!GREEDY) {
+    if (xhit) p.xlog[r] = xval;
+  }
   const int lane = tid & 63, wave = tid >> 6;
   if constexpr (GREEDY) {
     wave_am(bv, bi);
@@ -384,14 +409,23 @@ struct Decision {
 
 // Stochastic decision of request b, computed by one wave, returned to every
 // lane.  Lane i (i <= k) reduces the chunk stats of target row i, lane i < k
-// also those of draft row i and runs ratio test i; a ballot finds the first
-// rejection.  Three dependent load rounds in all (stats, draft ids, logits).
+// also those of draft row i and runs ratio test i with the draft-token logits
+// stats_kernel recorded; a ballot finds the first rejection.  Every load is
+// issued before the arithmetic: one memory round trip.
 // With `write`, the wave also writes the accepted prefix, num_emitted, the
 // rollback slots and the decision record read by select_kernel.
 template <typename T>
 __device__ Decision decide(const AccParams& p, int b, bool write) {
   const int lane = threadIdx.x & 63;
   const int k = p.k;
+  int64_t x = 0;
+  float xt = 0.f, xd = 0.f, u = 0.f;
+  if (lane < k) {
+    x = p.dtok[(int64_t)b * k + lane];
+    xt = p.xlog[b * (k + 1) + lane];
+    xd = p.xlog[p.B * (k + 1) + b * k + lane];
+    u = p.u[(int64_t)b * (k + 1) + lane];
+  }
   float mt = -INFINITY, zt = 0.f, md = -INFINITY, zd = 0.f;
   if (lane <= k) {
     const float2* st = p.stats + (int64_t)(b * (k + 1) + lane) * p.nch;
@@ -410,18 +444,16 @@ __device__ Decision decide(const AccParams& p, int b, bool write) {
     }
   }
   bool reject = false;
-  int64_t x = 0;
   if (lane < k) {
-    x = p.dtok[(int64_t)b * k + lane];
     if (x < 0 || x >= p.V) {
       if (write) atomicOr(p.flags, 4);
       reject = true;
     } else {
-      const float lt = Logit<T>::at(p.tl, trow(p, b, lane) + x) * p.c;
-      const float ld = Logit<T>::at(p.dl, drow(p, b, lane) + x) * p.c;
+      const float lt = xt * p.c;
+      const float ld = xd * p.c;
       const float pt = exp2f(lt - mt) / zt;
       const float pd = exp2f(ld - md) / zd;
-      reject = pd > 0.f && !(p.u[(int64_t)b * (k + 1) + lane] < fminf(1.f, pt / pd));
+      reject = pd > 0.f && !(u < fminf(1.f, pt / pd));
     }
   }
   const uint64_t rej = __builtin_amdgcn_ballot_w64(reject);
@@ -812,25 +844,13 @@ __device__ __forceinline__ Decision load_decision(const float* dd) {
   return d;
 }
 
+// Streams ns steps of the decided row pair from vocabulary index v0 (this
+// lane's first logit) and writes each step's sums (residual, target) -- each
+// an inclusive wave scan of the lanes' 8-logit runs -- to out[0 .. ns).
 template <typename T>
-__global__ __launch_bounds__(kRsThreads) void resolve_kernel(AccParams p) {
-  __shared__ Decision s_d;
-  const int b = blockIdx.y;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  if (wave == 0) {
-    const Decision d = decide<T>(p, b, blockIdx.x == 0);  // split 0 writes the outputs
-    if (lane == 0) s_d = d;
-  }
-  __syncthreads();
-  const Decision d = s_d;
-  if (d.mode == 1 && p.bonus) return;  // the bonus comes from the caller
-  const int64_t to = trow(p, b, d.j);
-  const int64_t dof = d.mode == 0 ? drow(p, b, d.j) : 0;
-  const int ns = rs_steps(p.V);
-  const int r = blockIdx.x * kRsWaves + wave;
-  const int v0 = r * ns * kRsStep + 8 * lane;
-  float2* out = p.rsum + ((int64_t)b * kRsRanges + r) * kRsMaxSteps;
+__device__ __forceinline__ void stream_step_sums(const AccParams& p, const Decision& d,
+                                                 int64_t to, int64_t dof, int ns, int v0,
+                                                 int lane, float2* out) {
   constexpr int G = 8;  // steps whose loads are in flight together
   for (int q0 = 0; q0 < ns; q0 += G) {
     StepRaw<T> raw[G];
@@ -850,24 +870,45 @@ __global__ __launch_bounds__(kRsThreads) void resolve_kernel(AccParams p) {
 }
 
 template <typename T>
-__global__ __launch_bounds__(64) void select_kernel2(AccParams p) {
-  const int b = blockIdx.x;
-  const int lane = threadIdx.x;
-  const Decision d = load_decision(p.dec + (int64_t)b * 8);
-  if (d.mode == 1 && p.bonus) {  // all accepted: the caller's filtered bonus draw
-    if (lane == 0) p.emitted[(int64_t)b * (p.k + 1) + d.j] = p.bonus[b];
-    return;
+__global__ __launch_bounds__(kRsThreads) void resolve_kernel(AccParams p) {
+  __shared__ Decision s_d;
+  const int b = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  if (wave == 0) {
+    const Decision d = decide<T>(p, b, blockIdx.x == 0);  // split 0 writes the outputs
+    if (lane == 0) s_d = d;
   }
+  __syncthreads();
+  const Decision d = s_d;
+  if (d.mode == 1 && p.bonus) return;  // the bonus comes from the caller
+  const int ns = rs_steps(p.V);
+  const int r = blockIdx.x * kRsWaves + wave;
+  stream_step_sums<T>(p, d, trow(p, b, d.j), d.mode == 0 ? drow(p, b, d.j) : 0, ns,
+                      r * ns * kRsStep + 8 * lane, lane,
+                      p.rsum + ((int64_t)b * kRsRanges + r) * kRsMaxSteps);
+}
+
+// The token of request b from the step sums of R contiguous vocabulary
+// ranges of ns steps each (range r: steps r*ns .. r*ns + ns - 1; its sums at
+// sums[r * S .. r * S + ns)), one wave: lane r sums range r's steps in
+// order, a wave scan orders the ranges, the crossing lane finds its step,
+// and the whole wave recomputes that one step with the same arithmetic
+// (step_weights) to find the lane and the logit.  Rounding that leaves no
+// crossing picks the last positive weight.
+template <typename T, int R, int S>
+__device__ void select_token(const AccParams& p, int b, const Decision& d, int lane,
+                             const float2* sums, int ns) {
+  static_assert(R <= 64, "one range per lane");
   const int64_t to = trow(p, b, d.j);
   const int64_t dof = d.mode == 0 ? drow(p, b, d.j) : 0;
   const float u = p.u[(int64_t)b * (p.k + 1) + p.k];
-  const int ns = rs_steps(p.V);
-  const float2* rs = p.rsum + ((int64_t)b * kRsRanges + lane) * kRsMaxSteps;
-  float sr[kRsMaxSteps], sp[kRsMaxSteps];
+  const float2* rs = sums + (int64_t)min(lane, R - 1) * S;
+  float sr[S], sp[S];
   float lr = 0.f, lp = 0.f;
 #pragma unroll
-  for (int q = 0; q < kRsMaxSteps; ++q) {
-    const float2 v = q < ns ? rs[q] : make_float2(0.f, 0.f);
+  for (int q = 0; q < S; ++q) {
+    const float2 v = (lane < R && q < ns) ? rs[q] : make_float2(0.f, 0.f);
     sr[q] = v.x;
     sp[q] = v.y;
     lr += v.x;
@@ -895,7 +936,7 @@ __global__ __launch_bounds__(64) void select_kernel2(AccParams p) {
   float acc = lane == 0 ? 0.f : excl;
   if (lane == rsel) {
 #pragma unroll
-    for (int q = 0; q < kRsMaxSteps; ++q) {
+    for (int q = 0; q < S; ++q) {
       const float sq = use_pt ? sp[q] : sr[q];
       if (qs < 0 && q < ns) {
         if (!fallback && sq > 0.f && acc + sq > target) qs = q;
@@ -905,14 +946,14 @@ __global__ __launch_bounds__(64) void select_kernel2(AccParams p) {
     if (qs < 0) {  // rounding: last positive step of the range
       fallback = true;
 #pragma unroll
-      for (int q = 0; q < kRsMaxSteps; ++q)
+      for (int q = 0; q < S; ++q)
         if (q < ns && (use_pt ? sp[q] : sr[q]) > 0.f) qs = q;
     }
   }
   qs = __shfl(qs, rsel, 64);
   acc = __shfl(acc, rsel, 64);
   fallback = __shfl((int)fallback, rsel, 64) != 0;
-  // recompute that step exactly as resolve_kernel summed it
+  // recompute that step exactly as it was summed
   const int v = (rsel * ns + qs) * kRsStep + 8 * lane;
   StepRaw<T> raw;
   step_load<T>(p, to, dof, d.mode, v, raw);
@@ -939,9 +980,23 @@ __global__ __launch_bounds__(64) void select_kernel2(AccParams p) {
   }
 }
 
+template <typename T>
+__global__ __launch_bounds__(64) void select_kernel2(AccParams p) {
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x;
+  const Decision d = load_decision(p.dec + (int64_t)b * 8);
+  if (d.mode == 1 && p.bonus) {  // all accepted: the caller's filtered bonus draw
+    if (lane == 0) p.emitted[(int64_t)b * (p.k + 1) + d.j] = p.bonus[b];
+    return;
+  }
+  select_token<T, kRsRanges, kRsMaxSteps>(p, b, d, lane,
+                                          p.rsum + (int64_t)b * kRsRanges * kRsMaxSteps,
+                                          rs_steps(p.V));
+}
+
 struct Layout {
   int rows, nch, cs, nch2, cs2;
-  int64_t stats_off, dec_off, psum_off, rsum_off, total;
+  int64_t stats_off, dec_off, psum_off, rsum_off, xlog_off, total;
 };
 
 Layout layout(int B, int k, int V, bool greedy) {
@@ -961,7 +1016,8 @@ Layout layout(int B, int k, int V, bool greedy) {
   L.dec_off = L.stats_off + al((int64_t)rows_max * kMaxChunks * 8);
   L.psum_off = L.dec_off + al((int64_t)B * 8 * 4);
   L.rsum_off = L.psum_off + al((int64_t)B * kMaxChunks * 4);
-  L.total = L.rsum_off + al((int64_t)B * kRsRanges * kRsMaxSteps * 8);
+  L.xlog_off = L.rsum_off + al((int64_t)B * kRsRanges * kRsMaxSteps * 8);
+  L.total = L.xlog_off + al((int64_t)rows_max * 4);
   return L;
 }
 
@@ -1087,6 +1143,7 @@ extern "C" int32_t nsg_spec_accept(const void* target_logits, int64_t target_req
   p.dec = reinterpret_cast<float*>(ws + L.dec_off);
   p.psum = reinterpret_cast<float*>(ws + L.psum_off);
   p.rsum = reinterpret_cast<float2*>(ws + L.rsum_off);
+  p.xlog = reinterpret_cast<float*>(ws + L.xlog_off);
   // 16-byte vector loads need 16-byte aligned bases; rows are checked per row
   const uintptr_t mis = reinterpret_cast<uintptr_t>(target_logits) |
                         (greedy ? 0 : reinterpret_cast<uintptr_t>(draft_logits));

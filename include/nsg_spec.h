@@ -42,7 +42,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 10
+#define NSG_ABI_VERSION 11
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -200,6 +200,11 @@ int32_t nsg_spec_step_fill(const int32_t* page_table, int64_t page_table_stride,
  * k may be 0: the call then samples one token per request from row 0
  *   (argmax when greedy), which is the reference's sample_token
  *   (sampling.py:25-50) without top-k / top-p (nsg_sample has them).
+ * Bad inputs found on the device leave well-defined outputs and set bits of
+ *   an error-flag word at the start of the workspace (which should start at
+ *   zero), read with nsg_spec_accept_check_flags: bit 1, a rolled-back
+ *   position past the request's pages (its slot is -1); bit 2, a draft token
+ *   outside [0, vocab) (rejected, as a draft the target never proposes).
  * ---------------------------------------------------------------------- */
 int64_t nsg_spec_accept_workspace_bytes(int32_t batch, int32_t k, int32_t vocab);
 
@@ -214,6 +219,10 @@ int32_t nsg_spec_accept(const void* target_logits, int64_t target_req_stride,
                         int32_t page_size, int32_t* num_emitted, int64_t* emitted,
                         int64_t* rollback_slots, void* workspace, int64_t workspace_bytes,
                         nsg_stream_t stream);
+
+/* Copies the acceptance workspace's error flags (bits as above) to *flags_h
+ * after synchronising the stream, and clears them. */
+int32_t nsg_spec_accept_check_flags(void* workspace, int32_t* flags_h, nsg_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Sampling with temperature, top-k and top-p: one token per logits row.

@@ -377,6 +377,10 @@ __global__ __launch_bounds__(64) void greedy_finalize_kernel(AccParams p) {
   const int lane = threadIdx.x;
   const int k = p.k;
   int64_t* em = p.emitted + (int64_t)b * (k + 1);
+  if (lane < k) {  // a draft token outside the vocabulary never matches; flag it
+    const int64_t d = p.dtok[(int64_t)b * k + lane];
+    if (d < 0 || d >= p.V) atomicOr(p.flags, 4);
+  }
   int n = k + 1;
   for (int i = 0; i <= k; ++i) {
     const int r = b * (k + 1) + i;
@@ -1160,4 +1164,15 @@ extern "C" int32_t nsg_spec_accept(const void* target_logits, int64_t target_req
     return NSG_ERR_ARG;
   }
   return launch_accept<float>(p, L.rows, s);
+}
+
+extern "C" int32_t nsg_spec_accept_check_flags(void* workspace, int32_t* flags_h,
+                                               nsg_stream_t stream) {
+  NSG_CHECK_ARG(workspace && flags_h, "null argument");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  NSG_CHECK_HIP(hipMemcpyAsync(flags_h, workspace, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+  NSG_CHECK_HIP(hipStreamSynchronize(s));
+  NSG_CHECK_HIP(hipMemsetAsync(workspace, 0, sizeof(int32_t), s));
+  clear_error();
+  return NSG_OK;
 }

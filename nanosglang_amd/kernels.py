@@ -335,6 +335,18 @@ class AcceptWorkspace:
                                    device=self.device)
         return self.buf
 
+    def check_flags(self) -> int:
+        """Synchronises and returns (then clears) the acceptance kernels'
+        error flags: bit 1, a rolled-back position past its request's pages;
+        bit 2, a draft token outside [0, vocab)."""
+        if self.buf.numel() == 0:
+            return 0
+        f = C.c_int32(0)
+        check(_lib().nsg_spec_accept_check_flags(self.buf.data_ptr(), C.byref(f),
+                                                 _stream_ptr(self.device)),
+              "nsg_spec_accept_check_flags")
+        return f.value
+
 
 _default_ws: dict[torch.device, AcceptWorkspace] = {}
 

@@ -145,6 +145,48 @@ def test_rollback_without_page_table_is_minus_one():
     assert (rb == -1).all()
 
 
+@pytest.mark.parametrize("temperature", [0.0, 0.8])
+def test_bad_device_inputs_set_flags_and_keep_outputs_defined(temperature):
+    """Draft tokens outside the vocabulary are rejected and set flag bit 2;
+    rolled-back positions past a request's pages get slot -1 and set bit 1;
+    nsg_spec_accept_check_flags returns the flags and clears them."""
+    from nanosglang_amd.kernels import AcceptWorkspace, spec_accept
+    B, k, V = 4, 3, 1000
+    a = workloads.acceptance_batch(batch=B, k=k, vocab=V, seed=9)
+    greedy = temperature < 1e-6
+    ws = AcceptWorkspace("cuda")
+    start, indptr, indices = _page_table(B, k, 9)
+    t, d = _dev(a["target"], torch.bfloat16), _dev(a["draft"], torch.bfloat16)
+    u = _dev(_uniforms(B, k, 9), torch.float32)
+
+    def call(tokens, start):
+        n, em, rb = spec_accept(t, None if greedy else d, _dev(tokens, torch.int64),
+                                None if greedy else u, temperature, _dev(indptr, torch.int32),
+                                _dev(indices, torch.int32), _dev(start, torch.int32),
+                                page_size=16, workspace=ws)
+        return n.cpu().numpy(), em.cpu().numpy(), rb.cpu().numpy()
+
+    n0, em0, rb0 = call(a["draft_tokens"], start)
+    assert ws.check_flags() == 0
+    bad = a["draft_tokens"].copy()
+    bad[1, 0] = V
+    bad[2, 0] = -1
+    n, em, rb = call(bad, start)
+    assert ws.check_flags() == 4
+    assert ws.check_flags() == 0                     # cleared by the read
+    for b in (1, 2):                                 # rejected at position 0
+        assert n[b] == 1 and 0 <= em[b, 0] < V and (em[b, 1:] == -1).all()
+        assert (rb[b] >= 0).all()
+    np.testing.assert_array_equal(n[[0, 3]], n0[[0, 3]])
+    np.testing.assert_array_equal(em[[0, 3]], em0[[0, 3]])
+    # request 1's verify positions lie past its pages: every rollback slot -1
+    past = start.copy()
+    past[1] = (indptr[2] - indptr[1]) * 16
+    n, em, rb = call(bad, past)
+    assert ws.check_flags() == 4 | 2
+    assert n[1] == 1 and (rb[1] == -1).all()
+
+
 def test_bad_arguments_raise():
     from nanosglang_amd.kernels import spec_accept
     t = torch.zeros(2, 5, 100, dtype=torch.bfloat16, device="cuda")

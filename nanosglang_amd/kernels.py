@@ -60,6 +60,21 @@ def _dev_i32(t, device) -> torch.Tensor:
     return torch.as_tensor(t, dtype=torch.int32).contiguous().to(device, non_blocking=True)
 
 
+def attn_work_bound(qo_h: np.ndarray, kvp_h: np.ndarray, last_h: np.ndarray,
+                    num_qo_heads: int, num_kv_heads: int, page_size: int) -> int:
+    """Upper bound on the work (plus merge) items of a dynamic attention plan:
+    every query tile split into every 32-token KV step, plus one merge item."""
+    bound = 0
+    G = max(1, num_qo_heads // max(1, num_kv_heads))
+    T = max(1, min(64 // G, int(np.diff(qo_h).max(initial=1))))
+    for b in range(len(qo_h) - 1):
+        ql = int(qo_h[b + 1] - qo_h[b])
+        npg = int(kvp_h[b + 1] - kvp_h[b])
+        L = (npg - 1) * page_size + int(last_h[b]) if npg else 0
+        bound += math.ceil(ql / T) * (1 + max(1, math.ceil(L / 32)))
+    return bound
+
+
 class BatchPrefillWithPagedKVCacheWrapper:
     """Ragged multi-query attention over an NHD paged KV cache.
 
@@ -255,15 +270,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
 
     def _plan_dynamic(self, lib, qo_h, kvp_h, last_h, B, num_qo_heads, num_kv_heads,
                       head_dim_qk, page_size, causal) -> AttnPlan:
-        # an upper bound on work items: every query tile split into every 32-token step
-        bound = 0
-        G = max(1, num_qo_heads // max(1, num_kv_heads))
-        T = max(1, min(64 // G, int(np.diff(qo_h).max(initial=1))))
-        for b in range(B):
-            ql = int(qo_h[b + 1] - qo_h[b])
-            npg = int(kvp_h[b + 1] - kvp_h[b])
-            L = (npg - 1) * page_size + int(last_h[b]) if npg else 0
-            bound += math.ceil(ql / T) * (1 + max(1, math.ceil(L / 32)))
+        bound = attn_work_bound(qo_h, kvp_h, last_h, num_qo_heads, num_kv_heads, page_size)
         if bound > self._work_cap:
             self._work_cap = max(bound, 2 * self._work_cap, 64)
             self._work_h = np.zeros(self._work_cap * NSG_ATTN_WORK_INTS, np.int32)

@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import ctypes as C
 import math
+import threading
 
 import numpy as np
 import torch
@@ -355,14 +356,21 @@ class AcceptWorkspace:
         return f.value
 
 
-_default_ws: dict[torch.device, AcceptWorkspace] = {}
+_default_ws: dict[tuple, AcceptWorkspace] = {}
+_default_ws_lock = threading.Lock()
 
 
 def _accept_ws(device) -> AcceptWorkspace:
+    """The default workspace of the current stream on ``device``: calls on one
+    stream run in order, so they may share it; calls on different streams (or
+    threads using different streams) get their own."""
     device = torch.device(device)
-    if device not in _default_ws:
-        _default_ws[device] = AcceptWorkspace(device)
-    return _default_ws[device]
+    key = (device, _stream_ptr(device))
+    ws = _default_ws.get(key)
+    if ws is None:
+        with _default_ws_lock:
+            ws = _default_ws.setdefault(key, AcceptWorkspace(device))
+    return ws
 
 
 def spec_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor | None,

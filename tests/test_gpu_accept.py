@@ -187,6 +187,32 @@ def test_bad_device_inputs_set_flags_and_keep_outputs_defined(temperature):
     assert n[1] == 1 and (rb[1] == -1).all()
 
 
+def test_calls_on_two_streams_use_separate_default_workspaces():
+    """Stochastic calls enqueued on two streams at once, each with the
+    default workspace: the same results as the calls one after the other."""
+    from nanosglang_amd.kernels import spec_accept
+    B, k, V = 16, 4, 20000
+    inputs = []
+    for seed in (11, 12):
+        a = workloads.acceptance_batch(batch=B, k=k, vocab=V, seed=seed)
+        inputs.append((_dev(a["target"], torch.bfloat16), _dev(a["draft"], torch.bfloat16),
+                       _dev(a["draft_tokens"], torch.int64),
+                       _dev(_uniforms(B, k, seed), torch.float32)))
+    ref = [spec_accept(t, d, x, u, 0.8) for t, d, x, u in inputs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [None, None]
+    for rep in range(3):
+        for i, s in enumerate(streams):
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                outs[i] = spec_accept(*inputs[i][:3], inputs[i][3], 0.8)
+        torch.cuda.synchronize()
+        for i in range(2):
+            for x, y in zip(outs[i], ref[i]):
+                assert torch.equal(x, y), (rep, i)
+
+
 def test_bad_arguments_raise():
     from nanosglang_amd.kernels import spec_accept
     t = torch.zeros(2, 5, 100, dtype=torch.bfloat16, device="cuda")

@@ -222,3 +222,31 @@ def test_bad_arguments_raise():
     with pytest.raises(TypeError):
         spec_accept(t.half(), None, torch.zeros(2, 4, dtype=torch.int64, device="cuda"),
                     None, 0.0)
+
+
+def test_greedy_large_shape_full_size_closed_form():
+    """The large shape's acceptance (64 requests, k = 8, vocab 128,256, bf16),
+    greedy: the closed form -- drafts accepted while each equals the first
+    argmax of its target row, then that argmax emitted -- with drafts that
+    match a random prefix of every request."""
+    from nanosglang_amd.kernels import spec_accept
+    B, k, V = 64, 8, 128256
+    print("case: greedy acceptance, large shape", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(22)
+    tl = (2 * torch.randn(B, k + 1, V, generator=g, device="cuda")).bfloat16()
+    am = tl.float().argmax(-1).cpu().numpy()          # first maximal index
+    rng = np.random.default_rng(22)
+    prefix = rng.integers(0, k + 1, B)
+    drafts = rng.integers(0, V, (B, k))
+    for b in range(B):
+        drafts[b, :prefix[b]] = am[b, :prefix[b]]
+        if prefix[b] < k and drafts[b, prefix[b]] == am[b, prefix[b]]:
+            drafts[b, prefix[b]] = (am[b, prefix[b]] + 1) % V
+    n, em, rb = spec_accept(tl, None, _dev(drafts, torch.int64), None, 0.0)
+    n, em = n.cpu().numpy(), em.cpu().numpy()
+    np.testing.assert_array_equal(n, prefix + 1)
+    for b in range(B):
+        j = prefix[b]
+        assert list(em[b, :j]) == list(drafts[b, :j])
+        assert em[b, j] == am[b, j]
+        assert (em[b, j + 1:] == -1).all()

@@ -222,3 +222,55 @@ def test_graph_mode_replays_after_replanning(q_len, B, max_kv):
         assert err <= TOL_SPEC
         assert (np.abs(got - ref) <= TOL_TIGHT + 2.0 ** -8 * np.abs(ref)).all()
     assert wg.check_flags() == 0
+
+
+def test_large_shape_full_size():
+    """The large shape itself: 64 requests of 9 query tokens, 32 / 8 heads,
+    head dim 128, KV lengths U[2048, 8192] on 16-token pages scattered over
+    the pool.  Two requests (the first and the longest) against the oracle;
+    the whole output unchanged, bit for bit, when the pool's pages move and
+    the page table follows them."""
+    from nanosglang_amd.kernels import BatchPrefillWithPagedKVCacheWrapper
+    B, ql, Hq, Hkv, D, P = 64, 9, 32, 8, 128, 16
+    rng = np.random.default_rng(21)
+    L = rng.integers(2048, 8193, B)
+    npg = (L + P - 1) // P
+    N = int(npg.sum()) + 64
+    idx = rng.permutation(N)[:npg.sum()].astype(np.int32)
+    kvp = np.concatenate([[0], np.cumsum(npg)]).astype(np.int32)
+    qo = (np.arange(B + 1) * ql).astype(np.int32)
+    last = (L - (npg - 1) * P).astype(np.int32)
+    print(f"case: large shape full size, {N} pages, L max {L.max()}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(21)
+    q = torch.randn(B * ql, Hq, D, generator=g, device="cuda").bfloat16()
+    k = (0.5 * torch.randn(N, P, Hkv, D, generator=g, device="cuda")).bfloat16()
+    v = (0.5 * torch.randn(N, P, Hkv, D, generator=g, device="cuda")).bfloat16()
+    ws = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+
+    def run(k_, v_, idx_):
+        w = BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+        w.plan(qo, kvp, idx_, last, Hq, Hkv, D, P)
+        out = w.run(q, (k_, v_))
+        torch.cuda.synchronize()
+        assert w.check_flags() == 0
+        return out, w.plan_info
+
+    out, plan = run(k, v, idx)
+    assert plan.max_splits > 1 and plan.num_merge > 0     # the split-and-merge regime
+    moved = torch.from_numpy(rng.permutation(N)).cuda()   # new location of page p
+    k2, v2 = torch.empty_like(k), torch.empty_like(v)
+    k2[moved], v2[moved] = k, v
+    out2, _ = run(k2, v2, moved.cpu().numpy()[idx].astype(np.int32))
+    assert torch.equal(out, out2)
+    del k2, v2
+    for b in (0, int(np.argmax(L))):
+        pages = torch.from_numpy(idx[kvp[b]:kvp[b + 1]].astype(np.int64)).cuda()
+        ref = verify_attention(q[b * ql:(b + 1) * ql].float().cpu().numpy(),
+                               k[pages].float().cpu().numpy(), v[pages].float().cpu().numpy(),
+                               np.array([0, ql], np.int32), np.array([0, npg[b]], np.int32),
+                               np.arange(npg[b], dtype=np.int32), last[b:b + 1],
+                               1.0 / np.sqrt(D), True)
+        got = out[b * ql:(b + 1) * ql].float().cpu().numpy()
+        err = np.abs(got - ref)
+        print(f"  request {b} (L {L[b]}): max abs err {err.max():.2e}", flush=True)
+        assert (err <= TOL_TIGHT + 2.0 ** -8 * np.abs(ref)).all()

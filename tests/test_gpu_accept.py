@@ -250,3 +250,49 @@ def test_greedy_large_shape_full_size_closed_form():
         assert list(em[b, :j]) == list(drafts[b, :j])
         assert em[b, j] == am[b, j]
         assert (em[b, j + 1:] == -1).all()
+
+
+def test_stochastic_large_shape_full_size_properties():
+    """The large shape's stochastic acceptance (64 requests, k = 8, vocab
+    128,256, T = 1, bf16) through properties that need no full oracle run:
+    accepted drafts are emitted unchanged; every decided ratio test agrees
+    with u vs min(1, p_t / p_d) recomputed in float64 (or lies within 1e-5 of
+    it); a token drawn after a rejection lies in the residual's support
+    (p_t > p_d).  Identical draft and target rows accept all k drafts."""
+    from nanosglang_amd.kernels import spec_accept
+    B, k, V, T = 64, 8, 128256, 1.0
+    print("case: stochastic acceptance, large shape", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(23)
+    dl = (2 * torch.randn(B, k, V, generator=g, device="cuda")).bfloat16()
+    tl = torch.empty(B, k + 1, V, dtype=torch.bfloat16, device="cuda")
+    tl[:, :k] = (dl.float() + 0.5 * torch.randn(B, k, V, generator=g, device="cuda")).bfloat16()
+    tl[:, k] = (2 * torch.randn(B, V, generator=g, device="cuda")).bfloat16()
+    pd = torch.softmax(dl.double() / T, -1)
+    drafts = torch.multinomial(pd.view(-1, V).float(), 1, generator=g).view(B, k)
+    u = torch.from_numpy(_uniforms(B, k, 23)).cuda()
+    n, em, _ = spec_accept(tl, dl, drafts, u, T)
+    n, em = n.cpu().numpy(), em.cpu().numpy()
+    lpt = torch.log_softmax(tl.double() / T, -1)
+    lpd = torch.log_softmax(dl.double() / T, -1)
+    d_h, u_h = drafts.cpu().numpy(), u.cpu().numpy()
+    ratio = torch.exp(lpt[:, :k].gather(-1, drafts[..., None]) -
+                      lpd.gather(-1, drafts[..., None]))[..., 0].clamp(max=1.0).cpu().numpy()
+    rejected = 0
+    for b in range(B):
+        j = n[b] - 1
+        assert 0 <= j <= k
+        assert list(em[b, :j]) == list(d_h[b, :j])
+        for i in range(j):                                # accepted: u < min(1, ratio)
+            assert u_h[b, i] < ratio[b, i] or abs(u_h[b, i] - ratio[b, i]) < MARGIN
+        if j < k:                                         # rejected at j
+            rejected += 1
+            assert u_h[b, j] >= ratio[b, j] or abs(u_h[b, j] - ratio[b, j]) < MARGIN
+            x = int(em[b, j])
+            assert 0 <= x < V
+            assert lpt[b, j, x] > lpd[b, j, x] - 1e-9     # residual support
+        assert (em[b, j + 1:] == -1).all()
+    print(f"  rejections {rejected} / {B}", flush=True)
+    assert rejected > 0
+    tl[:, :k] = dl                                        # identical distributions
+    n, _, _ = spec_accept(tl, dl, drafts, u, T)
+    assert (n.cpu().numpy() == k + 1).all()

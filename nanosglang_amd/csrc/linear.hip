@@ -480,9 +480,11 @@ int32_t launch_epi(LinParams p, hipStream_t s) {
     if (p.N >= kWideN) {  // lm_head
       if (p.M == 1) return launch_cfg<1, 1, 1, 8, EPI>(p, s);
       if (p.M <= 8) return launch_cfg<1, 1, 2, 8, EPI>(p, s);
+      if (p.K >= 2048) {  // long rows (8B-class lm_head): eight column tiles
+        if (p.M <= 16) return launch_cfg<2, 1, 8, 4, EPI>(p, s);
+        return launch_cfg<2, 1, 8, 2, EPI>(p, s);
+      }
       if (p.M <= 16) return launch_cfg<1, 1, 4, 1, EPI>(p, s);
-      // long rows: one wave per workgroup keeps more workgroups per CU
-      if (p.K >= 2048) return launch_cfg<2, 1, 4, 1, EPI>(p, s);
       return launch_cfg<2, 1, 4, 2, EPI>(p, s);
     }
     if (p.M <= 16) return launch_cfg<1, 1, 1, 8, EPI>(p, s);

@@ -180,6 +180,35 @@ def pmc_probe(torch):
 
 COPY_BYTES = 256 << 20
 
+# the large verify shape: 8B-shape heads, k = 8, batch 64, contexts U[2048, 8192]
+LARGE_SHAPE = dict(batch=64, q_len=9, num_qo_heads=32, num_kv_heads=8, head_dim=128,
+                   min_len=2048, max_len=8192, num_pages=21000)
+
+
+def pmc_probe_large(torch, launches=3):
+    """Verify-attention launches at the large shape alone (plus their merge
+    launches), for rocprofv3 --pmc passes such as MfmaUtil / MfmaFlopsBF16."""
+    from nanosglang_amd import workloads
+    from nanosglang_amd.kernels import BatchPrefillWithPagedKVCacheWrapper
+    dev = torch.device("cuda", 0)
+    c = workloads.verify_attention_batch(seed=0, **LARGE_SHAPE)
+    Hq, Hkv, D = c["q"].shape[1], c["k"].shape[2], c["k"].shape[3]
+    k = torch.from_numpy(c["k"]).to(dev).bfloat16()
+    v = torch.from_numpy(c["v"]).to(dev).bfloat16()
+    q = torch.from_numpy(c["q"]).to(dev).bfloat16()
+    ws = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    wr = BatchPrefillWithPagedKVCacheWrapper(ws)
+    wr.plan(c["qo_indptr"], c["kv_indptr"], c["kv_indices"], c["kv_last_page_len"], Hq, Hkv, D,
+            c["page_size"])
+    out = torch.empty_like(q)
+    torch.cuda.synchronize()
+    for _ in range(launches):
+        wr.run(q, (k, v), out=out)
+    torch.cuda.synchronize()
+    flops = sum(4 * Hq * D * sum(int(L) - int(ql) + r + 1 for r in range(int(ql)))
+                for ql, L in zip(c["q_lens"], c["kv_lens"]))
+    print(json.dumps({"attention_launches": launches, "attention_flops": flops}), flush=True)
+
 
 def traffic_bytes():
     """HBM bytes per verify-attention launch at the verify shape, from the
@@ -288,6 +317,9 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only a 256 MiB device copy (3x) and 10 verify-attention launches at "
                          "the verify shape, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
+    ap.add_argument("--pmc-probe-large", action="store_true",
+                    help="only 3 verify-attention launches at the large shape, for rocprofv3 "
+                         "--pmc passes (MFMA utilisation)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the verify "
@@ -298,6 +330,9 @@ def main():
     sys.path.insert(0, ROOT)
     if args.pmc_probe:
         pmc_probe(torch)
+        return
+    if args.pmc_probe_large:
+        pmc_probe_large(torch)
         return
     if args.workload == "large-shape":
         large_shape(args, torch)
@@ -366,9 +401,7 @@ def main():
         log(f"acceptance stochastic: {acc_s}")
         acc_g = bench_acceptance(torch, dev, greedy=True)
         log(f"acceptance greedy: {acc_g}")
-        big = bench_verify_attention(torch, None, dev, reps=20, pools=1, shape=dict(
-            batch=64, q_len=9, num_qo_heads=32, num_kv_heads=8, head_dim=128, min_len=2048,
-            max_len=8192, num_pages=21000))
+        big = bench_verify_attention(torch, None, dev, reps=20, pools=1, shape=LARGE_SHAPE)
         log(f"verify attention (large shape): {big}")
 
         def k_entry(d):

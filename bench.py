@@ -185,6 +185,41 @@ LARGE_SHAPE = dict(batch=64, q_len=9, num_qo_heads=32, num_kv_heads=8, head_dim=
                    min_len=2048, max_len=8192, num_pages=21000)
 
 
+def pmc_probe_accept(torch, sets=3):
+    """A 256 MiB device copy (3x, the counter calibration), then one
+    stochastic and one greedy acceptance call at the acceptance shape on each
+    of `sets` rotated buffer sets, for rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes."""
+    from nanosglang_amd import workloads
+    from nanosglang_amd.kernels import philox_uniform, spec_accept
+    dev = torch.device("cuda", 0)
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    a = workloads.acceptance_batch(seed=0)
+    B, k1, V = a["target"].shape
+    tl = torch.from_numpy(a["target"]).to(dev).bfloat16()
+    dl = torch.from_numpy(a["draft"]).to(dev).bfloat16()
+    dt = torch.from_numpy(a["draft_tokens"]).to(dev)
+    u = philox_uniform(123, 0, 0, B * k1, dev).view(B, k1)
+    bufs = [(tl, dl)] + [(tl.clone(), dl.clone()) for _ in range(sets - 1)]
+    torch.cuda.synchronize()
+    for t_, d_ in bufs:
+        spec_accept(t_, d_, dt, u, a["temperature"])
+    for t_, d_ in bufs:
+        spec_accept(t_, None, dt, None, 0.0)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "calls": sets,
+                      "stochastic_algorithmic_bytes":
+                          workloads.algorithmic_bytes_acceptance(B, k1 - 1, V, False),
+                      "greedy_algorithmic_bytes":
+                          workloads.algorithmic_bytes_acceptance(B, k1 - 1, V, True)}),
+          flush=True)
+
+
 def pmc_probe_large(torch, launches=3):
     """Verify-attention launches at the large shape alone (plus their merge
     launches), for rocprofv3 --pmc passes such as MfmaUtil / MfmaFlopsBF16."""
@@ -317,6 +352,10 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only a 256 MiB device copy (3x) and 10 verify-attention launches at "
                          "the verify shape, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
+    ap.add_argument("--pmc-probe-accept", action="store_true",
+                    help="only a 256 MiB device copy (3x) and 3 stochastic + 3 greedy acceptance "
+                         "calls at the acceptance shape, for rocprofv3 --pmc FETCH_SIZE / "
+                         "WRITE_SIZE passes")
     ap.add_argument("--pmc-probe-large", action="store_true",
                     help="only 3 verify-attention launches at the large shape, for rocprofv3 "
                          "--pmc passes (MFMA utilisation)")
@@ -330,6 +369,9 @@ def main():
     sys.path.insert(0, ROOT)
     if args.pmc_probe:
         pmc_probe(torch)
+        return
+    if args.pmc_probe_accept:
+        pmc_probe_accept(torch)
         return
     if args.pmc_probe_large:
         pmc_probe_large(torch)

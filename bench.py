@@ -221,11 +221,19 @@ def pmc_probe_accept(torch, sets=3):
 
 
 def pmc_probe_large(torch, launches=3):
-    """Verify-attention launches at the large shape alone (plus their merge
-    launches), for rocprofv3 --pmc passes such as MfmaUtil / MfmaFlopsBF16."""
+    """A 256 MiB device copy (3x, the counter calibration), then
+    verify-attention launches at the large shape (plus their merge launches),
+    for rocprofv3 --pmc passes (MfmaUtil / MfmaFlopsBF16, FETCH_SIZE /
+    WRITE_SIZE)."""
     from nanosglang_amd import workloads
     from nanosglang_amd.kernels import BatchPrefillWithPagedKVCacheWrapper
     dev = torch.device("cuda", 0)
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
     c = workloads.verify_attention_batch(seed=0, **LARGE_SHAPE)
     Hq, Hkv, D = c["q"].shape[1], c["k"].shape[2], c["k"].shape[3]
     k = torch.from_numpy(c["k"]).to(dev).bfloat16()
@@ -242,7 +250,11 @@ def pmc_probe_large(torch, launches=3):
     torch.cuda.synchronize()
     flops = sum(4 * Hq * D * sum(int(L) - int(ql) + r + 1 for r in range(int(ql)))
                 for ql, L in zip(c["q_lens"], c["kv_lens"]))
-    print(json.dumps({"attention_launches": launches, "attention_flops": flops}), flush=True)
+    nbytes = workloads.algorithmic_bytes_verify_attention(
+        c["kv_lens"], c["qo_indptr"][-1], Hq, Hkv, D, len(c["kv_lens"]), c["kv_indptr"][-1])
+    print(json.dumps({"copy_bytes": COPY_BYTES, "attention_launches": launches,
+                      "attention_flops": flops, "attention_algorithmic_bytes": nbytes}),
+          flush=True)
 
 
 def traffic_bytes():
@@ -357,8 +369,8 @@ def main():
                          "calls at the acceptance shape, for rocprofv3 --pmc FETCH_SIZE / "
                          "WRITE_SIZE passes")
     ap.add_argument("--pmc-probe-large", action="store_true",
-                    help="only 3 verify-attention launches at the large shape, for rocprofv3 "
-                         "--pmc passes (MFMA utilisation)")
+                    help="only a 256 MiB device copy (3x) and 3 verify-attention launches at "
+                         "the large shape, for rocprofv3 --pmc passes (MFMA, HBM traffic)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the verify "

@@ -164,6 +164,11 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
   constexpr int PSTRIDE = D + 4;          // partial row: O[D], m, l, 2 pad
   constexpr int NTHR = RT * KS * 64;
   constexpr int kNBuf = ring_depth(KS);
+  // Cache policy of the K / V copies.  One KV group (long contexts split over
+  // many workgroups) streams the pool once: non-temporal (measured 321 -> 301
+  // us at the large shape).  Several groups (decode / verify steps, a few
+  // short items): the default policy (non-temporal measured 9.8 -> 10.7 us).
+  constexpr int kDmaPolicy = KS == 1 ? 2 : 0;  // 2: the nt bit
   __shared__ __attribute__((aligned(16))) bf16 ring[KS][kNBuf][2][TILE];
   __shared__ int s_pages[kMaxItemPages];
 
@@ -324,7 +329,7 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
       // kernel stubs of this template
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
                                        static_cast<void*>(&ring[grp][slot][0][0] + d_lds[i]), 16,
-                                       0, 0);
+                                       0, kDmaPolicy);
     }
   };
 

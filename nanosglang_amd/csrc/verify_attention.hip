@@ -164,11 +164,12 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
   constexpr int PSTRIDE = D + 4;          // partial row: O[D], m, l, 2 pad
   constexpr int NTHR = RT * KS * 64;
   constexpr int kNBuf = ring_depth(KS);
-  // Cache policy of the K / V copies.  One KV group (long contexts split over
-  // many workgroups) streams the pool once: non-temporal (measured 321 -> 301
-  // us at the large shape).  Several groups (decode / verify steps, a few
-  // short items): the default policy (non-temporal measured 9.8 -> 10.7 us).
-  constexpr int kDmaPolicy = KS == 1 ? 2 : 0;  // 2: the nt bit
+  // Cache policy of the K / V copies: non-temporal (the pool is streamed
+  // once) for one or two KV groups -- measured 321 -> 301 us at the large
+  // shape (one group), 30.7 -> 29.4 us for head dim 128 verify steps (two
+  // groups) -- but the default policy for the four groups of head dim 64,
+  // where non-temporal measured 9.8 -> 10.7 us at the verify shape.
+  constexpr int kDmaPolicy = KS <= 2 ? 2 : 0;  // 2: the nt bit
   __shared__ __attribute__((aligned(16))) bf16 ring[KS][kNBuf][2][TILE];
   __shared__ int s_pages[kMaxItemPages];
 

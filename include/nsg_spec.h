@@ -97,7 +97,9 @@ int32_t nsg_attn_plan(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
  * NSG_ERR_WORKSPACE.  With max_kv_len > 0 (at most 1022 pages) no request's
  * KV range is split: the list holds one work item per query tile, no merge
  * items, and nsg_attn_run launches no merge pass; a longer request is an
- * argument error. */
+ * argument error.  With max_kv_len <= 0 (long contexts) the plan always takes
+ * the one-KV-group shape: KV ranges split over enough workgroups to fill the
+ * GPU, merged by the second launch. */
 int32_t nsg_attn_fixed_capacity(int32_t batch, int32_t max_q_len, int32_t num_qo_heads,
                                 int32_t num_kv_heads, int32_t num_cus, int32_t max_kv_len,
                                 int32_t* max_work, int32_t* max_merge);

@@ -619,9 +619,12 @@ long long target_items(int kv_groups, int num_cus, int num_kv_heads) {
   return std::max(1, (kv_groups > 1 ? num_cus : num_cus * kTargetWgPerCu) / num_kv_heads);
 }
 
-// Graph-captured plans are decode / verify steps: the latency regime, fixed.
-// With a KV-length bound (max_kv_len > 0) they never split a query tile's KV
-// range: one work item per tile and no merge launch at all.
+// Graph-captured plans keep one shape across re-plans.  With a KV-length
+// bound (max_kv_len > 0: decode / verify steps over short contexts) they take
+// the latency regime and never split a query tile's KV range: one work item
+// per tile and no merge launch at all.  Without one (long contexts) they take
+// the one-group regime, split to fill the GPU and merged by a second launch
+// (at the large shape 456 us per call in the latency regime, 301 us here).
 void fixed_capacity(int batch, int max_ql, int G, int num_kv_heads, int num_cus, int max_kv_len,
                     int* max_work, int* max_merge) {
   const int T = q_tile_tokens(G, max_ql);
@@ -631,7 +634,7 @@ void fixed_capacity(int batch, int max_ql, int G, int num_kv_heads, int num_cus,
     *max_merge = 0;
     return;
   }
-  *max_work = (int)target_items(2, num_cus, num_kv_heads) + groups;
+  *max_work = (int)target_items(1, num_cus, num_kv_heads) + groups;
   *max_merge = groups;
 }
 
@@ -706,12 +709,13 @@ int32_t plan_impl(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
     }
   }
   // KV groups: several per workgroup when even minimum-length items cannot
-  // fill the GPU (the latency regime), one otherwise; graph-captured plans
-  // always take the latency shape.  A split is at least kMinSplitSteps steps
-  // per group: its partial rows cost about as much traffic as one step of K
-  // and V.
+  // fill the GPU (the latency regime), one otherwise; a graph-captured plan
+  // takes the latency regime exactly when it has a KV-length bound (see
+  // fixed_capacity).  A split is at least kMinSplitSteps steps per group: its
+  // partial rows cost about as much traffic as one step of K and V.
   const long long t1 = target_items(1, num_cus, num_kv_heads);
-  const bool latency = fixed_work >= 0 || (total_it + t1 - 1) / t1 <= kMinSplitSteps;
+  const bool latency = fixed_work >= 0 ? fixed_kv_len > 0
+                                       : (total_it + t1 - 1) / t1 <= kMinSplitSteps;
   const int KS = latency ? kv_groups_max(head_dim) : 1;
   const long long tgt = target_items(KS, num_cus, num_kv_heads);
   long long chunk_it = std::max<long long>(

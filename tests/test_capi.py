@@ -116,22 +116,28 @@ def _plan_fixed(lib, q_lens, kv_lens, batch_cap, max_q, Hq=14, Hkv=2, D=64, P=16
 
 @pytest.mark.parametrize("q,B", [(1, 32), (5, 32), (5, 7), (9, 64)])
 def test_fixed_plan_pads_to_a_constant_grid(lib, q, B):
-    """The graph-mode plan: same grid and tile shape for every step; the real
-    items are exactly the dynamic planner's; the rest are empty."""
+    """The graph-mode plan without a KV bound: same grid and tile shape for
+    every step, one KV group; on long contexts, where the dynamic planner
+    takes that regime too, the real items are exactly the dynamic planner's;
+    the rest are empty."""
     rng = np.random.default_rng(q * 100 + B)
     shapes = set()
     for step in range(6):
-        # decode / verify contexts: the latency regime, where the dynamic
-        # planner takes the same shape the graph does
-        kv_lens = list(rng.integers(q, 180 * (step + 1), B))
+        kv_lens = list(rng.integers(2000, 2000 + 4000 * (step + 1), B))
         rc, pl, work, (mw, mm) = _plan_fixed(lib, [q] * B, kv_lens, B, q)
         assert rc == 0, lib.nsg_last_error()
         shapes.add((pl.num_work, pl.num_merge, pl.row_tiles, pl.q_tile_tokens,
                     pl.workspace_bytes))
         assert (pl.num_work, pl.num_merge) == (mw, mm)
+        assert pl.kv_groups == 1
+        qo = np.concatenate([[0], np.cumsum([q] * B)]).astype(np.int32)
+        kvp = np.concatenate([[0], np.cumsum([(L + 15) // 16 for L in kv_lens])]).astype(np.int32)
+        _check_cover(pl, work[:mw][work[:mw, 1] > 0], work[mw:][work[mw:, 3] > 1], [q] * B,
+                     kv_lens, qo, kvp)
         rc2, pd, wd, _, _ = _plan(lib, [q] * B, kv_lens)
         assert rc2 == 0
-        assert pd.kv_groups == pl.kv_groups > 1
+        if pd.kv_groups != 1:      # the dynamic planner chose the latency regime
+            continue
         n, m = pd.num_work, pd.num_merge
         assert np.array_equal(work[:n], wd[:n])                       # real work items
         assert (work[n:mw] == 0).all()                                # empty work items

@@ -212,8 +212,10 @@ def test_graph_mode_replays_after_replanning(q_len, B, max_kv):
             grid0 = grid
         assert grid == grid0                              # the captured launch stays valid
         got = out_s.float().cpu().numpy()
-        if max_kv == 0:   # same split plan as the eager wrapper: bit-identical
-            assert np.array_equal(got, eager.float().cpu().numpy())
+        if max_kv == 0:
+            assert wg.plan_info.kv_groups == 1            # long-context shape, split
+            if we.plan_info.kv_groups == 1:               # the eager plan too: bit-identical
+                assert np.array_equal(got, eager.float().cpu().numpy())
         else:             # never split (no merge launch): oracle tolerance only
             assert wg.plan_info.num_merge == 0 and wg.plan_info.max_splits == 1
         ref = _oracle(c)

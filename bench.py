@@ -310,7 +310,7 @@ def large_shape(args, torch):
                       rms_norm_eps=1e-5, rope_theta=5e5, tie_word_embeddings=False,
                       attention_bias=False)
     t0 = time.perf_counter()
-    model = CausalLM(cfg, device=dev, seed=0).quantize_fp8()
+    model = CausalLM(cfg, device=dev, seed=0).quantize_fp8(resident_dequant=True)
     torch.cuda.empty_cache()
     log(f"8B-shape FP8 model built in {time.perf_counter() - t0:.1f} s")
     blocks = int(sum((int(L) + n_out + k + 1 + P - 1) // P for L in ctx)) + B + 8

@@ -628,7 +628,8 @@ def _check_fp8(weight, w_scale, K):
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
            swiglu: bool = False, out: torch.Tensor | None = None,
-           force: bool = False, w_scale: torch.Tensor | None = None) -> torch.Tensor:
+           force: bool = False, w_scale: torch.Tensor | None = None,
+           w_dequant: torch.Tensor | None = None) -> torch.Tensor:
     """y = x @ weight.T (+ bias) for bf16 (M, K) rows (C ABI: nsg_linear).
 
     ``swiglu``: weight holds the fused [gate; up] rows (2I, K) and the
@@ -650,7 +651,10 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     # FP8 weights stay on the kernel whenever it fits: the library path would
     # first write the dequantised bf16 weights (three times the FP8 bytes)
     if not fits or not (force or fp8 or lib.nsg_linear_preferred(M, N, K)):
-        w = dequant_fp8(weight, w_scale) if fp8 else weight
+        if fp8:   # ``w_dequant``: a resident copy of exactly dequant_fp8(weight, w_scale)
+            w = w_dequant if w_dequant is not None else dequant_fp8(weight, w_scale)
+        else:
+            w = weight
         y = torch.nn.functional.linear(x, w, bias)
         if swiglu:
             return silu_mul(y, out)
@@ -682,7 +686,8 @@ def linear_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | N
                    positions: torch.Tensor, cos_table: torch.Tensor, sin_table: torch.Tensor,
                    slots: torch.Tensor | None, k_cache: torch.Tensor | None,
                    v_cache: torch.Tensor | None, q_out: torch.Tensor | None = None,
-                   force: bool = False, w_scale: torch.Tensor | None = None) -> torch.Tensor:
+                   force: bool = False, w_scale: torch.Tensor | None = None,
+                   w_dequant: torch.Tensor | None = None) -> torch.Tensor:
     """q/k/v projection + RoPE + KV-slot write (C ABI: nsg_linear_rope_kv, or
     nsg_linear_rope_kv_fp8 for float8_e4m3fn weights with per-row w_scale).
 
@@ -699,7 +704,7 @@ def linear_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | N
             and N == (num_qo_heads + 2 * num_kv_heads) * head_dim and x.stride(1) == 1
             and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0 and x.dtype == torch.bfloat16)
     if not fits or not (force or fp8 or lib.nsg_linear_preferred(M, N, K)):
-        qkv = linear(x, weight, bias, w_scale=w_scale)
+        qkv = linear(x, weight, bias, w_scale=w_scale, w_dequant=w_dequant)
         return rope_kv_write(qkv, num_qo_heads, num_kv_heads, head_dim, positions, cos_table,
                              sin_table, slots, k_cache, v_cache, q_out)
     if not fp8 and (weight.dtype != torch.bfloat16 or weight.stride(1) != 1

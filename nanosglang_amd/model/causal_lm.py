@@ -124,12 +124,19 @@ class CausalLM:
         self.lm_head = self.embed  # tie_word_embeddings
         self.rope_cos, self.rope_sin = rope_tables(c, self.device)
 
-    def quantize_fp8(self) -> "CausalLM":
+    def quantize_fp8(self, resident_dequant: bool = False) -> "CausalLM":
         """FP8 (E4M3) weights for every decoder layer's q/k/v, o_proj,
         gate/up and down_proj, one per-tensor scale each (FP8Linear.from_linear,
         nano_sglang/decode/quantization.py:54-75); embeddings, lm_head and
         norms stay bf16, as the reference's default skip list keeps them
-        (:220-221).  In place; returns self."""
+        (:220-221).  In place; returns self.
+
+        ``resident_dequant``: also keep the dequantised bf16 weights
+        (``dequant_fp8``, bit-identical to dequantising per call) for the
+        row counts that go to the library GEMM, so those calls read 2 bytes
+        per weight instead of dequantising first (3 more); the FP8 bytes
+        still serve the weight-streaming kernel.  Costs 2 bytes per weight of
+        HBM."""
         from .quantization import fp8_quantize_rows
         c = self.config
         Hq, Hkv, D, I = (c.num_attention_heads, c.num_key_value_heads, c.head_dim,
@@ -141,6 +148,10 @@ class CausalLM:
             L["o"], L["o_s"] = fp8_quantize_rows(L["o"], [L["o"].shape[0]])
             L["gate_up"], L["gate_up_s"] = fp8_quantize_rows(L["gate_up"], [I, I])
             L["down"], L["down_s"] = fp8_quantize_rows(L["down"], [L["down"].shape[0]])
+        if resident_dequant:
+            for L in self.layers:
+                for n in ("qkv", "o", "gate_up", "down"):
+                    L[n + "_d"] = kernels.dequant_fp8(L[n], L[n + "_s"])
         return self
 
     @property
@@ -172,13 +183,16 @@ class CausalLM:
                                 residual=None if x is None else residual)
             q = kernels.linear_rope_kv(h, L["qkv"], L["qkv_b"], Hq, Hkv, D, positions,
                                        self.rope_cos, self.rope_sin, write_indices,
-                                       k_pool[li], v_pool[li], w_scale=L.get("qkv_s"))
+                                       k_pool[li], v_pool[li], w_scale=L.get("qkv_s"),
+                                       w_dequant=L.get("qkv_d"))
             attn = attn_wrapper.run(q, (k_pool[li], v_pool[li]))
-            x = kernels.linear(attn.view(-1, Hq * D), L["o"], w_scale=L.get("o_s"))
+            x = kernels.linear(attn.view(-1, Hq * D), L["o"], w_scale=L.get("o_s"),
+                               w_dequant=L.get("o_d"))
             h = kernels.rmsnorm(x, L["ln2"], eps, residual=residual)   # causal_lm.py:147-154
             x = kernels.linear(kernels.linear(h, L["gate_up"], swiglu=True,
-                                              w_scale=L.get("gate_up_s")),
-                               L["down"], w_scale=L.get("down_s"))
+                                              w_scale=L.get("gate_up_s"),
+                                              w_dequant=L.get("gate_up_d")),
+                               L["down"], w_scale=L.get("down_s"), w_dequant=L.get("down_d"))
         h = kernels.rmsnorm(x, self.norm, eps, residual=residual)
         if logit_indices is not None:
             h = h[logit_indices]

@@ -332,3 +332,37 @@ def test_full_size_step_graph_equals_eager():
     assert outs[0][0] == outs[1][0]
     for step, (a, b) in enumerate(zip(outs[0][1], outs[1][1])):
         assert a == b, step
+
+
+def test_fp8_resident_dequant_gives_identical_logits():
+    """quantize_fp8(resident_dequant=True) keeps bf16 copies of the
+    dequantised weights for the row counts that go to the library GEMM (a
+    200-token prefill here): logits bit-identical to dequantising per call;
+    a 32-token call still runs the weight-streaming kernel on the FP8 bytes."""
+    from nanosglang_amd.engine.paged_kv_cache import BlockManager, PagedKVCache
+    from nanosglang_amd.kernels import BatchPrefillWithPagedKVCacheWrapper
+    print("case: fp8 resident dequantised weights", flush=True)
+    outs = []
+    for resident in (False, True):
+        _, gpu = _tiny_models(scale=1.0)
+        gpu.quantize_fp8(resident_dequant=resident)
+        assert ("qkv_d" in gpu.layers[0]) == resident
+        rng = np.random.default_rng(5)
+        res = []
+        for S in (200, 32):
+            prompt = rng.integers(0, 1000, S).tolist()
+            bm = BlockManager(64, 16, 4, 2, 64, torch.bfloat16, "cuda")
+            kv = PagedKVCache(bm)
+            t = kv.allocate_for_request(S)
+            w = BatchPrefillWithPagedKVCacheWrapper(
+                torch.empty(32 << 20, dtype=torch.uint8, device="cuda"))
+            w.plan(np.array([0, S], np.int32), np.array([0, t.num_blocks], np.int32),
+                   np.asarray(t.block_indices, np.int32), np.array([(S % 16) or 16], np.int32),
+                   4, 2, 64, 16, causal=True)
+            res.append(gpu.forward_packed(torch.tensor(prompt, device="cuda"),
+                                          torch.arange(S, device="cuda"),
+                                          (bm.k_cache, bm.v_cache), w,
+                                          torch.tensor(kv.slots(t, 0, S), device="cuda")))
+        outs.append(res)
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)

@@ -364,6 +364,9 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only a 256 MiB device copy (3x) and 10 verify-attention launches at "
                          "the verify shape, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
+    ap.add_argument("--tune-gemms", action="store_true",
+                    help="large-shape: let PyTorch's TunableOp pick the library GEMM algorithm "
+                         "per shape during the warm-up (results in a temporary file)")
     ap.add_argument("--pmc-probe-accept", action="store_true",
                     help="only a 256 MiB device copy (3x) and 3 stochastic + 3 greedy acceptance "
                          "calls at the acceptance shape, for rocprofv3 --pmc FETCH_SIZE / "
@@ -388,6 +391,13 @@ def main():
     if args.pmc_probe_large:
         pmc_probe_large(torch)
         return
+    if args.tune_gemms:
+        import tempfile
+        torch.cuda.tunable.enable(True)
+        torch.cuda.tunable.tuning_enable(True)
+        torch.cuda.tunable.set_filename(os.path.join(tempfile.mkdtemp(), "tunableop.csv"))
+        torch.cuda.tunable.set_max_tuning_duration(30)
+        torch.cuda.tunable.set_max_tuning_iterations(20)
     if args.workload == "large-shape":
         large_shape(args, torch)
         return

@@ -23,5 +23,5 @@ def test_help_lists_the_modes():
     r = _run("--help")
     assert r.returncode == 0
     for opt in ("--steps", "--warmup", "--workload", "--pmc-probe", "--pmc-probe-accept",
-                "--pmc-probe-large"):
+                "--pmc-probe-large", "--tune-gemms"):
         assert opt in r.stdout

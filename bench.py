@@ -18,11 +18,16 @@ U[100, 640], pages scattered over an 8000-block pool): algorithmic bytes per
 launch / mean launch time, timed with HIP events around replays of a HIP
 graph of 160 launches on the launch stream, with 16 pool copies (~1 GB)
 rotated so no launch is served from the 256 MB Infinity Cache.
-``kernels`` adds the acceptance kernels (batch 64, k 4, vocab 151936, T 0.8,
-three rotated buffer sets) and the large verify shape (Llama-3-8B heads,
-k 8, batch 64, KV U[2048, 8192]).  ``cpu_baseline`` times the oracle's fp32
-PyTorch CPU speculative loop (batch 1, the reference's own algorithm) on a
-bounded sample of the same workload.
+``kernels`` adds the acceptance calls -- ratio tests or the greedy rule,
+residual / bonus draw and rollback slots from a page table -- at batch 64,
+k 4, vocab 151936, T 0.8 and at batch 64, k 8, vocab 128256, T 1.0 (three
+rotated buffer sets each), and the large verify shape (Llama-3-8B heads, k 8,
+batch 64, KV U[2048, 8192]).  ``cpu_baseline`` is the CPU plumbing workload
+(batch 1, the seed-0 0.5B-shape target with a 2-layer draft, prompt of 64
+uniform ids, k 4, greedy, 32 tokens) on the oracle's fp32 PyTorch-CPU
+restatement of the reference's loop, every affinity core, median of 5 runs
+after a warm-up, prefill also timed alone; its ``kernels`` time the oracle's
+numpy restatements of both kernels on the same inputs as the GPU calls.
 
     python bench.py --workload large-shape [--steps K] [--warmup W]
 
@@ -116,30 +121,53 @@ def bench_verify_attention(torch, w, dev, reps=160, pools=16, shape=None):
     del ks, vs
     return {"us": t, "bytes": nbytes, "gbs": nbytes / t / 1e3, "flops": flops,
             "work_items": pi.num_work, "merge_items": pi.num_merge, "kv_groups": pi.kv_groups,
-            "row_tiles": pi.row_tiles, "pools_rotated": pools}
+            "row_tiles": pi.row_tiles, "pools_rotated": pools, "inputs": c}
 
 
-def bench_acceptance(torch, dev, greedy, sets=3, reps=60, **kw):
+def acceptance_inputs(**kw):
+    """Host inputs of one acceptance workload: logits, draft tokens and the
+    page table of the rollback slots (workloads.acceptance_batch /
+    acceptance_page_table, seed 0)."""
+    from nanosglang_amd import workloads
+    a = workloads.acceptance_batch(seed=0, **kw)
+    B, k1, _ = a["target"].shape
+    a["start"], a["kv_indptr"], a["kv_indices"] = workloads.acceptance_page_table(
+        batch=B, k=k1 - 1, seed=0)
+    return a
+
+
+def bench_acceptance(torch, dev, a, greedy, sets=3, reps=60):
+    """Mean time of one full acceptance call (ratio tests or greedy rule,
+    residual / bonus draw, emitted tokens, counts and rollback slots from the
+    page table) on `sets` rotated logit buffers, from replays of a HIP graph
+    of `reps` calls.  Fills a["uniforms"] (host copy of the Philox uniforms
+    the calls used)."""
     from nanosglang_amd import workloads
     from nanosglang_amd.kernels import philox_uniform, spec_accept
-    a = workloads.acceptance_batch(seed=0, **kw)
     B, k1, V = a["target"].shape
     k = k1 - 1
     tl = torch.from_numpy(a["target"]).to(dev).bfloat16()
     dl = torch.from_numpy(a["draft"]).to(dev).bfloat16()
     dt = torch.from_numpy(a["draft_tokens"]).to(dev)
     u = philox_uniform(123, 0, 0, B * k1, dev).view(B, k1)
+    a["uniforms"] = u.cpu().numpy()
+    pt = [torch.from_numpy(a[n]).to(dev) for n in ("kv_indptr", "kv_indices", "start")]
     bufs = [(tl, dl)] + [(tl.clone(), dl.clone()) for _ in range(sets - 1)]
     T = 0.0 if greedy else a["temperature"]
+    out = (torch.empty(B, dtype=torch.int32, device=dev),
+           torch.empty(B, k1, dtype=torch.int64, device=dev),
+           torch.empty(B, k, dtype=torch.int64, device=dev))
 
     def call(i):
         t_, d_ = bufs[i % sets]
-        spec_accept(t_, None if greedy else d_, dt, None if greedy else u, T)
+        spec_accept(t_, None if greedy else d_, dt, None if greedy else u, T, *pt,
+                    page_size=16, out=out)
 
     for i in range(2 * sets):
         call(i)
     t = graph_time_us(torch, call, reps)
     nbytes = workloads.algorithmic_bytes_acceptance(B, k, V, greedy)
+    del bufs
     return {"us": t, "bytes": nbytes, "gbs": nbytes / t / 1e3, "sets_rotated": sets}
 
 
@@ -187,9 +215,9 @@ LARGE_SHAPE = dict(batch=64, q_len=9, num_qo_heads=32, num_kv_heads=8, head_dim=
 
 def pmc_probe_accept(torch, sets=3):
     """A 256 MiB device copy (3x, the counter calibration), then one
-    stochastic and one greedy acceptance call at the acceptance shape on each
-    of `sets` rotated buffer sets, for rocprofv3 FETCH_SIZE / WRITE_SIZE
-    passes."""
+    stochastic and one greedy acceptance call (rollback slots included) at
+    the acceptance shape on each of `sets` rotated buffer sets, for rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes."""
     from nanosglang_amd import workloads
     from nanosglang_amd.kernels import philox_uniform, spec_accept
     dev = torch.device("cuda", 0)
@@ -199,18 +227,19 @@ def pmc_probe_accept(torch, sets=3):
         dst.copy_(src)
     torch.cuda.synchronize()
     del src, dst
-    a = workloads.acceptance_batch(seed=0)
+    a = acceptance_inputs()
     B, k1, V = a["target"].shape
     tl = torch.from_numpy(a["target"]).to(dev).bfloat16()
     dl = torch.from_numpy(a["draft"]).to(dev).bfloat16()
     dt = torch.from_numpy(a["draft_tokens"]).to(dev)
     u = philox_uniform(123, 0, 0, B * k1, dev).view(B, k1)
+    pt = [torch.from_numpy(a[n]).to(dev) for n in ("kv_indptr", "kv_indices", "start")]
     bufs = [(tl, dl)] + [(tl.clone(), dl.clone()) for _ in range(sets - 1)]
     torch.cuda.synchronize()
     for t_, d_ in bufs:
-        spec_accept(t_, d_, dt, u, a["temperature"])
+        spec_accept(t_, d_, dt, u, a["temperature"], *pt, page_size=16)
     for t_, d_ in bufs:
-        spec_accept(t_, None, dt, None, 0.0)
+        spec_accept(t_, None, dt, None, 0.0, *pt, page_size=16)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes": COPY_BYTES, "calls": sets,
                       "stochastic_algorithmic_bytes":
@@ -269,29 +298,118 @@ def traffic_bytes():
         return json.load(f).get("traffic_bytes_per_launch")
 
 
-def cpu_baseline(prompts, outs, n_tokens=48):
-    """The oracle's fp32 PyTorch CPU speculative loop on request 0 of the
-    workload (prompt + n_tokens outputs), batch 1, k 4, 4-layer draft."""
+def _cpu_model_name() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(runs=5, n_tokens=32, prompt_len=64):
+    """The CPU plumbing workload on the oracle's fp32 PyTorch-CPU restatement
+    of the reference's speculative loop (speculative.py:51-184): the seed-0
+    random-init 0.5B-shape target, a draft of its first 2 layers plus the
+    shared embedding / norm / lm_head, batch 1, a prompt of 64 uniform-random
+    ids, k = 4, greedy, 32 output tokens.  Every affinity core; 1 warm-up run,
+    then the median of `runs`; the prompt's prefill (target + draft forward
+    over the prompt) is also timed on its own."""
     import torch
     sys.path.insert(0, ROOT)
-    from oracle.model import CPUCausalLM, CPUSpeculativeDecoder, ModelConfig, init_weights
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    from oracle.model import (CPUCausalLM, CPUSpeculativeDecoder, ModelConfig, causal_mask,
+                              init_weights)
+    cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     cfg = ModelConfig()
     w = init_weights(cfg, seed=0)
-    target = CPUCausalLM(cfg, w, max_pos=1024)
-    draft = CPUCausalLM(cfg, w, num_layers=4, max_pos=1024)
+    target = CPUCausalLM(cfg, w, max_pos=256)
+    draft = CPUCausalLM(cfg, w, num_layers=2, max_pos=256)
+    prompt = np.random.default_rng(0).integers(0, cfg.vocab_size, prompt_len).tolist()
     spec = CPUSpeculativeDecoder(draft, target, 4, temperature=0.0)
-    p = prompts[0]
-    spec.generate(p[:16], 2)                   # warm-up
-    t0 = time.perf_counter()
-    out = spec.generate(p, n_tokens)
-    dt = time.perf_counter() - t0
-    return {"value": len(out) / dt, "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"request 0 of the workload (prompt {len(p)} tokens) -> {n_tokens} output "
-                      f"tokens, batch 1, fp32, k=4, 4-layer draft, greedy, prefill included; "
-                      f"{dt:.1f} s", "seconds": dt,
-            "torch": torch.__version__}
+    spec.generate(prompt, n_tokens)                         # warm-up
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        out = spec.generate(prompt, n_tokens)
+        times.append(time.perf_counter() - t0)
+    assert len(out) == n_tokens
+    ids, pos, mask = torch.tensor([prompt]), torch.arange(prompt_len)[None], \
+        causal_mask(prompt_len, prompt_len)
+    pre = []
+    for _ in range(3):
+        tc, dc = target.new_cache(1, prompt_len), draft.new_cache(1, prompt_len)
+        t0 = time.perf_counter()
+        target.forward(ids, pos, tc, 0, mask)
+        draft.forward(ids, pos, dc, 0, mask)
+        pre.append(time.perf_counter() - t0)
+    med, prefill = float(np.median(times)), float(np.median(pre))
+    return {"value": round(n_tokens / med, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"the whole CPU plumbing workload per run: batch 1, prompt {prompt_len} "
+                      f"uniform ids, {n_tokens} output tokens (prefill included), fp32, "
+                      f"0.5B-shape target / 2-layer draft, k=4, greedy; median of {runs} runs "
+                      f"after 1 warm-up",
+            "median_s": round(med, 3), "runs_s": [round(t, 3) for t in times],
+            "prefill_s": round(prefill, 4),
+            "decode_tok_per_s": round((n_tokens - 1) / max(1e-9, med - prefill), 3),
+            "acceptance_rate": round(spec.stats["accepted"] / max(1, spec.stats["proposed"]), 4),
+            "cpu_model": _cpu_model_name(), "torch": torch.__version__}
+
+
+def cpu_restatements(c2, c3, c5, big, runs=3, big_requests=8):
+    """The oracle's numpy restatements of the two kernels timed on the same
+    inputs as the GPU calls (median of `runs`): verify attention at the
+    verify shape (all 32 requests) and at the large shape (the first
+    `big_requests` of 64, one run), acceptance at the
+    acceptance shape and the large shape (stochastic and greedy, rollback
+    slots included).  float64 numpy on the host: one thread for the
+    elementwise work, the BLAS threads numpy was given for the einsums."""
+    sys.path.insert(0, ROOT)
+    from nanosglang_amd import workloads
+    from oracle.acceptance import spec_accept as oracle_accept
+    from oracle.verify_attention import verify_attention
+
+    def med(fn, runs=runs):
+        ts = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
+    def attn_entry(c, n_req, n_runs):
+        kvl = np.asarray(c["kv_lens"][:n_req])
+        qo = c["qo_indptr"][:n_req + 1]
+        kvp = c["kv_indptr"][:n_req + 1]
+        t = med(lambda: verify_attention(c["q"][:qo[-1]], c["k"], c["v"], qo, kvp,
+                                         c["kv_indices"], c["kv_last_page_len"][:n_req],
+                                         c["sm_scale"]), n_runs)
+        nb = workloads.algorithmic_bytes_verify_attention(
+            kvl, qo[-1], c["q"].shape[1], c["k"].shape[2], c["k"].shape[3], n_req, kvp[-1])
+        return {"ms": round(t * 1e3, 2), "algorithmic_bytes": int(nb),
+                "gbs": round(nb / t / 1e9, 3), "requests": int(n_req)}
+
+    def acc_entry(a, greedy):
+        B, k1, V = a["target"].shape
+        t = med(lambda: oracle_accept(a["target"], None if greedy else a["draft"],
+                                      a["draft_tokens"], None if greedy else a["uniforms"],
+                                      0.0 if greedy else a["temperature"], a["kv_indptr"],
+                                      a["kv_indices"], a["start"], 16))
+        nb = workloads.algorithmic_bytes_acceptance(B, k1 - 1, V, greedy)
+        return {"ms": round(t * 1e3, 2), "algorithmic_bytes": int(nb),
+                "gbs": round(nb / t / 1e9, 3)}
+
+    out = {"verify_attention_verify_shape": attn_entry(c2, len(c2["kv_lens"]), runs)}
+    if big is not None:   # about 5 s per run: one run
+        out["verify_attention_large_shape_sample"] = attn_entry(big, big_requests, 1)
+    out["acceptance_stochastic_b64_k4_v151936"] = acc_entry(c3, False)
+    out["acceptance_greedy_b64_k4_v151936"] = acc_entry(c3, True)
+    if c5 is not None:
+        out["acceptance_stochastic_b64_k8_v128256"] = acc_entry(c5, False)
+        out["acceptance_greedy_b64_k8_v128256"] = acc_entry(c5, True)
+    return out
 
 
 def large_shape(args, torch):
@@ -348,6 +466,7 @@ def large_shape(args, torch):
                    "batch": B, "k": k, "page_size": P, "num_blocks": blocks},
         "acceptance_rate": round(float(np.mean([s["acceptance_rate"] for s in stats])), 4),
         "tokens_per_step": round(float(np.mean([s["tokens_per_step"] for s in stats])), 3),
+        "tune_gemms": bool(args.tune_gemms),
     }
     print(json.dumps(result), flush=True)
 
@@ -391,15 +510,22 @@ def main():
     if args.pmc_probe_large:
         pmc_probe_large(torch)
         return
-    if args.tune_gemms:
-        import tempfile
-        torch.cuda.tunable.enable(True)
-        torch.cuda.tunable.tuning_enable(True)
-        torch.cuda.tunable.set_filename(os.path.join(tempfile.mkdtemp(), "tunableop.csv"))
-        torch.cuda.tunable.set_max_tuning_duration(30)
-        torch.cuda.tunable.set_max_tuning_iterations(20)
+    if args.tune_gemms and args.workload != "large-shape":
+        print("--tune-gemms applies to --workload large-shape only (the default line runs "
+              "no tuned library GEMM)", file=sys.stderr)
+        sys.exit(2)
     if args.workload == "large-shape":
-        large_shape(args, torch)
+        if not args.tune_gemms:
+            large_shape(args, torch)
+            return
+        import tempfile
+        with tempfile.TemporaryDirectory() as tmp:
+            torch.cuda.tunable.enable(True)
+            torch.cuda.tunable.tuning_enable(True)
+            torch.cuda.tunable.set_filename(os.path.join(tmp, "tunableop.csv"))
+            torch.cuda.tunable.set_max_tuning_duration(30)
+            torch.cuda.tunable.set_max_tuning_iterations(20)
+            large_shape(args, torch)
         return
     from nanosglang_amd.engine.spec_engine import SpecEngine
     from nanosglang_amd.model.causal_lm import CausalLM, ModelConfig
@@ -450,8 +576,10 @@ def main():
     del engine, model
     torch.cuda.empty_cache()
 
+    inputs = {}
     if not args.skip_kernels:
         va = bench_verify_attention(torch, None, dev)
+        inputs["c2"] = va.pop("inputs")
         log(f"verify attention (verify shape): {va}")
         launches = ("verify_attn_kernel" + (" + verify_merge_kernel" if va["merge_items"] else ""))
         result["roofline"] = {
@@ -461,12 +589,21 @@ def main():
                       f"{va['kv_groups']} KV groups of {va['row_tiles']} waves per workgroup), "
                       f"batch 32, 5 query tokens, 14/2 heads, D 64",
             "us_per_launch": round(va["us"], 2), "algorithmic_bytes": va["bytes"]}
-        acc_s = bench_acceptance(torch, dev, greedy=False)
-        log(f"acceptance stochastic: {acc_s}")
-        acc_g = bench_acceptance(torch, dev, greedy=True)
-        log(f"acceptance greedy: {acc_g}")
+        entries = {"verify_attention_verify_shape": va}
+        for name, kw in (("b64_k4_v151936", {}),
+                         ("b64_k8_v128256", dict(k=8, vocab=128256, temperature=1.0))):
+            a = acceptance_inputs(**kw)
+            for greedy in (False, True):
+                mode = "greedy" if greedy else "stochastic"
+                d = bench_acceptance(torch, dev, a, greedy)
+                log(f"acceptance {mode} {name}: {d}")
+                entries[f"acceptance_{mode}_{name}"] = d
+            inputs[name] = a
+            torch.cuda.empty_cache()
         big = bench_verify_attention(torch, None, dev, reps=20, pools=1, shape=LARGE_SHAPE)
+        inputs["large"] = big.pop("inputs")
         log(f"verify attention (large shape): {big}")
+        entries["verify_attention_large_shape"] = big
 
         def k_entry(d):
             e = {"us": round(d["us"], 2), "algorithmic_bytes": d["bytes"],
@@ -475,18 +612,17 @@ def main():
                 e["tflops"] = round(d["flops"] / d["us"] / 1e6, 2)
             return e
 
-        result["kernels"] = {
-            "verify_attention_verify_shape": k_entry(va),
-            "acceptance_stochastic_b64_k4_v151936": k_entry(acc_s),
-            "acceptance_greedy_b64_k4_v151936": k_entry(acc_g),
-            "verify_attention_large_shape": k_entry(big),
-        }
+        result["kernels"] = {n: k_entry(d) for n, d in entries.items()}
 
     if not args.skip_cpu:
-        cb = cpu_baseline(prompts, outs)
+        cb = cpu_baseline()
         log(f"cpu baseline: {cb}")
-        result["cpu_baseline"] = {k: cb[k] for k in ("value", "unit", "cores", "kind", "sample")}
-        result["cpu_baseline"]["value"] = round(cb["value"], 3)
+        result["cpu_baseline"] = cb
+        if inputs:
+            rs = cpu_restatements(inputs["c2"], inputs["b64_k4_v151936"],
+                                  inputs["b64_k8_v128256"], inputs["large"])
+            log(f"cpu restatements: {rs}")
+            result["cpu_baseline"]["kernels"] = rs
     print(json.dumps(result), flush=True)
 
 

@@ -44,6 +44,14 @@ inline int32_t launch_status(const char* what) {
   return NSG_OK;
 }
 
+// ---- workspaces ----
+// The acceptance and sampling entry points may be handed one workspace (one
+// per stream, by their callers).  Its first kWorkspaceHeaderBytes hold the
+// acceptance kernels' error-flag word and their cross-workgroup counters;
+// the sampler's layout starts after them, so a sampling call never touches
+// what an acceptance call reads back or relies on being zero.
+constexpr int64_t kWorkspaceHeaderBytes = 256;
+
 // ---- device types ----
 typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));

@@ -663,7 +663,7 @@ SLayout slayout(int rows, int V) {
   L.cs = ((V + L.nch - 1) / L.nch + 7) / 8 * 8;
   L.nch = (V + L.cs - 1) / L.cs;
   auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
-  L.cmax_off = 0;
+  L.cmax_off = kWorkspaceHeaderBytes;  // the acceptance header stays untouched
   L.hcnt_off = L.cmax_off + al((int64_t)rows * kSMaxChunks * 8);
   L.hmass_off = L.hcnt_off + al((int64_t)rows * kMaxStages * kBins * 4);
   L.st_off = L.hmass_off + al((int64_t)rows * kMaxStages * kBins * 8);

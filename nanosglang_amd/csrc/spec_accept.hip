@@ -48,7 +48,6 @@ constexpr int kMaxK = 32;
 constexpr int kMaxBatch = 1 << 14;
 constexpr int kMaxChunks = 64;
 constexpr int kTargetWgs = 4096;
-constexpr int64_t kFlagBytes = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kSlack = 16.f;  // lazy-rescale headroom of the running sums (log2 units)
 
@@ -1016,7 +1015,7 @@ Layout layout(int B, int k, int V, bool greedy) {
   L.nch2 = (V + L.cs2 - 1) / L.cs2;
   auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
   const int rows_max = B * (2 * k + 1);  // one workspace serves both modes
-  L.stats_off = kFlagBytes;
+  L.stats_off = kWorkspaceHeaderBytes;
   L.dec_off = L.stats_off + al((int64_t)rows_max * kMaxChunks * 8);
   L.psum_off = L.dec_off + al((int64_t)B * 8 * 4);
   L.rsum_off = L.psum_off + al((int64_t)B * kMaxChunks * 4);

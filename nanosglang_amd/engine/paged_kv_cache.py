@@ -127,9 +127,9 @@ class BlockManager:
         return (self.k_cache.nelement() + self.v_cache.nelement()) * self.k_cache.element_size()
 
     def __repr__(self) -> str:
-        mb = self.memory_bytes / 1024 / 1024
-        return (f"BlockManager(blocks={self.num_blocks}, block_size={self.block_size}, "
-                f"free={self.num_free_blocks}, memory={mb:.1f}MB)")
+        used = self.num_blocks - self.num_free_blocks
+        return (f"<BlockManager {used}/{self.num_blocks} pages in use, {self.block_size} "
+                f"tokens per page, {self.memory_bytes / 2**30:.2f} GiB of K/V>")
 
 
 class PagedKVCache:

@@ -215,6 +215,11 @@ class SpecEngine:
         # workgroups instead, with the merge launch captured as well.
         self.max_kv_len = 0 if kv_split else min(c.max_position_embeddings, 1022 * block_size)
         self._noise = False
+        # trace: a list to receive, after every speculative step, the step's
+        # verify logits and acceptance inputs / outputs (numpy / CPU tensors),
+        # so that a caller can check the acceptance on exactly the logits the
+        # step produced; None (default) records nothing.
+        self.trace: list | None = None
 
     # ---- helpers ----
     def _uniforms(self, stream: int, n: int) -> torch.Tensor:
@@ -352,6 +357,7 @@ class SpecEngine:
         g.vids[:, 0].copy_(A["tok0"])
         g.vids[:, 1:].copy_(g.drafts)
         tl = m.forward_packed(g.vids.view(-1), A["vpos"], pool, g.attn[k], A["vslot"])
+        g.tl = tl        # allocated from the graph's pool: every replay rewrites it
         bonus = self._bonus(tl.view(bs, k + 1, -1), g.u, workspace=self._accept_ws,
                             out=g.bonus)
         kernels.spec_accept(tl.view(bs, k + 1, -1), g.dlog, g.drafts, g.u, self.temperature,
@@ -411,7 +417,26 @@ class SpecEngine:
         g.n_h.copy_(g.n_out, non_blocking=True)
         g.em_h.copy_(g.emitted, non_blocking=True)
         torch.cuda.current_stream(self.device).synchronize()
+        if self.trace is not None:
+            k, (si, sx, _) = self.k, g.strides
+            kvp = g.arena.h["kvp"][k * si:k * si + B + 1].copy()
+            self._record(g.tl.view(g.bs, k + 1, -1)[:B], g.drafts[:B],
+                         g.arena.h["start"][:B], kvp,
+                         g.arena.h["idx"][k * sx:k * sx + int(kvp[-1])],
+                         g.n_out[:B], g.emitted[:B], g.rollback[:B])
         return g.n_h.numpy()[:B], g.em_h.numpy()[:B]
+
+    def _record(self, tl, drafts, start, kv_indptr, kv_indices, n_out, emitted, rollback):
+        """Append one step's verify logits, acceptance inputs and outputs to
+        ``self.trace`` (host copies)."""
+        self.trace.append({
+            "verify_logits": tl.detach().cpu(), "drafts": drafts.cpu().numpy(),
+            "start": np.asarray(start, np.int64).copy(),
+            "kv_indptr": np.asarray(kv_indptr, np.int32).copy(),
+            "kv_indices": np.asarray(kv_indices, np.int32).copy(),
+            "num_emitted": n_out.cpu().numpy(), "emitted": emitted.cpu().numpy(),
+            "rollback": rollback.cpu().numpy(), "page_size": self.P,
+            "temperature": self.temperature})
 
     # ---- eager mode ----
     def _step_eager(self, active: list):
@@ -443,10 +468,13 @@ class SpecEngine:
         sl = self._to_dev(self._slots(active, starts, [k + 1] * B))
         tl = self.model.forward_packed(vids.view(-1), vpos, self._pool(), self.attn, sl)
         u = None if self.greedy else self._uniforms(0, B * (k + 1)).view(B, k + 1)
-        n_out, emitted, _ = kernels.spec_accept(
+        n_out, emitted, rollback = kernels.spec_accept(
             tl.view(B, k + 1, -1), dlog, drafts, u, self.temperature,
             self._to_dev(kvp), self._to_dev(idx), self._to_dev(start_pos, torch.int32),
             page_size=self.P, bonus_tokens=self._bonus(tl.view(B, k + 1, -1), u))
+        if self.trace is not None:
+            self._record(tl.view(B, k + 1, -1), drafts, start_pos, kvp, idx, n_out, emitted,
+                         rollback)
         return n_out.cpu().numpy(), emitted.cpu().numpy()
 
     # ---- main entry ----

@@ -626,6 +626,15 @@ def _check_fp8(weight, w_scale, K):
     return True
 
 
+def _check_dequant(w_dequant: torch.Tensor, weight: torch.Tensor) -> None:
+    """A resident dequantised copy must be the bf16 twin of ``weight``: same
+    shape, same device (a stale copy of another tensor would go unnoticed)."""
+    if (w_dequant.dtype != torch.bfloat16 or tuple(w_dequant.shape) != tuple(weight.shape)
+            or w_dequant.device != weight.device):
+        raise ValueError(f"w_dequant must be bfloat16 {tuple(weight.shape)} on {weight.device}, "
+                         f"got {w_dequant.dtype} {tuple(w_dequant.shape)} on {w_dequant.device}")
+
+
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
            swiglu: bool = False, out: torch.Tensor | None = None,
            force: bool = False, w_scale: torch.Tensor | None = None,
@@ -652,7 +661,11 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     # first write the dequantised bf16 weights (three times the FP8 bytes)
     if not fits or not (force or fp8 or lib.nsg_linear_preferred(M, N, K)):
         if fp8:   # ``w_dequant``: a resident copy of exactly dequant_fp8(weight, w_scale)
-            w = w_dequant if w_dequant is not None else dequant_fp8(weight, w_scale)
+            if w_dequant is not None:
+                _check_dequant(w_dequant, weight)
+                w = w_dequant
+            else:
+                w = dequant_fp8(weight, w_scale)
         else:
             w = weight
         y = torch.nn.functional.linear(x, w, bias)

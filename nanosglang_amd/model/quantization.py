@@ -102,13 +102,13 @@ def quantize_model(model: nn.Module, method: str = "fp8", group_size: int = 128,
         raise NotImplementedError(f"quantization method {method!r}: only 'fp8' is built")
     if skip_modules is None:
         skip_modules = ["embed_tokens", "lm_head", "norm"]
-    for name, module in model.named_modules():
-        if any(skip in name for skip in skip_modules):
-            continue
-        for child_name, child in module.named_children():
-            if isinstance(child, nn.Linear):
-                full = f"{name}.{child_name}" if name else child_name
-                if any(skip in full for skip in skip_modules):
-                    continue
-                setattr(module, child_name, FP8Linear.from_linear(child))
+    # A linear is skipped when any skip substring occurs in its dotted path
+    # (a parent's name is a prefix of that path, so one test covers both
+    # levels the reference checks).  Targets are collected first, then swapped.
+    targets = [path for path, mod in model.named_modules()
+               if isinstance(mod, nn.Linear) and not any(s in path for s in skip_modules)]
+    for path in targets:
+        parent_path, _, attr = path.rpartition(".")
+        parent = model.get_submodule(parent_path) if parent_path else model
+        setattr(parent, attr, FP8Linear.from_linear(getattr(parent, attr)))
     return model

@@ -22,11 +22,15 @@ import numpy as np
 
 
 def _bf16_round(x: np.ndarray) -> np.ndarray:
-    """Round float32 to the nearest bf16 (ties to even), returned as float32."""
-    x = np.ascontiguousarray(x, dtype=np.float32)
-    u = x.view(np.uint32).astype(np.uint64)
-    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16
-    return u.astype(np.uint32).view(np.float32)
+    """Round finite float32 to the nearest bf16 (ties to even), returned as
+    float32.  In uint32 arithmetic: a finite float's bits are at most
+    0xFF7FFFFF, so adding at most 0x8000 cannot wrap."""
+    u = np.array(x, dtype=np.float32, copy=True).view(np.uint32)
+    r = (u >> 16) & np.uint32(1)
+    r += np.uint32(0x7FFF)
+    u += r
+    u &= np.uint32(0xFFFF0000)
+    return u.view(np.float32)
 
 
 def verify_attention_batch(batch=32, q_len=5, num_qo_heads=14, num_kv_heads=2, head_dim=64,
@@ -76,6 +80,25 @@ def acceptance_batch(batch=64, k=4, vocab=151936, temperature=0.8, seed=0):
             c = np.cumsum(p)
             tokens[b, i] = min(int(np.searchsorted(c, u[b, i] * c[-1], side="right")), vocab - 1)
     return dict(target=target, draft=draft, draft_tokens=tokens, temperature=temperature)
+
+
+def acceptance_page_table(batch=64, k=4, page_size=16, num_pages=8000, min_len=100,
+                          max_len=640, seed=0):
+    """Page table of an acceptance call: request b's verify window sits at
+    positions start_b .. start_b + k (start_b = L_b - k - 1 with L_b uniform in
+    [min_len, max_len], the verify-attention workload's KV lengths), on pages
+    drawn as a seeded permutation of the pool.  Returns (start_pos int32 [B],
+    kv_indptr int32 [B+1], kv_indices int32) for the rollback slots."""
+    rng = np.random.default_rng(seed)
+    L = rng.integers(max(min_len, k + 1), max_len + 1, size=batch)
+    start = (L - k - 1).astype(np.int32)
+    need = (L + page_size - 1) // page_size
+    if need.sum() > num_pages:
+        raise ValueError(f"{need.sum()} pages needed, pool has {num_pages}")
+    indptr = np.zeros(batch + 1, np.int32)
+    indptr[1:] = np.cumsum(need)
+    indices = rng.permutation(num_pages).astype(np.int32)[:indptr[-1]].copy()
+    return start, indptr, indices
 
 
 def algorithmic_bytes_verify_attention(kv_lens, q_total, num_qo_heads, num_kv_heads, head_dim,

@@ -81,15 +81,3 @@ def words_to_uniform(w: np.ndarray) -> np.ndarray:
 def philox_uniforms(seed: int, stream: int, offset: int, n: int) -> np.ndarray:
     """float32 uniforms ``offset .. offset+n-1`` of ``stream`` under ``seed``."""
     return words_to_uniform(philox_words(seed, stream, offset, n))
-
-
-def philox_normals(seed: int, stream: int, offset: int, n: int) -> np.ndarray:
-    """Standard normals by Box-Muller on consecutive uniform pairs (float64).
-
-    Used only by the synthetic-input builders: u1 = (w0>>8+1)*2^-24 in (0,1],
-    u2 = (w1>>8)*2^-24; z = sqrt(-2 ln u1) * cos(2 pi u2).
-    """
-    w = philox_words(seed, stream, 2 * offset, 2 * n).reshape(n, 2)
-    u1 = ((w[:, 0] >> np.uint32(8)).astype(np.float64) + 1.0) * 2.0 ** -24
-    u2 = (w[:, 1] >> np.uint32(8)).astype(np.float64) * 2.0 ** -24
-    return np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)

@@ -1,6 +1,6 @@
 // Prints Philox4x32-10 words from rocRAND's host-callable engine, used to pin
 // the oracle's (seed, stream, offset) -> word mapping against an independent
-// implementation.  Build: see make_golden.sh.
+// implementation.  Build: see make_philox_golden.sh.
 #include <cstdio>
 #include <cstdlib>
 #include <rocrand/rocrand_philox4x32_10.h>

@@ -296,3 +296,39 @@ def test_stochastic_large_shape_full_size_properties():
     tl[:, :k] = dl                                        # identical distributions
     n, _, _ = spec_accept(tl, dl, drafts, u, T)
     assert (n.cpu().numpy() == k + 1).all()
+
+
+def test_stochastic_large_shape_full_size_oracle():
+    """The large shape's stochastic acceptance at full size (64 requests,
+    k = 8, vocab 128,256, T = 1, bf16 logits, rollback slots from a page
+    table) against the float64 oracle, to the bar of the acceptance shape:
+    bit-exact except requests whose decision margin is below 1e-5."""
+    print("case: stochastic acceptance, large shape, oracle", flush=True)
+    a = workloads.acceptance_batch(batch=64, k=8, vocab=128256, temperature=1.0, seed=24)
+    u = _uniforms(64, 8, 24)
+    n, em, rb, ref = _run(a, 1.0, u, seed=24)
+    print(f"  mean emitted {n.mean():.2f}, resample rows {(n < 9).sum()}", flush=True)
+    _assert_stochastic(n, em, rb, ref)
+
+
+def test_sample_then_accept_on_one_workspace_keeps_flags_clear():
+    """A filtered draw (nsg_sample, top-k) and an acceptance call share one
+    workspace, as the engine's captured step does: the sampler leaves the
+    acceptance header alone, so the acceptance flags read back as zero."""
+    from nanosglang_amd.kernels import AcceptWorkspace, sample, spec_accept
+    B, k, V = 8, 4, 20000
+    a = workloads.acceptance_batch(batch=B, k=k, vocab=V, seed=25)
+    from nanosglang_amd import _native
+    lib = _native.load()
+    ws = AcceptWorkspace("cuda")
+    ws.get(max(lib.nsg_sample_workspace_bytes(B, V), lib.nsg_spec_accept_workspace_bytes(B, k, V)))
+    t, d = _dev(a["target"], torch.bfloat16), _dev(a["draft"], torch.bfloat16)
+    u = _dev(_uniforms(B, k, 25), torch.float32)
+    dt = _dev(a["draft_tokens"], torch.int64)
+    for _ in range(2):
+        sample(t[:, 0], 0.8, top_k=50, top_p=0.9, uniforms=u[:, 0].contiguous(), workspace=ws)
+        spec_accept(t, d, dt, u, 0.8, workspace=ws)
+        assert ws.check_flags() == 0
+        sample(t[:, 0], 0.8, top_k=50, uniforms=u[:, 0].contiguous(), workspace=ws)
+        spec_accept(t, None, dt, None, 0.0, workspace=ws)
+        assert ws.check_flags() == 0

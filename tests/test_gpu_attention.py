@@ -229,9 +229,10 @@ def test_graph_mode_replays_after_replanning(q_len, B, max_kv):
 def test_large_shape_full_size():
     """The large shape itself: 64 requests of 9 query tokens, 32 / 8 heads,
     head dim 128, KV lengths U[2048, 8192] on 16-token pages scattered over
-    the pool.  Two requests (the first and the longest) against the oracle;
-    the whole output unchanged, bit for bit, when the pool's pages move and
-    the page table follows them."""
+    the pool.  Eight requests spanning the length range (the shortest, the
+    longest and six evenly spaced ranks between) against the oracle; the
+    whole output unchanged, bit for bit, when the pool's pages move and the
+    page table follows them."""
     from nanosglang_amd.kernels import BatchPrefillWithPagedKVCacheWrapper
     B, ql, Hq, Hkv, D, P = 64, 9, 32, 8, 128, 16
     rng = np.random.default_rng(21)
@@ -265,7 +266,9 @@ def test_large_shape_full_size():
     out2, _ = run(k2, v2, moved.cpu().numpy()[idx].astype(np.int32))
     assert torch.equal(out, out2)
     del k2, v2
-    for b in (0, int(np.argmax(L))):
+    order = np.argsort(L, kind="stable")
+    picks = [int(order[i]) for i in np.linspace(0, B - 1, 8).round().astype(int)]
+    for b in picks:
         pages = torch.from_numpy(idx[kvp[b]:kvp[b + 1]].astype(np.int64)).cuda()
         ref = verify_attention(q[b * ql:(b + 1) * ql].float().cpu().numpy(),
                                k[pages].float().cpu().numpy(), v[pages].float().cpu().numpy(),

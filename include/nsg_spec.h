@@ -8,7 +8,8 @@
  *   - returns 0 on success or an NSG_ERR_* code, with a message available from
  *     nsg_last_error() (thread-local).  No C++ exception crosses the ABI.
  * All tensors are borrowed; the library frees nothing it did not allocate and
- * keeps no global mutable state besides the per-thread error string.
+ * keeps no global mutable state besides the per-thread error string and the
+ * per-GPU static workspace of nsg_spec_accept_noalloc.
  *
  * Layouts follow the reference (xiehuanyi/nanoSGLang):
  *   KV pool per layer: [num_pages, page_size, num_kv_heads, head_dim] bf16
@@ -42,7 +43,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 11
+#define NSG_ABI_VERSION 12
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -225,6 +226,30 @@ int32_t nsg_spec_accept(const void* target_logits, int64_t target_req_stride,
 /* Copies the acceptance workspace's error flags (bits as above) to *flags_h
  * after synchronising the stream, and clears them. */
 int32_t nsg_spec_accept_check_flags(void* workspace, int32_t* flags_h, nsg_stream_t stream);
+
+/* nsg_spec_accept without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It has no counterpart in the reference.
+ * The workspace is a static device array of the library, one per GPU, of
+ * nsg_spec_accept_noalloc_max_bytes() bytes (8 MiB), held until the process
+ * ends; a call whose nsg_spec_accept_workspace_bytes(batch, k, vocab)
+ * exceeds it returns NSG_ERR_WORKSPACE and launches nothing.  The call makes
+ * no allocation of any kind.  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (different streams or threads) race.
+ * flags: a device int32 that receives the error bits nsg_spec_accept keeps in
+ * its workspace (the caller zeroes it; NULL: not reported).  Every other
+ * argument and all outputs are those of nsg_spec_accept, bit for bit. */
+int64_t nsg_spec_accept_noalloc_max_bytes(void);
+int32_t nsg_spec_accept_noalloc(const void* target_logits, int64_t target_req_stride,
+                                int64_t target_row_stride, const void* draft_logits,
+                                int64_t draft_req_stride, int64_t draft_row_stride,
+                                int32_t logits_dtype, const int64_t* draft_tokens,
+                                const float* uniforms, const int64_t* bonus_tokens,
+                                int32_t batch, int32_t k, int32_t vocab, float temperature,
+                                const int32_t* kv_indptr, const int32_t* kv_indices,
+                                const int32_t* start_pos, int32_t page_size,
+                                int32_t* num_emitted, int64_t* emitted, int64_t* rollback_slots,
+                                int32_t* flags, nsg_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Sampling with temperature, top-k and top-p: one token per logits row.

@@ -36,6 +36,7 @@
 //     select_kernel (chunk prefix, block scan of one chunk).
 #include <cfloat>
 #include <climits>
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
@@ -1070,17 +1071,20 @@ extern "C" int64_t nsg_spec_accept_workspace_bytes(int32_t batch, int32_t k, int
   return layout(batch, k, vocab, false).total;
 }
 
-extern "C" int32_t nsg_spec_accept(const void* target_logits, int64_t target_req_stride,
-                                   int64_t target_row_stride, const void* draft_logits,
-                                   int64_t draft_req_stride, int64_t draft_row_stride,
-                                   int32_t logits_dtype, const int64_t* draft_tokens,
-                                   const float* uniforms, const int64_t* bonus_tokens,
-                                   int32_t batch, int32_t k,
-                                   int32_t vocab, float temperature, const int32_t* kv_indptr,
-                                   const int32_t* kv_indices, const int32_t* start_pos,
-                                   int32_t page_size, int32_t* num_emitted, int64_t* emitted,
-                                   int64_t* rollback_slots, void* workspace,
-                                   int64_t workspace_bytes, nsg_stream_t stream) {
+namespace nsg {
+namespace {
+
+// The body of both acceptance entry points: argument checks, the workspace
+// layout and the launches.  `flags` receives the device-detected error bits.
+int32_t accept_impl(const void* target_logits, int64_t target_req_stride,
+                    int64_t target_row_stride, const void* draft_logits,
+                    int64_t draft_req_stride, int64_t draft_row_stride, int32_t logits_dtype,
+                    const int64_t* draft_tokens, const float* uniforms,
+                    const int64_t* bonus_tokens, int32_t batch, int32_t k, int32_t vocab,
+                    float temperature, const int32_t* kv_indptr, const int32_t* kv_indices,
+                    const int32_t* start_pos, int32_t page_size, int32_t* num_emitted,
+                    int64_t* emitted, int64_t* rollback_slots, void* workspace,
+                    int64_t workspace_bytes, int* flags, nsg_stream_t stream) {
   NSG_CHECK_ARG(batch >= 0 && batch <= kMaxBatch, "batch %d outside [0, %d]", batch, kMaxBatch);
   NSG_CHECK_ARG(k >= 0 && k <= kMaxK, "k %d outside [0, %d]", k, kMaxK);
   NSG_CHECK_ARG(vocab > 0, "vocab %d", vocab);
@@ -1141,7 +1145,7 @@ extern "C" int32_t nsg_spec_accept(const void* target_logits, int64_t target_req
   p.nch2 = L.nch2;
   p.cs2 = L.cs2;
   char* ws = static_cast<char*>(workspace);
-  p.flags = reinterpret_cast<int*>(ws);
+  p.flags = flags;
   p.stats = reinterpret_cast<float2*>(ws + L.stats_off);
   p.dec = reinterpret_cast<float*>(ws + L.dec_off);
   p.psum = reinterpret_cast<float*>(ws + L.psum_off);
@@ -1163,6 +1167,96 @@ extern "C" int32_t nsg_spec_accept(const void* target_logits, int64_t target_req
     return NSG_ERR_ARG;
   }
   return launch_accept<float>(p, L.rows, s);
+}
+
+}  // namespace
+}  // namespace nsg
+
+extern "C" int32_t nsg_spec_accept(const void* target_logits, int64_t target_req_stride,
+                                   int64_t target_row_stride, const void* draft_logits,
+                                   int64_t draft_req_stride, int64_t draft_row_stride,
+                                   int32_t logits_dtype, const int64_t* draft_tokens,
+                                   const float* uniforms, const int64_t* bonus_tokens,
+                                   int32_t batch, int32_t k,
+                                   int32_t vocab, float temperature, const int32_t* kv_indptr,
+                                   const int32_t* kv_indices, const int32_t* start_pos,
+                                   int32_t page_size, int32_t* num_emitted, int64_t* emitted,
+                                   int64_t* rollback_slots, void* workspace,
+                                   int64_t workspace_bytes, nsg_stream_t stream) {
+  return accept_impl(target_logits, target_req_stride, target_row_stride, draft_logits,
+                     draft_req_stride, draft_row_stride, logits_dtype, draft_tokens, uniforms,
+                     bonus_tokens, batch, k, vocab, temperature, kv_indptr, kv_indices, start_pos,
+                     page_size, num_emitted, emitted, rollback_slots, workspace, workspace_bytes,
+                     static_cast<int*>(workspace), stream);
+}
+
+// ---- the allocation-free variant ----
+//
+// Its workspace is `scratch`, a static device array of this file: every GPU
+// the library runs on holds one copy of kNoAllocScratchBytes until the
+// process ends.  In host code `scratch` names a host-side stand-in, so the
+// array is only ever reached through the device address hipGetSymbolAddress
+// returns, looked up once per device with that device current and kept in
+// g_scratch_ptr.  Every call on a GPU shares that GPU's array (the kernels
+// rewrite what they read and leave their counters at zero), so calls that
+// overlap on one GPU race.
+namespace {
+
+constexpr int64_t kNoAllocScratchBytes = 8ll << 20;
+constexpr int kMaxScratchDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+int32_t scratch_address(void** out) {
+  int dev = -1;
+  NSG_CHECK_HIP(hipGetDevice(&dev));
+  NSG_CHECK_ARG(dev >= 0 && dev < kMaxScratchDevices, "device %d outside [0, %d)", dev,
+                kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      set_error("hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                hipGetErrorString(e));
+      return NSG_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return NSG_OK;
+}
+
+}  // namespace
+
+extern "C" int64_t nsg_spec_accept_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int32_t nsg_spec_accept_noalloc(
+    const void* target_logits, int64_t target_req_stride, int64_t target_row_stride,
+    const void* draft_logits, int64_t draft_req_stride, int64_t draft_row_stride,
+    int32_t logits_dtype, const int64_t* draft_tokens, const float* uniforms,
+    const int64_t* bonus_tokens, int32_t batch, int32_t k, int32_t vocab, float temperature,
+    const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* start_pos,
+    int32_t page_size, int32_t* num_emitted, int64_t* emitted, int64_t* rollback_slots,
+    int32_t* flags, nsg_stream_t stream) {
+  NSG_CHECK_ARG(batch >= 0 && k >= 0 && vocab > 0, "batch %d, k %d, vocab %d", batch, k, vocab);
+  const int64_t need = layout(batch, k, vocab, false).total;
+  if (need > kNoAllocScratchBytes) {
+    set_error("batch %d, k %d, vocab %d needs %lld bytes of workspace; the static scratch of "
+              "nsg_spec_accept_noalloc holds %lld", batch, k, vocab, (long long)need,
+              (long long)kNoAllocScratchBytes);
+    return NSG_ERR_WORKSPACE;
+  }
+  void* ws = nullptr;
+  const int32_t rc = scratch_address(&ws);
+  if (rc) return rc;
+  // without a caller word the flags land in the scratch header, unread
+  return accept_impl(target_logits, target_req_stride, target_row_stride, draft_logits,
+                     draft_req_stride, draft_row_stride, logits_dtype, draft_tokens, uniforms,
+                     bonus_tokens, batch, k, vocab, temperature, kv_indptr, kv_indices, start_pos,
+                     page_size, num_emitted, emitted, rollback_slots, ws, kNoAllocScratchBytes,
+                     flags ? flags : static_cast<int*>(ws), stream);
 }
 
 extern "C" int32_t nsg_spec_accept_check_flags(void* workspace, int32_t* flags_h,

@@ -45,12 +45,49 @@ inline int32_t launch_status(const char* what) {
 }
 
 // ---- workspaces ----
-// The acceptance and sampling entry points may be handed one workspace (one
-// per stream, by their callers).  Its first kWorkspaceHeaderBytes hold the
-// acceptance kernels' error-flag word and their cross-workgroup counters;
-// the sampler's layout starts after them, so a sampling call never touches
-// what an acceptance call reads back or relies on being zero.
+// An acceptance workspace starts with a header of kWorkspaceHeaderBytes whose
+// first word holds the error flags; the sampler's layout skips the same
+// header.
 constexpr int64_t kWorkspaceHeaderBytes = 256;
+
+// ---- hand-off between workgroups of one launch ----
+// gfx950's L2 is per XCD and, for ordinary device memory, coherent across
+// XCDs only at kernel boundaries.  The few words one workgroup hands to
+// another inside a launch are therefore written and read only with
+// device-scope read-modify-write atomics -- an exchange to write, an add of
+// zero to read -- which the memory side performs in one order for every
+// XCD.  hand_put_sync also waits for its exchange to return, so that the word
+// is in place before anything this thread writes later; no L2 write-back or
+// invalidate is needed, and the bulk data (logits) keeps its ordinary path.
+__device__ __forceinline__ void hand_put(uint32_t* p, uint32_t v) { (void)atomicExch(p, v); }
+__device__ __forceinline__ void hand_put_sync(uint32_t* p, uint32_t v) {
+  const uint32_t old = atomicExch(p, v);
+  asm volatile("" ::"v"(old));   // the returned word: the exchange has been performed
+}
+__device__ __forceinline__ uint32_t hand_get(const uint32_t* p) {
+  return atomicAdd(const_cast<uint32_t*>(p), 0u);
+}
+__device__ __forceinline__ void hand_put(float* p, float v) {
+  hand_put(reinterpret_cast<uint32_t*>(p), __float_as_uint(v));
+}
+__device__ __forceinline__ void hand_put_sync(float* p, float v) {
+  hand_put_sync(reinterpret_cast<uint32_t*>(p), __float_as_uint(v));
+}
+__device__ __forceinline__ float hand_get(const float* p) {
+  return __uint_as_float(hand_get(reinterpret_cast<const uint32_t*>(p)));
+}
+__device__ __forceinline__ uint64_t hand_get_bits(const float2* p) {
+  return atomicAdd(reinterpret_cast<unsigned long long*>(const_cast<float2*>(p)), 0ull);
+}
+__device__ __forceinline__ void hand_put(float2* p, float2 v) {
+  const unsigned long long bits =
+      (unsigned long long)__float_as_uint(v.x) | ((unsigned long long)__float_as_uint(v.y) << 32);
+  (void)atomicExch(reinterpret_cast<unsigned long long*>(p), bits);
+}
+__device__ __forceinline__ float2 hand_get(const float2* p) {
+  const uint64_t bits = hand_get_bits(p);
+  return make_float2(__uint_as_float((uint32_t)bits), __uint_as_float((uint32_t)(bits >> 32)));
+}
 
 // ---- device types ----
 typedef __bf16 bf16;

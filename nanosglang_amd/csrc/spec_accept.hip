@@ -15,25 +15,25 @@
 //     or the caller's bonus token when one is given (a top-k / top-p draw
 //     from target row k, speculative.py:174-182).
 //
-// Launches (no workgroup waits on another inside a launch: on gfx950 that
-// handshake needs agent-scope fences, which write back and invalidate the
-// XCD's L2):
-//   stats_kernel   grid (chunks, rows): every target row (and draft row when
-//     stochastic) is cut into chunks; a workgroup reduces its chunk to
-//     (max, sum 2^x) -- or (max, first argmax) when greedy -- from batches of
-//     non-temporal 16-byte loads issued together, with a lazily rescaled
-//     running sum (fma + exp + add per logit).  This pass streams every logit
-//     once.
-//   greedy: finalize_kernel, one wave per request: combine the argmax chunks,
-//     compare with the drafts, write tokens and rollback slots.
-//   stochastic (V % 8 == 0): resolve_kernel grid (16, B): each workgroup
-//     runs the decision (the k ratio tests, a ballot for the first
-//     rejection), then its 4 waves stream 4 of the request's 64 vocabulary
-//     ranges of the one decided row pair and write per-step weight sums;
-//     select_kernel2, one wave per request, walks those sums to the step and
-//     recomputes that one step for the token.
-//   stochastic (other V): decide_kernel, sum_kernel (chunk sums) and
-//     select_kernel (chunk prefix, block scan of one chunk).
+// Launches:
+//   greedy: greedy_fused_kernel, grid (chunks, target rows): every target
+//     row is cut into chunks; a workgroup reduces its chunk to (max, first
+//     argmax) from batches of non-temporal 16-byte loads issued together, and
+//     each request's last workgroup loads all of that request's chunk records
+//     at once, compares with the drafts and writes tokens, counts and rollback
+//     slots.  One launch, one read of every logit; a request's tail overlaps
+//     later requests' streaming.
+//   stochastic (V % 8 == 0): stoch_fused_kernel, one launch: chunk statistics
+//     (max, sum 2^x with a lazily rescaled running sum; the chunk holding a
+//     draft token publishes that logit) of every target and draft row; each
+//     request's decision (k ratio tests, a ballot for the first rejection) by
+//     its last statistics workgroup; then range workgroups that stream the
+//     decided row pair into step sums, and the token pick by inverse CDF.
+//   stochastic (other V): stats_kernel, then decide_kernel, sum_kernel
+//     (chunk sums) and select_kernel (chunk prefix, block scan of one chunk).
+// Workgroups hand words to each other inside a launch only through
+// device-scope atomic exchanges and coherent loads of slots that read zero
+// between calls (common.hpp; "hand-off slots" below).
 #include <cfloat>
 #include <climits>
 #include <mutex>
@@ -51,6 +51,10 @@ constexpr int kMaxChunks = 64;
 constexpr int kTargetWgs = 4096;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kSlack = 16.f;  // lazy-rescale headroom of the running sums (log2 units)
+constexpr int kSpinLimit = 1 << 20;  // polls of a hand-off slot before giving up (flag bit 3)
+// Per-request decision record (three hand-off slots), one 128-byte line per
+// request, so that the pollers of different requests use different lines.
+constexpr int kDecStride = 32;       // floats per request
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -65,6 +69,7 @@ struct AccParams {
   int B, k, V;
   float c;  // log2(e) / T
   int greedy;
+  int rpr;  // rows per request: k+1 (greedy) or 2k+1 (target rows, then draft rows)
   const int* kv_indptr;
   const int* kv_indices;
   const int* start_pos;
@@ -74,11 +79,11 @@ struct AccParams {
   int64_t* rollback;
   int nch, cs;    // stats chunks / chunk size
   int nch2, cs2;  // sample chunks / chunk size
-  float2* stats;  // [rows][nch]
-  float* dec;     // [B][8]
+  float2* stats;  // [B][rpr][nch] chunk records, request-major
+  float* dec;     // [B][kDecStride]: decision slots
   float* psum;    // [B][nch2]
   float2* rsum;   // [B][kRsRanges][kRsMaxSteps] step sums (residual, target)
-  float* xlog;    // [rows] logit at the row's draft token (stochastic rows i < k)
+  float* xlog;    // [B][rpr] logit at the row's draft token (stochastic rows)
   int* flags;
 };
 
@@ -118,6 +123,17 @@ struct Logit<float> {
   static constexpr int kAlign = 4;
 };
 
+// Element e of 8 logits held as raw 16-byte words.
+template <typename T>
+__device__ __forceinline__ float raw_at(const u32x4* r, int e) {
+  if constexpr (sizeof(T) == 2) {
+    const uint32_t w = r[0][e >> 1];
+    return __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
+  } else {
+    return __uint_as_float(r[e >> 2][e & 3]);
+  }
+}
+
 // (max, sum 2^(x - max)) pair merge.
 __device__ __forceinline__ void ms_merge(float& m, float& s, float m2, float s2) {
   const float M = fmaxf(m, m2);
@@ -156,20 +172,6 @@ __device__ __forceinline__ void wave_am(float& v, int& i) {
   }
 }
 
-__device__ __forceinline__ void row_of(const AccParams& p, int r, int& b, int& i, bool& draft) {
-  const int nt = p.B * (p.k + 1);
-  if (r < nt) {
-    b = r / (p.k + 1);
-    i = r - b * (p.k + 1);
-    draft = false;
-  } else {
-    const int r2 = r - nt;
-    b = r2 / p.k;
-    i = r2 - b * p.k;
-    draft = true;
-  }
-}
-
 __device__ __forceinline__ int64_t trow(const AccParams& p, int b, int i) {
   return (int64_t)b * p.t_req + (int64_t)i * p.t_row;
 }
@@ -177,35 +179,118 @@ __device__ __forceinline__ int64_t drow(const AccParams& p, int b, int i) {
   return (int64_t)b * p.d_req + (int64_t)i * p.d_row;
 }
 
-// Flat slots of the rejected verify positions start+n .. start+k.
-__device__ void write_rollback(const AccParams& p, int b, int n) {
-  if (!p.rollback) return;
-  for (int i = 0; i < p.k; ++i) {
-    int64_t slot = -1;
-    const int pos = p.start_pos[b] + n + i;
-    if (n + i <= p.k && p.kv_indptr) {
-      const int pb = p.kv_indptr[b];
-      const int np = p.kv_indptr[b + 1] - pb;
-      const int pg = pos >> p.log2P;
-      if (pos >= 0 && pg < np) {
-        slot = ((int64_t)p.kv_indices[pb + pg] << p.log2P) + (pos & ((1 << p.log2P) - 1));
-      } else {
-        atomicOr(p.flags, 2);
-      }
+// Flat slot of rejected verify position start + n + i, lane i < k of one wave
+// (-1 past start + k, or past the request's pages, which also sets flag bit 1).
+__device__ void rollback_lanes(const AccParams& p, int b, int n, int lane) {
+  if (!p.rollback || lane >= p.k) return;
+  int64_t slot = -1;
+  const int pos = p.start_pos[b] + n + lane;
+  if (n + lane <= p.k) {
+    const int pb = p.kv_indptr[b];
+    const int np = p.kv_indptr[b + 1] - pb;
+    const int pg = pos >> p.log2P;
+    if (pos >= 0 && pg < np) {
+      slot = ((int64_t)p.kv_indices[pb + pg] << p.log2P) + (pos & ((1 << p.log2P) - 1));
+    } else {
+      atomicOr(p.flags, 2);
     }
-    p.rollback[(int64_t)b * p.k + i] = slot;
   }
+  p.rollback[(int64_t)b * p.k + lane] = slot;
 }
 
+// ---- hand-off slots ----
+// Every word the acceptance kernels write into the workspace body is zero
+// again when the call ends (the reader of each word clears it), so the body
+// is all zero between calls whatever layout (batch, k, vocabulary) the
+// previous call used.  Chunk records and step sums pass between workgroups
+// of one launch through slots that hold zero between calls.  A published value is never all-zero
+// bits -- a greedy record is (max, ~index); a stochastic record (m, s) has
+// s >= 1, or m = -FLT_MAX for an all -inf chunk; step sums carry their sign
+// bit set (both sums are >= +0) -- so a reader polls a slot until it is
+// non-zero, and the one reader of a slot clears it after use.  Each
+// request's finishing workgroup is the last one dispatched among those it
+// waits for (workgroups start in index order), so its polls end at once or
+// after the stragglers' last stores; they are bounded all the same (flag
+// bit 3).
+__device__ __forceinline__ float2 poll_slot(const AccParams& p, float2* slot) {
+  uint64_t bits = hand_get_bits(slot);
+  for (int n = 0; bits == 0; ++n) {
+    if (n == kSpinLimit) {
+      atomicOr(p.flags, 8);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    bits = hand_get_bits(slot);
+  }
+  return make_float2(__uint_as_float((uint32_t)bits), __uint_as_float((uint32_t)(bits >> 32)));
+}
+
+__device__ __forceinline__ void clear_slot(float2* slot) { hand_put(slot, make_float2(0.f, 0.f)); }
+
+__device__ __forceinline__ float2 mark_sums(float a, float b) {
+  return make_float2(__uint_as_float(__float_as_uint(a) | 0x80000000u),
+                     __uint_as_float(__float_as_uint(b) | 0x80000000u));
+}
+
+__device__ __forceinline__ float2 unmark_sums(float2 v) {
+  return make_float2(__uint_as_float(__float_as_uint(v.x) & 0x7fffffffu),
+                     __uint_as_float(__float_as_uint(v.y) & 0x7fffffffu));
+}
+
+__device__ __forceinline__ void clear_slots(float2* base, int n) {
+  for (int c = threadIdx.x & 63; c < n; c += 64) clear_slot(base + c);
+}
+
+constexpr int kRecCap = 128;  // chunk records per request: two per lane of one wave
+
+// A request's n <= kRecCap chunk records, lane l holding records l and l + 64
+// (both loads in flight together; each re-polled until published).
+struct Recs {
+  uint64_t r0, r1;
+};
+__device__ __forceinline__ uint64_t repoll(const AccParams& p, const float2* slot, uint64_t bits) {
+  for (int n = 0; bits == 0; ++n) {
+    if (n == kSpinLimit) {
+      atomicOr(p.flags, 8);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    bits = hand_get_bits(slot);
+  }
+  return bits;
+}
+__device__ __forceinline__ Recs poll_recs(const AccParams& p, const float2* base, int n) {
+  const int lane = threadIdx.x & 63;
+  Recs r;
+  r.r0 = lane < n ? hand_get_bits(base + lane) : 1;
+  r.r1 = lane + 64 < n ? hand_get_bits(base + lane + 64) : 1;
+  r.r0 = repoll(p, base + lane, r.r0);
+  r.r1 = repoll(p, base + lane + 64, r.r1);
+  return r;
+}
+// Record idx (< kRecCap) of the request, fetched from the lane holding it
+// (every lane of the wave takes part).
+__device__ __forceinline__ float2 rec_at(const Recs& r, int idx) {
+  const int src = idx & 63;
+  const uint32_t a0 = __shfl((uint32_t)r.r0, src, 64), b0 = __shfl((uint32_t)(r.r0 >> 32), src, 64);
+  const uint32_t a1 = __shfl((uint32_t)r.r1, src, 64), b1 = __shfl((uint32_t)(r.r1 >> 32), src, 64);
+  return idx < 64 ? make_float2(__uint_as_float(a0), __uint_as_float(b0))
+                  : make_float2(__uint_as_float(a1), __uint_as_float(b1));
+}
+
+// Chunk `chunk` of request b's row lr (target rows 0..k, then draft rows
+// k+1..2k) reduced by the whole workgroup; thread 0 publishes the chunk record
+// at record lr * nch + chunk of the request and, for a stochastic ratio-test
+// row, the thread whose vector holds the draft token publishes that logit
+// first (hand-off words, so that a workgroup on another XCD may read them
+// inside the same launch).
 template <typename T, bool GREEDY>
-__global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
+__device__ void row_chunk_stats(const AccParams& p, int b, int lr, int chunk) {
   __shared__ float sm_a[kThreads / 64];
   __shared__ float sm_b[kThreads / 64];
-  const int r = blockIdx.y;
-  const int chunk = blockIdx.x;
-  int b, i;
-  bool draft;
-  row_of(p, r, b, i, draft);
+  const bool draft = lr > p.k;
+  const int i = draft ? lr - p.k - 1 : lr;
+  const int r = b * p.rpr + lr;
   const void* base = draft ? p.dl : p.tl;
   const int64_t roff = draft ? drow(p, b, i) : trow(p, b, i);
   const int v0 = chunk * p.cs;
@@ -228,8 +313,17 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
   // (-FLT_MAX): an all -inf chunk then sums exact zeros instead of NaN.
   float m = -FLT_MAX, s = 0.f;
   float m_hi = -FLT_MAX;         // rescale threshold: m + kSlack
-  float bv = -INFINITY;          // greedy: best value / index
+  float bv = -INFINITY;          // greedy, scalar elements: best value / index
   int bi = INT_MAX;
+  // greedy, whole vectors (branch-free): the first vector holding this lane's
+  // maximum (strict >), its start index and its raw words; the element is
+  // found once, after the stream
+  constexpr int W = sizeof(T) * 8 / 16;  // 16-byte words per 8 logits
+  float vbest = -INFINITY;
+  int vidx = INT_MAX;
+  u32x4 vraw[W];
+#pragma unroll
+  for (int w = 0; w < W; ++w) vraw[w] = u32x4{0u, 0u, 0u, 0u};
   auto take = [&](float x, int v) {
     if constexpr (GREEDY) {
       am_merge(bv, bi, x, v);
@@ -251,18 +345,15 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
   // Per 8 logits: greedy -- one max, and the (rare) index search only when the
   // vector beats the running best; stochastic -- max on the raw logits (c > 0),
   // then exp2(fma(x, c, -m)) with the bare v_exp_f32 (arguments <= 0).
-  auto take8 = [&](const float* x, int vv) {
+  auto take8 = [&](const float* x, int vv, const u32x4* rw) {
     float mx = fmaxf(fmaxf(fmaxf(fmaxf(x[0], x[1]), x[2]), fmaxf(x[3], x[4])),
                      fmaxf(fmaxf(x[5], x[6]), x[7]));  // v_max3 x 3 + v_max
     if constexpr (GREEDY) {
-      if (mx > bv || bi == INT_MAX) {
-        int e = 0;
-        while (e < 7 && !(x[e] == mx)) ++e;   // first index of the max (NaN-free rows)
-        if (mx > bv || bi == INT_MAX) {
-          bv = mx;
-          bi = vv + e;
-        }
-      }
+      const bool better = mx > vbest || vidx == INT_MAX;   // selects, no branch
+      vbest = better ? mx : vbest;
+      vidx = better ? vv : vidx;
+#pragma unroll
+      for (int w = 0; w < W; ++w) vraw[w] = better ? rw[w] : vraw[w];
     } else {
       if (__builtin_expect(vv == (xt & ~7), 0)) {  // never for xt = -1
 #pragma unroll
@@ -291,7 +382,6 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
   if (vec) {
     constexpr int U = 8;
     constexpr int STRIDE = kThreads * 8;
-    constexpr int W = sizeof(T) * 8 / 16;  // 16-byte loads per 8 logits
     auto batch = [&](int vb, auto full) {
       u32x4 raw[U][W];
 #pragma unroll
@@ -325,7 +415,7 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
 #pragma unroll
           for (int i = 0; i < 8; ++i) x[i] = __uint_as_float(raw[u][i >> 2][i & 3]);
         }
-        take8(x, vb + u * STRIDE);
+        take8(x, vb + u * STRIDE, raw[u]);
       }
     };
     int vb = v;
@@ -337,10 +427,18 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
   for (int vv = (vec ? vfull : v0) + tid; vv < v1; vv += kThreads) take(Logit<T>::at(base, roff + vv), vv);
 
   if constexpr (!GREEDY) {
-    if (xhit) p.xlog[r] = xval;
+    if (xhit) hand_put_sync(p.xlog + r, xval);  // in place before the record vouching for it
   }
   const int lane = tid & 63, wave = tid >> 6;
   if constexpr (GREEDY) {
+    if (vidx != INT_MAX) {  // the first element of the best vector equal to its max
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = raw_at<T>(vraw, e);
+      int e = 0;
+      while (e < 7 && !(x[e] == vbest)) ++e;   // NaN-free rows
+      am_merge(bv, bi, vbest, vidx + e);
+    }
     wave_am(bv, bi);
     if (lane == 0) {
       sm_a[wave] = bv;
@@ -366,43 +464,53 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
         ms_merge(a, c2, sm_a[w], sm_b[w]);
       }
     }
-    p.stats[(int64_t)r * p.nch + chunk] = make_float2(a, c2);
+    if constexpr (GREEDY) c2 = __int_as_float(~__float_as_int(c2));  // never all-zero bits
+    hand_put(p.stats + (int64_t)r * p.nch + chunk, make_float2(a, c2));
   }
 }
 
-// Greedy: one wave per request combines the argmax chunks of its k+1 target
-// rows, compares them with the drafts and writes every output.
-__global__ __launch_bounds__(64) void greedy_finalize_kernel(AccParams p) {
-  const int b = blockIdx.x;
-  const int lane = threadIdx.x;
+template <typename T, bool GREEDY>
+__global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
+  const int b = blockIdx.y / p.rpr;
+  row_chunk_stats<T, GREEDY>(p, b, blockIdx.y - b * p.rpr, blockIdx.x);
+}
+
+// Greedy: one wave combines the argmax chunk records of request b's k+1
+// target rows (all loaded at once), compares them with the drafts and writes
+// every output; then it clears the records.
+__device__ void greedy_finalize(const AccParams& p, int b) {
+  const int lane = threadIdx.x & 63;
   const int k = p.k;
+  const int n = (k + 1) * p.nch;
+  int64_t x = -1;
+  if (lane < k) x = p.dtok[(int64_t)b * k + lane];   // in flight with the records
+  float2* recs = p.stats + (int64_t)b * n;
+  const Recs rc = poll_recs(p, recs, n);
+  float v = -INFINITY;   // lane i <= k: argmax of target row i (first index on ties)
+  int ix = INT_MAX;
+  for (int c = 0; c < p.nch; ++c) {
+    const float2 st = rec_at(rc, min(lane, k) * p.nch + c);
+    if (lane <= k) am_merge(v, ix, st.x, ~__float_as_int(st.y));
+  }
+  if (lane < k && (x < 0 || x >= p.V)) atomicOr(p.flags, 4);  // never matches; flag it
+  const uint64_t miss = __builtin_amdgcn_ballot_w64(lane < k && x != (int64_t)ix);
+  const int j = miss ? (int)__builtin_ctzll(miss) : k;           // first mismatch, or k
   int64_t* em = p.emitted + (int64_t)b * (k + 1);
-  if (lane < k) {  // a draft token outside the vocabulary never matches; flag it
-    const int64_t d = p.dtok[(int64_t)b * k + lane];
-    if (d < 0 || d >= p.V) atomicOr(p.flags, 4);
-  }
-  int n = k + 1;
-  for (int i = 0; i <= k; ++i) {
-    const int r = b * (k + 1) + i;
-    float v = -INFINITY;
-    int ix = INT_MAX;
-    for (int c = lane; c < p.nch; c += 64) {
-      const float2 st = p.stats[(int64_t)r * p.nch + c];
-      am_merge(v, ix, st.x, __float_as_int(st.y));
-    }
-    wave_am(v, ix);
-    const bool match = i < k && p.dtok[(int64_t)b * k + i] == (int64_t)ix;
-    if (lane == 0) em[i] = ix;
-    if (!match) {
-      n = i + 1;
-      break;
-    }
-  }
-  if (lane == 0) {
-    for (int i = n; i <= k; ++i) em[i] = -1;
-    p.n_out[b] = n;
-    write_rollback(p, b, n);
-  }
+  if (lane <= k) em[lane] = lane < j ? x : (lane == j ? (int64_t)ix : -1);
+  if (lane == 0) p.n_out[b] = j + 1;
+  rollback_lanes(p, b, j + 1, lane);
+  clear_slots(recs, n);
+}
+
+// Greedy in one launch: the argmax pass over every target row; request b's
+// last workgroup (its last row's last chunk, the last of b's workgroups to
+// start) finalises b while later requests still stream.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void greedy_fused_kernel(AccParams p) {
+  const int b = blockIdx.y / p.rpr;
+  const int lr = blockIdx.y - b * p.rpr;
+  row_chunk_stats<T, true>(p, b, lr, blockIdx.x);
+  if (lr == p.k && (int)blockIdx.x == p.nch - 1 && threadIdx.x < 64) greedy_finalize(p, b);
 }
 
 struct Decision {
@@ -411,46 +519,92 @@ struct Decision {
   float Mt, iZt, Md, iZd;
 };
 
-// Stochastic decision of request b, computed by one wave, returned to every
-// lane.  Lane i (i <= k) reduces the chunk stats of target row i, lane i < k
-// also those of draft row i and runs ratio test i with the draft-token logits
-// stats_kernel recorded; a ballot finds the first rejection.  Every load is
-// issued before the arithmetic: one memory round trip.
-// With `write`, the wave also writes the accepted prefix, num_emitted, the
-// rollback slots and the decision record read by select_kernel.
+// The decision record of request b: three hand-off slots, each never
+// all-zero bits once published -- (j + 1, mode + 1), (Mt, 1/Zt) with 1/Zt > 0,
+// (Md, 1/Zd) with 1/Zd > 0, or (0, 1) when mode = 1 -- cleared by the
+// request's token pick.
+__device__ __forceinline__ float2* dec_slots(const AccParams& p, int b) {
+  return reinterpret_cast<float2*>(p.dec + (int64_t)b * kDecStride);
+}
+__device__ __forceinline__ void clear_slots3(float2* ds) {
+  for (int i = 0; i < 3; ++i) clear_slot(ds + i);
+}
+__device__ __forceinline__ void publish_decision(const AccParams& p, int b, const Decision& d,
+                                                 int lane) {
+  float2* ds = dec_slots(p, b);
+  if (lane == 0) hand_put(ds, make_float2(__int_as_float(d.j + 1), __int_as_float(d.mode + 1)));
+  if (lane == 1) hand_put(ds + 1, make_float2(d.Mt, d.iZt));
+  if (lane == 2) hand_put(ds + 2, d.mode == 0 ? make_float2(d.Md, d.iZd) : make_float2(0.f, 1.f));
+}
+// Every lane returns request b's decision (lanes 0..2 poll one slot each).
+__device__ Decision read_decision(const AccParams& p, int b) {
+  const int lane = threadIdx.x & 63;
+  const float2* ds = dec_slots(p, b);
+  uint64_t bits = lane < 3 ? hand_get_bits(ds + lane) : 1;
+  bits = repoll(p, ds + min(lane, 2), bits);
+  const uint32_t lo = (uint32_t)bits, hi = (uint32_t)(bits >> 32);
+  Decision d;
+  d.j = (int)__shfl(lo, 0, 64) - 1;
+  d.mode = (int)__shfl(hi, 0, 64) - 1;
+  d.Mt = __uint_as_float(__shfl(lo, 1, 64));
+  d.iZt = __uint_as_float(__shfl(hi, 1, 64));
+  d.Md = __uint_as_float(__shfl(lo, 2, 64));
+  d.iZd = __uint_as_float(__shfl(hi, 2, 64));
+  return d;
+}
+
+// Request b's decision in a later launch than the one that published it.
+__device__ __forceinline__ Decision decision_of(const AccParams& p, int b) {
+  const float2* ds = dec_slots(p, b);
+  const float2 s0 = ds[0], s1 = ds[1], s2 = ds[2];
+  Decision d;
+  d.j = __float_as_int(s0.x) - 1;
+  d.mode = __float_as_int(s0.y) - 1;
+  d.Mt = s1.x;
+  d.iZt = s1.y;
+  d.Md = s2.x;
+  d.iZd = s2.y;
+  return d;
+}
+
+// Stochastic decision of request b by one wave: every chunk record of its 2k+1
+// rows is loaded at once (lane l: records l and l + 64), then lane i merges
+// target row i and draft row i and runs ratio test i with the draft-token
+// logits the chunks published; a ballot finds the first rejection.  The wave
+// writes the accepted prefix, num_emitted, the rollback slots and the caller's
+// bonus (all accepted), publishes the decision and clears the records.
 template <typename T>
-__device__ Decision decide(const AccParams& p, int b, bool write) {
+__device__ Decision decide(const AccParams& p, int b) {
   const int lane = threadIdx.x & 63;
   const int k = p.k;
+  const int rpr = 2 * k + 1;
+  const int n = rpr * p.nch;
   int64_t x = 0;
-  float xt = 0.f, xd = 0.f, u = 0.f;
-  if (lane < k) {
+  float u = 0.f;
+  if (lane < k) {                            // in flight with the records
     x = p.dtok[(int64_t)b * k + lane];
-    xt = p.xlog[b * (k + 1) + lane];
-    xd = p.xlog[p.B * (k + 1) + b * k + lane];
     u = p.u[(int64_t)b * (k + 1) + lane];
   }
-  float mt = -INFINITY, zt = 0.f, md = -INFINITY, zd = 0.f;
-  if (lane <= k) {
-    const float2* st = p.stats + (int64_t)(b * (k + 1) + lane) * p.nch;
-#pragma unroll 8
-    for (int c = 0; c < p.nch; ++c) {
-      const float2 v = st[c];
-      ms_merge(mt, zt, v.x, v.y);
-    }
+  float2* recs = p.stats + (int64_t)b * n;
+  const Recs rc = poll_recs(p, recs, n);
+  float xt = 0.f, xd = 0.f;
+  if (lane < k) {  // published before the records that vouch for them
+    xt = hand_get(p.xlog + (int64_t)b * rpr + lane);
+    xd = hand_get(p.xlog + (int64_t)b * rpr + k + 1 + lane);
+    hand_put(p.xlog + (int64_t)b * rpr + lane, 0.f);          // the workspace ends zero
+    hand_put(p.xlog + (int64_t)b * rpr + k + 1 + lane, 0.f);
   }
-  if (lane < k) {
-    const float2* st = p.stats + (int64_t)(p.B * (k + 1) + b * k + lane) * p.nch;
-#pragma unroll 8
-    for (int c = 0; c < p.nch; ++c) {
-      const float2 v = st[c];
-      ms_merge(md, zd, v.x, v.y);
-    }
+  float mt = -INFINITY, zt = 0.f, md = -INFINITY, zd = 0.f;
+  for (int c = 0; c < p.nch; ++c) {
+    const float2 t = rec_at(rc, min(lane, k) * p.nch + c);
+    const float2 dr = rec_at(rc, (k + 1 + min(lane, k - 1)) * p.nch + c);
+    if (lane <= k) ms_merge(mt, zt, t.x, t.y);
+    if (lane < k) ms_merge(md, zd, dr.x, dr.y);
   }
   bool reject = false;
   if (lane < k) {
     if (x < 0 || x >= p.V) {
-      if (write) atomicOr(p.flags, 4);
+      atomicOr(p.flags, 4);
       reject = true;
     } else {
       const float lt = xt * p.c;
@@ -469,38 +623,16 @@ __device__ Decision decide(const AccParams& p, int b, bool write) {
   d.iZt = 1.f / __shfl(zt, j, 64);
   d.Md = j < k ? __shfl(md, j, 64) : 0.f;
   d.iZd = j < k ? 1.f / __shfl(zd, j, 64) : 0.f;
-  if (write) {
-    int64_t* em = p.emitted + (int64_t)b * (k + 1);
-    if (lane < j) em[lane] = x;
-    else if (lane <= k) em[lane] = -1;
-    const int n = j + 1;
-    if (lane == 0) p.n_out[b] = n;
-    if (p.rollback && lane < k) {
-      // flat slot of rejected verify position start + n + lane (if <= start + k)
-      int64_t slot = -1;
-      const int pos = p.start_pos[b] + n + lane;
-      if (n + lane <= k) {
-        const int pb = p.kv_indptr[b];
-        const int np = p.kv_indptr[b + 1] - pb;
-        const int pg = pos >> p.log2P;
-        if (pos >= 0 && pg < np) {
-          slot = ((int64_t)p.kv_indices[pb + pg] << p.log2P) + (pos & ((1 << p.log2P) - 1));
-        } else {
-          atomicOr(p.flags, 2);
-        }
-      }
-      p.rollback[(int64_t)b * k + lane] = slot;
-    }
-    if (lane == 0) {
-      float* dd = p.dec + (int64_t)b * 8;
-      dd[0] = __int_as_float(d.j);
-      dd[1] = __int_as_float(d.mode);
-      dd[2] = d.Mt;
-      dd[3] = d.iZt;
-      dd[4] = d.Md;
-      dd[5] = d.iZd;
-    }
+  int64_t* em = p.emitted + (int64_t)b * (k + 1);
+  if (lane < j) em[lane] = x;
+  else if (lane > j && lane <= k) em[lane] = -1;   // em[j]: the token pick's alone
+  if (lane == 0) {
+    p.n_out[b] = j + 1;
+    if (d.mode == 1 && p.bonus) em[k] = p.bonus[b];  // all accepted: the caller's bonus
   }
+  rollback_lanes(p, b, j + 1, lane);
+  publish_decision(p, b, d, lane);
+  clear_slots(recs, n);
   return d;
 }
 
@@ -533,7 +665,7 @@ __device__ float block_incl_scan(float x, float* sh) {
 // One wave per request: the decision, the accepted prefix, counts and slots.
 template <typename T>
 __global__ __launch_bounds__(64) void decide_kernel(AccParams p) {
-  decide<T>(p, blockIdx.x, true);
+  decide<T>(p, blockIdx.x);
 }
 
 // Chunk sums of the decided weights (residual of row j, or target row j).
@@ -543,14 +675,7 @@ __global__ __launch_bounds__(kThreads) void sum_kernel(AccParams p) {
   const int b = blockIdx.y;
   const int chunk = blockIdx.x;
   const int tid = threadIdx.x;
-  const float* dd = p.dec + (int64_t)b * 8;
-  Decision d;
-  d.j = __float_as_int(dd[0]);
-  d.mode = __float_as_int(dd[1]);
-  d.Mt = dd[2];
-  d.iZt = dd[3];
-  d.Md = dd[4];
-  d.iZd = dd[5];
+  const Decision d = decision_of(p, b);
   const int64_t to = trow(p, b, d.j);
   const int64_t dof = d.mode == 0 ? drow(p, b, d.j) : 0;
   const int v0 = chunk * p.cs2;
@@ -624,20 +749,21 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(AccParams p) {
   __shared__ float s_rem, s_tot;
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
-  const float* dd = p.dec + (int64_t)b * 8;
-  const int j = __float_as_int(dd[0]);
-  int mode = __float_as_int(dd[1]);
-  if (mode == 1 && p.bonus) {  // all accepted: the caller's filtered bonus draw
-    if (tid == 0) p.emitted[(int64_t)b * (p.k + 1) + j] = p.bonus[b];
+  const Decision dc = decision_of(p, b);
+  const int j = dc.j;
+  int mode = dc.mode;
+  if (mode == 1 && p.bonus) {  // all accepted: the decision emitted the caller's bonus
+    if (tid == 0) clear_slots3(dec_slots(p, b));
     return;
   }
-  const float Mt = dd[2], iZt = dd[3], Md = dd[4], iZd = dd[5];
+  const float Mt = dc.Mt, iZt = dc.iZt, Md = dc.Md, iZd = dc.iZd;
   const int64_t to = trow(p, b, j);
   const int64_t dof = mode == 0 ? drow(p, b, j) : 0;
   const float u = p.u[(int64_t)b * (p.k + 1) + p.k];
   if (tid < 64) {
     // chunk sums -> inclusive wave scan (nch2 <= 64), fixed order
     const float v = tid < p.nch2 ? p.psum[(int64_t)b * p.nch2 + tid] : 0.f;
+    if (tid < p.nch2) p.psum[(int64_t)b * p.nch2 + tid] = 0.f;   // the workspace ends zero
     float incl = v;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -733,25 +859,24 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(AccParams p) {
     atomicMax(&s_tok, last);
     __syncthreads();
   }
-  if (tid == 0) p.emitted[(int64_t)b * (p.k + 1) + j] = s_tok;
+  if (tid == 0) {
+    p.emitted[(int64_t)b * (p.k + 1) + j] = s_tok;
+    clear_slots3(dec_slots(p, b));   // zero between calls
+  }
 }
 
-// ---- stochastic tail in two launches (V % 8 == 0, V <= kRsMaxV) ----
+// ---- the decided row pair's step sums (V % 8 == 0, V <= kRsMaxV) ----
 //
-// resolve_kernel, grid (kRsSplits, B) x 256 threads: every workgroup of
-// request b runs the (identical) decision in wave 0 -- split 0 also writes
-// the accepted prefix, counts, slots and the decision record -- then each of
-// its waves streams one of the request's kRsRanges contiguous vocabulary
-// ranges of the decided row pair in 512-logit steps (lane l: logits
-// 8 l .. 8 l + 7 of a step, 1 KB contiguous per wave load) and writes the
-// step sums of the residual max(0, pt - pd) and of pt (the zero-residual
-// fallback needs no second pass) -- each an inclusive wave scan of the
-// lanes' 8-logit runs.
-// select_kernel2, one wave per request: lane r sums range r's steps in
-// order, a wave scan orders the ranges, the crossing lane finds its step,
-// and the whole wave recomputes that one step with the same arithmetic
-// (step_runs) to find the lane and the logit.  Rounding that leaves no
-// crossing picks the last positive weight.
+// The request's vocabulary is cut into kRsRanges contiguous ranges of ns
+// 512-logit steps.  A wave streams one range of the decided row pair (lane l:
+// logits 8 l .. 8 l + 7 of a step, 1 KB contiguous per wave load) and writes
+// each step's sums of the residual max(0, pt - pd) and of pt (the
+// zero-residual fallback needs no second pass), each an inclusive wave scan
+// of the lanes' 8-logit runs.  One wave then picks the token: lane r sums
+// range r's steps in order, a wave scan orders the ranges, the crossing lane
+// finds its step, and the whole wave recomputes that one step with the same
+// arithmetic (step_weights) to find the lane and the logit.  Rounding that
+// leaves no crossing picks the last positive weight.
 constexpr int kRsThreads = 256;
 constexpr int kRsWaves = kRsThreads / 64;
 constexpr int kRsSplits = 16;
@@ -795,16 +920,6 @@ __device__ __forceinline__ void step_load(const AccParams& p, int64_t to, int64_
   }
 }
 
-template <typename T>
-__device__ __forceinline__ float raw_at(const u32x4* r, int e) {
-  if constexpr (sizeof(T) == 2) {
-    const uint32_t w = r[0][e >> 1];
-    return __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
-  } else {
-    return __uint_as_float(r[e >> 2][e & 3]);
-  }
-}
-
 // ... and its residual and target weights (zero past V) and their runs.
 template <typename T>
 __device__ __forceinline__ void step_weights(const AccParams& p, int mode, const Decision& d,
@@ -828,26 +943,6 @@ __device__ __forceinline__ void step_weights(const AccParams& p, int mode, const
   }
 }
 
-__device__ __forceinline__ void store_decision(float* dd, const Decision& d) {
-  dd[0] = __int_as_float(d.j);
-  dd[1] = __int_as_float(d.mode);
-  dd[2] = d.Mt;
-  dd[3] = d.iZt;
-  dd[4] = d.Md;
-  dd[5] = d.iZd;
-}
-
-__device__ __forceinline__ Decision load_decision(const float* dd) {
-  Decision d;
-  d.j = __float_as_int(dd[0]);
-  d.mode = __float_as_int(dd[1]);
-  d.Mt = dd[2];
-  d.iZt = dd[3];
-  d.Md = dd[4];
-  d.iZd = dd[5];
-  return d;
-}
-
 // Streams ns steps of the decided row pair from vocabulary index v0 (this
 // lane's first logit) and writes each step's sums (residual, target) -- each
 // an inclusive wave scan of the lanes' 8-logit runs -- to out[0 .. ns).
@@ -855,7 +950,7 @@ template <typename T>
 __device__ __forceinline__ void stream_step_sums(const AccParams& p, const Decision& d,
                                                  int64_t to, int64_t dof, int ns, int v0,
                                                  int lane, float2* out) {
-  constexpr int G = 8;  // steps whose loads are in flight together
+  constexpr int G = 4;  // steps whose loads are in flight together
   for (int q0 = 0; q0 < ns; q0 += G) {
     StepRaw<T> raw[G];
 #pragma unroll
@@ -868,29 +963,9 @@ __device__ __forceinline__ void stream_step_sums(const AccParams& p, const Decis
       step_weights<T>(p, d.mode, d, v0 + (q0 + i) * kRsStep, raw[i], wr, wp, res, pts);
       const float sr = __shfl(wave_incl_scan(res, lane), 63, 64);
       const float sp = __shfl(wave_incl_scan(pts, lane), 63, 64);
-      if (lane == 0) out[q0 + i] = make_float2(sr, sp);
+      if (lane == 0) hand_put(out + q0 + i, mark_sums(sr, sp));
     }
   }
-}
-
-template <typename T>
-__global__ __launch_bounds__(kRsThreads) void resolve_kernel(AccParams p) {
-  __shared__ Decision s_d;
-  const int b = blockIdx.y;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  if (wave == 0) {
-    const Decision d = decide<T>(p, b, blockIdx.x == 0);  // split 0 writes the outputs
-    if (lane == 0) s_d = d;
-  }
-  __syncthreads();
-  const Decision d = s_d;
-  if (d.mode == 1 && p.bonus) return;  // the bonus comes from the caller
-  const int ns = rs_steps(p.V);
-  const int r = blockIdx.x * kRsWaves + wave;
-  stream_step_sums<T>(p, d, trow(p, b, d.j), d.mode == 0 ? drow(p, b, d.j) : 0, ns,
-                      r * ns * kRsStep + 8 * lane, lane,
-                      p.rsum + ((int64_t)b * kRsRanges + r) * kRsMaxSteps);
 }
 
 // The token of request b from the step sums of R contiguous vocabulary
@@ -908,13 +983,10 @@ __device__ void select_token(const AccParams& p, int b, const Decision& d, int l
   const int64_t dof = d.mode == 0 ? drow(p, b, d.j) : 0;
   const float u = p.u[(int64_t)b * (p.k + 1) + p.k];
   const float2* rs = sums + (int64_t)min(lane, R - 1) * S;
-  float sr[S], sp[S];
   float lr = 0.f, lp = 0.f;
-#pragma unroll
+#pragma unroll 4
   for (int q = 0; q < S; ++q) {
     const float2 v = (lane < R && q < ns) ? rs[q] : make_float2(0.f, 0.f);
-    sr[q] = v.x;
-    sp[q] = v.y;
     lr += v.x;
     lp += v.y;
   }
@@ -938,20 +1010,21 @@ __device__ void select_token(const AccParams& p, int b, const Decision& d, int l
   // the chosen range's step (sequential, in the order the range was summed)
   int qs = -1;
   float acc = lane == 0 ? 0.f : excl;
-  if (lane == rsel) {
-#pragma unroll
-    for (int q = 0; q < S; ++q) {
-      const float sq = use_pt ? sp[q] : sr[q];
-      if (qs < 0 && q < ns) {
+  if (lane == rsel) {  // the range's step sums again, summed in the same order
+    for (int q = 0; q < ns; ++q) {
+      const float2 v = rs[q];
+      const float sq = use_pt ? v.y : v.x;
+      if (qs < 0) {
         if (!fallback && sq > 0.f && acc + sq > target) qs = q;
         else acc += sq;
       }
     }
     if (qs < 0) {  // rounding: last positive step of the range
       fallback = true;
-#pragma unroll
-      for (int q = 0; q < S; ++q)
-        if (q < ns && (use_pt ? sp[q] : sr[q]) > 0.f) qs = q;
+      for (int q = 0; q < ns; ++q) {
+        const float2 v = rs[q];
+        if ((use_pt ? v.y : v.x) > 0.f) qs = q;
+      }
     }
   }
   qs = __shfl(qs, rsel, 64);
@@ -984,18 +1057,67 @@ __device__ void select_token(const AccParams& p, int b, const Decision& d, int l
   }
 }
 
+// ---- stochastic acceptance in one launch (V % 8 == 0, V <= kRsMaxV) ----
+//
+// Workgroups 0 .. B*(2k+1)*nch - 1 are the chunk statistics of every row,
+// request by request; request b's last one then runs b's decision in its
+// wave 0 (outputs, rollback slots) and publishes it in three slots.  The
+// kRsSplits workgroups per request after all of them poll those slots, and
+// each of their waves streams one of the request's kRsRanges vocabulary
+// ranges of the decided row pair into step sums; the request's last range
+// workgroup picks the token from all of them and clears every slot it read.
+// Every wait is on workgroups with smaller indices, which start first and
+// never wait on later ones.  (Range blocks interleaved among later requests'
+// statistics were measured slower: they compete with the statistics stream.)
 template <typename T>
-__global__ __launch_bounds__(64) void select_kernel2(AccParams p) {
-  const int b = blockIdx.x;
-  const int lane = threadIdx.x;
-  const Decision d = load_decision(p.dec + (int64_t)b * 8);
-  if (d.mode == 1 && p.bonus) {  // all accepted: the caller's filtered bonus draw
-    if (lane == 0) p.emitted[(int64_t)b * (p.k + 1) + d.j] = p.bonus[b];
+__global__ __launch_bounds__(kThreads) void stoch_fused_kernel(AccParams p) {
+  __shared__ float2 s_sums[kRsRanges * kRsMaxSteps];   // the token pick's step sums
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int per_req = p.rpr * p.nch;
+  const int t = blockIdx.x;
+  if (t < p.B * per_req) {                         // statistics, request by request
+    const int b = t / per_req;
+    const int sub = t - b * per_req;
+    const int lr = sub / p.nch;
+    row_chunk_stats<T, false>(p, b, lr, sub - lr * p.nch);
+    if (sub == per_req - 1 && wave == 0) decide<T>(p, b);   // request b's last chunk
     return;
   }
-  select_token<T, kRsRanges, kRsMaxSteps>(p, b, d, lane,
-                                          p.rsum + (int64_t)b * kRsRanges * kRsMaxSteps,
-                                          rs_steps(p.V));
+  const int b = (t - p.B * per_req) / kRsSplits;  // then the range blocks, request by request
+  const int split = t - p.B * per_req - b * kRsSplits;
+  const Decision d = read_decision(p, b);           // every wave polls the three slots
+  const bool draw = !(d.mode == 1 && p.bonus);     // else the decision emitted the caller's bonus
+  const int ns = rs_steps(p.V);
+  const int rg = split * kRsWaves + wave;
+  float2* sums = p.rsum + (int64_t)b * kRsRanges * kRsMaxSteps;
+  if (draw) {
+    stream_step_sums<T>(p, d, trow(p, b, d.j), d.mode == 0 ? drow(p, b, d.j) : 0, ns,
+                        rg * ns * kRsStep + 8 * lane, lane, sums + rg * kRsMaxSteps);
+  } else if (lane < ns) {                           // mark the range done
+    hand_put(sums + rg * kRsMaxSteps + lane, mark_sums(0.f, 0.f));
+  }
+  if (split == kRsSplits - 1 && wave == 0) {       // request b's last range workgroup
+    // lane r: range r's step sums, all loads in flight, kept in LDS for the pick
+    float2* mine = sums + lane * kRsMaxSteps;
+    constexpr int GQ = 8;                           // loads in flight together
+    for (int q0 = 0; q0 < ns; q0 += GQ) {
+      uint64_t bits[GQ];
+#pragma unroll
+      for (int q = 0; q < GQ; ++q) bits[q] = q0 + q < ns ? hand_get_bits(mine + q0 + q) : 1;
+#pragma unroll
+      for (int q = 0; q < GQ; ++q) {
+        if (q0 + q < ns) {
+          const uint64_t v = repoll(p, mine + q0 + q, bits[q]);
+          s_sums[lane * kRsMaxSteps + q0 + q] = unmark_sums(
+              make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32))));
+        }
+      }
+    }
+    if (draw) select_token<T, kRsRanges, kRsMaxSteps>(p, b, d, lane, s_sums, ns);
+    for (int q = 0; q < ns; ++q) clear_slot(mine + q);
+    if (lane == 0) clear_slots3(dec_slots(p, b));  // every range workgroup has read it
+  }
 }
 
 struct Layout {
@@ -1005,8 +1127,10 @@ struct Layout {
 
 Layout layout(int B, int k, int V, bool greedy) {
   Layout L;
-  L.rows = B * (k + 1) + (greedy ? 0 : B * k);
-  const int max_ch = std::max(1, std::min(kMaxChunks, (V + 2047) / 2048));
+  const int rpr = greedy ? k + 1 : 2 * k + 1;
+  L.rows = B * rpr;
+  // a request's chunk records fit one wave's two registers per lane
+  const int max_ch = std::max(1, std::min({kMaxChunks, (V + 2047) / 2048, kRecCap / rpr}));
   L.nch = std::max(1, std::min(max_ch, (kTargetWgs + L.rows - 1) / std::max(1, L.rows)));
   L.cs = ((V + L.nch - 1) / L.nch + 7) / 8 * 8;
   L.nch = (V + L.cs - 1) / L.cs;
@@ -1018,7 +1142,7 @@ Layout layout(int B, int k, int V, bool greedy) {
   const int rows_max = B * (2 * k + 1);  // one workspace serves both modes
   L.stats_off = kWorkspaceHeaderBytes;
   L.dec_off = L.stats_off + al((int64_t)rows_max * kMaxChunks * 8);
-  L.psum_off = L.dec_off + al((int64_t)B * 8 * 4);
+  L.psum_off = L.dec_off + al((int64_t)B * kDecStride * 4);
   L.rsum_off = L.psum_off + al((int64_t)B * kMaxChunks * 4);
   L.xlog_off = L.rsum_off + al((int64_t)B * kRsRanges * kRsMaxSteps * 8);
   L.total = L.xlog_off + al((int64_t)rows_max * 4);
@@ -1035,22 +1159,17 @@ template <typename T>
 int32_t launch_accept(const AccParams& p, int rows, hipStream_t s) {
   dim3 g1(p.nch, rows);
   if (p.greedy) {
-    hipLaunchKernelGGL((stats_kernel<T, true>), g1, dim3(kThreads), 0, s, p);
-    int32_t rc = launch_status("stats_kernel");
-    if (rc) return rc;
-    hipLaunchKernelGGL(greedy_finalize_kernel, dim3(p.B), dim3(64), 0, s, p);
-    return launch_status("greedy_finalize_kernel");
+    hipLaunchKernelGGL((greedy_fused_kernel<T>), g1, dim3(kThreads), 0, s, p);
+    return launch_status("greedy_fused_kernel");
+  }
+  if (rs_path(p)) {
+    hipLaunchKernelGGL((stoch_fused_kernel<T>), dim3(rows * p.nch + p.B * kRsSplits),
+                       dim3(kThreads), 0, s, p);
+    return launch_status("stoch_fused_kernel");
   }
   hipLaunchKernelGGL((stats_kernel<T, false>), g1, dim3(kThreads), 0, s, p);
   int32_t rc = launch_status("stats_kernel");
   if (rc) return rc;
-  if (rs_path(p)) {
-    hipLaunchKernelGGL((resolve_kernel<T>), dim3(kRsSplits, p.B), dim3(kRsThreads), 0, s, p);
-    rc = launch_status("resolve_kernel");
-    if (rc) return rc;
-    hipLaunchKernelGGL((select_kernel2<T>), dim3(p.B), dim3(64), 0, s, p);
-    return launch_status("select_kernel");
-  }
   hipLaunchKernelGGL((decide_kernel<T>), dim3(p.B), dim3(64), 0, s, p);
   rc = launch_status("decide_kernel");
   if (rc) return rc;
@@ -1133,6 +1252,7 @@ int32_t accept_impl(const void* target_logits, int64_t target_req_stride,
   p.V = vocab;
   p.c = greedy ? 0.f : kLog2e / temperature;
   p.greedy = greedy ? 1 : 0;
+  p.rpr = greedy ? k + 1 : 2 * k + 1;
   p.kv_indptr = kv_indptr;
   p.kv_indices = kv_indices;
   p.start_pos = start_pos;
@@ -1266,6 +1386,10 @@ extern "C" int32_t nsg_spec_accept_check_flags(void* workspace, int32_t* flags_h
   NSG_CHECK_HIP(hipMemcpyAsync(flags_h, workspace, sizeof(int32_t), hipMemcpyDeviceToHost, s));
   NSG_CHECK_HIP(hipStreamSynchronize(s));
   NSG_CHECK_HIP(hipMemsetAsync(workspace, 0, sizeof(int32_t), s));
+  if (*flags_h & 8) {   // a hand-off gave up: the counters may be left non-zero
+    NSG_CHECK_HIP(hipMemsetAsync(workspace, 0, kWorkspaceHeaderBytes, s));
+    NSG_CHECK_HIP(hipStreamSynchronize(s));
+  }
   clear_error();
   return NSG_OK;
 }

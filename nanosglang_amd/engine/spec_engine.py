@@ -207,6 +207,7 @@ class SpecEngine:
         self.max_batch = max_batch
         self._graphs: dict[int, _StepGraph] = {}
         self._accept_ws = kernels.AcceptWorkspace(self.device)
+        self._sample_ws = kernels.AcceptWorkspace(self.device)   # the sampler's own
         self._dummy_block = None
         self._tab = np.zeros((0, 0), np.int32)     # page-table mirror of graph mode
         # decode / verify contexts never exceed the position table: the
@@ -303,11 +304,12 @@ class SpecEngine:
         if self.k + 1 > self._max_pages() * self.P:
             raise ValueError("verify window exceeds the position range")
         V = c.vocab_size
-        # every accept call of every graph shares one workspace, sized once
-        need = max(kernels._lib().nsg_spec_accept_workspace_bytes(self.max_batch, self.k, V),
-                   kernels._lib().nsg_spec_accept_workspace_bytes(self.max_batch, 0, V),
-                   kernels._lib().nsg_sample_workspace_bytes(self.max_batch, V))
-        self._accept_ws.get(need)
+        # every accept call of every graph shares one workspace, every sampler
+        # call another, each sized once
+        lib = kernels._lib()
+        self._accept_ws.get(max(lib.nsg_spec_accept_workspace_bytes(self.max_batch, self.k, V),
+                                lib.nsg_spec_accept_workspace_bytes(self.max_batch, 0, V)))
+        self._sample_ws.get(lib.nsg_sample_workspace_bytes(self.max_batch, V))
         pool = torch.cuda.graph_pool_handle()
         for bs in graph_batch_sizes(self.max_batch):
             if bs in self._graphs:
@@ -348,7 +350,7 @@ class SpecEngine:
             u = None if g.ud is None else g.ud[i].view(bs, 1)
             if self.filtered:
                 kernels.sample(lg.view(bs, -1), self.temperature, self.top_k, self.top_p,
-                               u.view(bs), workspace=self._accept_ws, out=g.em1[:, 0])
+                               u.view(bs), workspace=self._sample_ws, out=g.em1[:, 0])
             else:
                 kernels.spec_accept(lg.view(bs, 1, -1), None, None, u, self.temperature,
                                     workspace=self._accept_ws, out=(g.n1, g.em1, g.rb1))
@@ -358,7 +360,7 @@ class SpecEngine:
         g.vids[:, 1:].copy_(g.drafts)
         tl = m.forward_packed(g.vids.view(-1), A["vpos"], pool, g.attn[k], A["vslot"])
         g.tl = tl        # allocated from the graph's pool: every replay rewrites it
-        bonus = self._bonus(tl.view(bs, k + 1, -1), g.u, workspace=self._accept_ws,
+        bonus = self._bonus(tl.view(bs, k + 1, -1), g.u, workspace=self._sample_ws,
                             out=g.bonus)
         kernels.spec_accept(tl.view(bs, k + 1, -1), g.dlog, g.drafts, g.u, self.temperature,
                             g.kvp[k], g.idx[k], A["start"], page_size=self.P,

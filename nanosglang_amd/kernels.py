@@ -330,8 +330,11 @@ class BatchPrefillWithPagedKVCacheWrapper:
 
 
 class AcceptWorkspace:
-    """Device scratch of :func:`spec_accept` (zero-filled once, grown on demand).
-    Calls that share one workspace must not overlap on different streams."""
+    """Device scratch of :func:`spec_accept` (zero-filled once, grown on
+    demand), or of :func:`sample` -- never both: the acceptance kernels pass
+    records between workgroups through slots that must read zero between
+    calls, and they leave them so.  Calls that share one workspace must not
+    overlap on different streams."""
 
     def __init__(self, device):
         self.device = torch.device(device)
@@ -346,13 +349,18 @@ class AcceptWorkspace:
     def check_flags(self) -> int:
         """Synchronises and returns (then clears) the acceptance kernels'
         error flags: bit 1, a rolled-back position past its request's pages;
-        bit 2, a draft token outside [0, vocab)."""
+        bit 2, a draft token outside [0, vocab); bit 3, a hand-off between
+        workgroups gave up waiting (the outputs of that call are undefined and
+        the whole workspace is zeroed again here)."""
         if self.buf.numel() == 0:
             return 0
         f = C.c_int32(0)
         check(_lib().nsg_spec_accept_check_flags(self.buf.data_ptr(), C.byref(f),
                                                  _stream_ptr(self.device)),
               "nsg_spec_accept_check_flags")
+        if f.value & 8:
+            self.buf.zero_()
+            torch.cuda.synchronize(self.device)
         return f.value
 
 
@@ -360,12 +368,13 @@ _default_ws: dict[tuple, AcceptWorkspace] = {}
 _default_ws_lock = threading.Lock()
 
 
-def _accept_ws(device) -> AcceptWorkspace:
-    """The default workspace of the current stream on ``device``: calls on one
-    stream run in order, so they may share it; calls on different streams (or
-    threads using different streams) get their own."""
+def _accept_ws(device, kind: str = "accept") -> AcceptWorkspace:
+    """The default ``kind`` ("accept" or "sample") workspace of the current
+    stream on ``device``: calls on one stream run in order, so they may share
+    it; calls on different streams (or threads using different streams) get
+    their own."""
     device = torch.device(device)
-    key = (device, _stream_ptr(device))
+    key = (device, _stream_ptr(device), kind)
     ws = _default_ws.get(key)
     if ws is None:
         with _default_ws_lock:
@@ -490,7 +499,7 @@ def sample(logits: torch.Tensor, temperature: float, top_k: int = 0, top_p: floa
         raise ValueError("out must be a contiguous int64 (R,) tensor")
     lib = _lib()
     need = lib.nsg_sample_workspace_bytes(R, V)
-    ws = (workspace or _accept_ws(dev)).get(need)
+    ws = (workspace or _accept_ws(dev, "sample")).get(need)
     check(lib.nsg_sample(logits.data_ptr(), logits.stride(0) if R > 1 else V, dt, R, V,
                          float(temperature), int(top_k), float(top_p),
                          _ptr(uniforms) if not greedy else None, 1, out.data_ptr(),

@@ -244,6 +244,8 @@ def test_greedy_large_shape_full_size_closed_form():
             drafts[b, prefix[b]] = (am[b, prefix[b]] + 1) % V
     n, em, rb = spec_accept(tl, None, _dev(drafts, torch.int64), None, 0.0)
     n, em = n.cpu().numpy(), em.cpu().numpy()
+    from nanosglang_amd.kernels import _accept_ws
+    assert _accept_ws("cuda").check_flags() == 0
     np.testing.assert_array_equal(n, prefix + 1)
     for b in range(B):
         j = prefix[b]
@@ -311,24 +313,58 @@ def test_stochastic_large_shape_full_size_oracle():
     _assert_stochastic(n, em, rb, ref)
 
 
-def test_sample_then_accept_on_one_workspace_keeps_flags_clear():
-    """A filtered draw (nsg_sample, top-k) and an acceptance call share one
-    workspace, as the engine's captured step does: the sampler leaves the
-    acceptance header alone, so the acceptance flags read back as zero."""
+def test_sampler_and_acceptance_interleaved_on_their_own_workspaces():
+    """The captured engine step interleaves filtered draws (nsg_sample) with
+    acceptance calls, each kind on its own workspace: the acceptance flags
+    read back as zero and every acceptance result equals a call on a fresh
+    workspace (the hand-off slots are left zero after every call)."""
     from nanosglang_amd.kernels import AcceptWorkspace, sample, spec_accept
     B, k, V = 8, 4, 20000
     a = workloads.acceptance_batch(batch=B, k=k, vocab=V, seed=25)
-    from nanosglang_amd import _native
-    lib = _native.load()
-    ws = AcceptWorkspace("cuda")
-    ws.get(max(lib.nsg_sample_workspace_bytes(B, V), lib.nsg_spec_accept_workspace_bytes(B, k, V)))
+    ws, sws = AcceptWorkspace("cuda"), AcceptWorkspace("cuda")
     t, d = _dev(a["target"], torch.bfloat16), _dev(a["draft"], torch.bfloat16)
     u = _dev(_uniforms(B, k, 25), torch.float32)
     dt = _dev(a["draft_tokens"], torch.int64)
-    for _ in range(2):
-        sample(t[:, 0], 0.8, top_k=50, top_p=0.9, uniforms=u[:, 0].contiguous(), workspace=ws)
-        spec_accept(t, d, dt, u, 0.8, workspace=ws)
+    fresh = [spec_accept(t, d, dt, u, 0.8, workspace=AcceptWorkspace("cuda")),
+             spec_accept(t, None, dt, None, 0.0, workspace=AcceptWorkspace("cuda"))]
+    for _ in range(3):
+        sample(t[:, 0], 0.8, top_k=50, top_p=0.9, uniforms=u[:, 0].contiguous(), workspace=sws)
+        got = [spec_accept(t, d, dt, u, 0.8, workspace=ws)]
+        sample(t[:, 0], 0.8, top_k=50, uniforms=u[:, 0].contiguous(), workspace=sws)
+        got.append(spec_accept(t, None, dt, None, 0.0, workspace=ws))
         assert ws.check_flags() == 0
-        sample(t[:, 0], 0.8, top_k=50, uniforms=u[:, 0].contiguous(), workspace=ws)
-        spec_accept(t, None, dt, None, 0.0, workspace=ws)
+        for g, f in zip(got, fresh):
+            for x, y in zip(g, f):
+                assert torch.equal(x, y)
+
+
+def test_one_workspace_across_shapes_and_modes_ends_zero():
+    """Acceptance calls of different batch, k, vocabulary and mode on one
+    workspace: each equals the same call on a fresh workspace, and after every
+    call the workspace (past the flag word) is all zero again -- the kernels'
+    hand-off slots must read zero at the start of any later call, whatever
+    layout the previous call used."""
+    from nanosglang_amd.kernels import AcceptWorkspace, spec_accept
+    ws = AcceptWorkspace("cuda")
+    cases = [(16, 8, 12288, 1.0), (32, 0, 3000, 0.7), (64, 4, 20000, 0.8), (8, 3, 3001, 0.9),
+             (32, 0, 3000, 0.7), (16, 8, 12288, 0.0), (64, 4, 20000, 0.0), (8, 3, 3001, 1.0)]
+    ws.get(max(_native_lib().nsg_spec_accept_workspace_bytes(B, k, V) for B, k, V, _ in cases))
+    for i, (B, k, V, T) in enumerate(cases):
+        a = workloads.acceptance_batch(batch=B, k=k, vocab=V, temperature=max(T, 0.5), seed=40 + i)
+        start, indptr, indices = _page_table(B, k, 40 + i)
+        args = (_dev(a["target"], torch.bfloat16), _dev(a["draft"], torch.bfloat16) if T else None,
+                _dev(a["draft_tokens"], torch.int64) if k else None,
+                _dev(_uniforms(B, k, 40 + i), torch.float32) if T else None, T,
+                _dev(indptr, torch.int32), _dev(indices, torch.int32), _dev(start, torch.int32))
+        got = spec_accept(*args, workspace=ws)
+        ref = spec_accept(*args, workspace=AcceptWorkspace("cuda"))
+        torch.cuda.synchronize()
+        for x, y in zip(got, ref):
+            assert torch.equal(x, y), (i, B, k, V, T)
         assert ws.check_flags() == 0
+        assert int((ws.buf.view(torch.int32)[1:] != 0).sum()) == 0, (i, B, k, V, T)
+
+
+def _native_lib():
+    from nanosglang_amd import _native
+    return _native.load()

@@ -179,19 +179,30 @@ __device__ __forceinline__ int64_t drow(const AccParams& p, int b, int i) {
   return (int64_t)b * p.d_req + (int64_t)i * p.d_row;
 }
 
-// Flat slot of rejected verify position start + n + i, lane i < k of one wave
-// (-1 past start + k, or past the request's pages, which also sets flag bit 1).
-__device__ void rollback_lanes(const AccParams& p, int b, int n, int lane) {
+// Rollback slots in two halves, so that the page-table loads leave the
+// finishing wave's critical path.  rollback_prefetch (lane i < k of one wave,
+// issued before the request's outcome is known): the flat slot of verify
+// position start + 1 + i, or -2 past the request's pages.  rollback_lanes,
+// once n tokens are emitted: lane i writes the slot of rejected position
+// start + n + i (-1 past start + k; past the pages -1 and flag bit 1).
+__device__ int64_t rollback_prefetch(const AccParams& p, int b, int lane) {
+  if (!p.rollback || lane >= p.k) return -1;
+  const int pos = p.start_pos[b] + 1 + lane;
+  const int pb = p.kv_indptr[b];
+  const int np = p.kv_indptr[b + 1] - pb;
+  const int pg = pos >> p.log2P;
+  if (pos < 0 || pg >= np) return -2;
+  return ((int64_t)p.kv_indices[pb + pg] << p.log2P) + (pos & ((1 << p.log2P) - 1));
+}
+__device__ void rollback_lanes(const AccParams& p, int b, int n, int lane, int64_t pre) {
+  const int src = min(63, max(0, n - 1 + lane));
+  const int64_t got = __shfl(pre, src, 64);   // every lane takes part
   if (!p.rollback || lane >= p.k) return;
   int64_t slot = -1;
-  const int pos = p.start_pos[b] + n + lane;
   if (n + lane <= p.k) {
-    const int pb = p.kv_indptr[b];
-    const int np = p.kv_indptr[b + 1] - pb;
-    const int pg = pos >> p.log2P;
-    if (pos >= 0 && pg < np) {
-      slot = ((int64_t)p.kv_indices[pb + pg] << p.log2P) + (pos & ((1 << p.log2P) - 1));
-    } else {
+    slot = got;
+    if (slot == -2) {
+      slot = -1;
       atomicOr(p.flags, 2);
     }
   }
@@ -478,7 +489,7 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(AccParams p) {
 // Greedy: one wave combines the argmax chunk records of request b's k+1
 // target rows (all loaded at once), compares them with the drafts and writes
 // every output; then it clears the records.
-__device__ void greedy_finalize(const AccParams& p, int b) {
+__device__ void greedy_finalize(const AccParams& p, int b, int64_t pre) {
   const int lane = threadIdx.x & 63;
   const int k = p.k;
   const int n = (k + 1) * p.nch;
@@ -498,7 +509,7 @@ __device__ void greedy_finalize(const AccParams& p, int b) {
   int64_t* em = p.emitted + (int64_t)b * (k + 1);
   if (lane <= k) em[lane] = lane < j ? x : (lane == j ? (int64_t)ix : -1);
   if (lane == 0) p.n_out[b] = j + 1;
-  rollback_lanes(p, b, j + 1, lane);
+  rollback_lanes(p, b, j + 1, lane, pre);
   clear_slots(recs, n);
 }
 
@@ -509,8 +520,10 @@ template <typename T>
 __global__ __launch_bounds__(kThreads) void greedy_fused_kernel(AccParams p) {
   const int b = blockIdx.y / p.rpr;
   const int lr = blockIdx.y - b * p.rpr;
+  const bool last = lr == p.k && (int)blockIdx.x == p.nch - 1 && threadIdx.x < 64;
+  const int64_t pre = last ? rollback_prefetch(p, b, threadIdx.x) : -1;  // under the stream
   row_chunk_stats<T, true>(p, b, lr, blockIdx.x);
-  if (lr == p.k && (int)blockIdx.x == p.nch - 1 && threadIdx.x < 64) greedy_finalize(p, b);
+  if (last) greedy_finalize(p, b, pre);
 }
 
 struct Decision {
@@ -574,7 +587,7 @@ __device__ __forceinline__ Decision decision_of(const AccParams& p, int b) {
 // writes the accepted prefix, num_emitted, the rollback slots and the caller's
 // bonus (all accepted), publishes the decision and clears the records.
 template <typename T>
-__device__ Decision decide(const AccParams& p, int b) {
+__device__ Decision decide(const AccParams& p, int b, int64_t pre) {
   const int lane = threadIdx.x & 63;
   const int k = p.k;
   const int rpr = 2 * k + 1;
@@ -630,7 +643,7 @@ __device__ Decision decide(const AccParams& p, int b) {
     p.n_out[b] = j + 1;
     if (d.mode == 1 && p.bonus) em[k] = p.bonus[b];  // all accepted: the caller's bonus
   }
-  rollback_lanes(p, b, j + 1, lane);
+  rollback_lanes(p, b, j + 1, lane, pre);
   publish_decision(p, b, d, lane);
   clear_slots(recs, n);
   return d;
@@ -665,7 +678,7 @@ __device__ float block_incl_scan(float x, float* sh) {
 // One wave per request: the decision, the accepted prefix, counts and slots.
 template <typename T>
 __global__ __launch_bounds__(64) void decide_kernel(AccParams p) {
-  decide<T>(p, blockIdx.x);
+  decide<T>(p, blockIdx.x, rollback_prefetch(p, blockIdx.x, threadIdx.x));
 }
 
 // Chunk sums of the decided weights (residual of row j, or target row j).
@@ -1080,8 +1093,10 @@ __global__ __launch_bounds__(kThreads) void stoch_fused_kernel(AccParams p) {
     const int b = t / per_req;
     const int sub = t - b * per_req;
     const int lr = sub / p.nch;
+    const bool last = sub == per_req - 1 && wave == 0;       // request b's last chunk
+    const int64_t pre = last ? rollback_prefetch(p, b, lane) : -1;   // under the stream
     row_chunk_stats<T, false>(p, b, lr, sub - lr * p.nch);
-    if (sub == per_req - 1 && wave == 0) decide<T>(p, b);   // request b's last chunk
+    if (last) decide<T>(p, b, pre);
     return;
   }
   const int b = (t - p.B * per_req) / kRsSplits;  // then the range blocks, request by request

@@ -3,8 +3,10 @@
     python -m nanosglang_amd.build
 
 compiles every ``csrc/*.hip`` for gfx950 with hipcc and links them into
-``nanosglang_amd/libnsg_spec.so``.  Packed-fp32 instructions are disabled on
-purpose (``-target-feature -packed-fp32-ops``).
+``nanosglang_amd/libnsg_spec.so`` (the C ABI), then ``csrc/torch_ops.cpp``
+into ``nanosglang_amd/libnsg_torch.so`` (the torch operators over it).
+Packed-fp32 instructions are disabled on purpose
+(``-target-feature -packed-fp32-ops``).
 """
 
 from __future__ import annotations
@@ -53,6 +55,36 @@ def _compile(src: str, obj: str) -> None:
         print(err, file=sys.stderr)
 
 
+TORCH_OPS_SRC = os.path.join(CSRC, "torch_ops.cpp")
+TORCH_OPS_LIB = os.path.join(PKG, "libnsg_torch.so")
+
+
+def build_torch_ops(verbose: bool = True) -> str:
+    """The torch operators (csrc/torch_ops.cpp: TORCH_LIBRARY over the C ABI)
+    as libnsg_torch.so, host C++ against the installed PyTorch-ROCm, linked to
+    libnsg_spec.so beside it."""
+    import torch
+    from torch.utils import cpp_extension
+    torch_lib = os.path.join(os.path.dirname(torch.__file__), "lib")
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    cxx = os.environ.get("CXX", shutil.which("g++") or "c++")
+    tmp = TORCH_OPS_LIB + ".tmp"
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wno-unused-function",
+           f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+           *[f"-I{d}" for d in cpp_extension.include_paths()], f"-I{rocm}/include",
+           TORCH_OPS_SRC, "-o", tmp, f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch",
+           "-ltorch_cpu", "-ltorch_hip", f"-L{PKG}", "-lnsg_spec", "-Wl,-rpath,$ORIGIN",
+           f"-Wl,-rpath,{torch_lib}"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"torch operator library failed to build:\n{r.stderr}")
+    os.replace(tmp, TORCH_OPS_LIB)
+    if verbose:
+        print(f"built {TORCH_OPS_LIB}")
+    return TORCH_OPS_LIB
+
+
 def build(verbose: bool = True) -> str:
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     objdir = os.path.join(PKG, "_build")
@@ -68,6 +100,7 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+    build_torch_ops(verbose)
     return LIB
 
 

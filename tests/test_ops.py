@@ -115,3 +115,15 @@ def test_device_operators_reject_host_tensors_before_any_gpu_call():
                                   torch.zeros(2, 4, dtype=torch.int64), None, 0.0)
     with pytest.raises(ValueError):
         ops.plan_from_record(torch.zeros(3, dtype=torch.int32))
+
+
+def test_operators_come_from_the_compiled_library():
+    """torch.ops.nsg.* are the C++ TORCH_LIBRARY registrations of
+    libnsg_torch.so (CUDA and CPU kernels), not Python custom ops."""
+    import os
+    maps = open(f"/proc/{os.getpid()}/maps").read()
+    assert ops.LIB_PATH in maps or os.path.realpath(ops.LIB_PATH) in maps
+    for name in ("verify_attention", "verify_attention_plan", "verify_attention_run",
+                 "spec_accept", "sample", "kv_write", "rope_kv_write"):
+        for key in ("CUDA", "CPU"):
+            assert torch._C._dispatch_has_kernel_for_dispatch_key(f"nsg::{name}", key), (name, key)

@@ -118,9 +118,12 @@ int64_t nsg_attn_workspace_bytes(const nsg_attn_plan_t* plan);
 
 /* Runs one layer (replaces wrapper.run, causal_lm.py:340).
  * q/out: [total_q, Hq, D] bf16; k_cache/v_cache: [num_pages, P, Hkv, D] bf16;
- * work_d: device copy of the planner's work list.  Page ids outside
- * [0, num_pages) read as zeros and raise a flag returned by
- * nsg_attn_check_flags. */
+ * work_d: device copy of the planner's work list.  sm_scale must be
+ * positive (the kernel scales each row's maximum raw score).  Page ids
+ * outside [0, num_pages) read other rows of the pool (the outputs of their
+ * rows are undefined) and raise a flag returned by nsg_attn_check_flags.
+ * page_size must be the plan's (plans with several KV groups need pages of
+ * 16+ tokens: the planner picks one group for smaller pages). */
 int32_t nsg_attn_run(const nsg_attn_plan_t* plan, const int32_t* work_d,
                      const void* q, const void* k_cache, const void* v_cache, void* out,
                      const int32_t* qo_indptr, const int32_t* kv_indptr,

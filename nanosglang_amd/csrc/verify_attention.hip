@@ -30,6 +30,7 @@
 //     from the LDS tile in the same token order;
 //   - the prefetched registers go to the other LDS buffer; one barrier.
 #include <algorithm>
+#include <type_traits>
 #include <cstdarg>
 #include <vector>
 
@@ -105,6 +106,57 @@ __device__ __forceinline__ void wait_steps(int later) {
   }
 }
 
+// Max / sum over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four lane groups
+// holding one query row) with gfx950's row swaps, which stay in the VALU:
+// v_permlane32_swap with both operands x leaves lane l holding x[l % 32] in
+// the first result and x[l % 32 + 32] in the second, v_permlane16_swap the
+// same for the even and odd 16-lane rows.  Sums pair the same two lanes in
+// both halves, so every lane ends with the same value.
+__device__ __forceinline__ float max_xor16_32(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_xor16_32(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Eight transposing LDS reads (V^T fragments of four d tiles) and the wait
+// for them, as one asm block.  Written through the builtin, every such read
+// after a global_load_lds gets a conservative vmcnt(0) from the compiler (it
+// cannot tell the read from the ring slots still being filled), which stalls
+// each step until every copy in flight has landed; the ring's own waits
+// (vmcnt per step plus the barrier) already order these reads.
+__device__ __forceinline__ void ds_read_tr8(v4i16 (&r)[8], const uint32_t (&a)[8]) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %8\n\t"
+      "ds_read_b64_tr_b16 %1, %9\n\t"
+      "ds_read_b64_tr_b16 %2, %10\n\t"
+      "ds_read_b64_tr_b16 %3, %11\n\t"
+      "ds_read_b64_tr_b16 %4, %12\n\t"
+      "ds_read_b64_tr_b16 %5, %13\n\t"
+      "ds_read_b64_tr_b16 %6, %14\n\t"
+      "ds_read_b64_tr_b16 %7, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]),
+        "=&v"(r[6]), "=&v"(r[7])
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7])
+      : "memory");
+}
+
+// 32-bit LDS address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 // LDS tile swizzles: 16-byte chunk c of token row t is stored at physical
 // chunk c ^ swz(t).  K fragments read one logical chunk of 16 consecutive
 // tokens (needs distinct banks across t).  A V^T transposing read takes one
@@ -125,17 +177,25 @@ __device__ __forceinline__ int swz_v(int t) {
 
 constexpr float kLazyRescale = 8.f;  // rescale O only when a row max grows by > 2^8
 
-// LDS ring depth (steps in flight: depth - 1).  With several KV groups a
-// workgroup fills the CU's LDS anyway; with one, a shallower ring lets more
-// workgroups (waves) share a CU, which hides more latency (measured: depth 3
-// beats 4 by ~8 % on the large shape).
+// LDS ring depth.  With one KV group a shallower ring lets more workgroups
+// (waves) share a CU, which hides more latency (measured: depth 3 beats 4 by
+// ~8 % on the large shape); depth - 1 steps are in flight ahead of the math.
+// With several KV groups (latency regime) the rings take all 160 KB of the
+// CU's LDS, 5 slots per group, and a group issues all of its first 5 steps
+// at once: up to 5 * 32 tokens per group, i.e. 640 tokens of an item at head
+// dim 64, arrive in one memory round trip (a 4-deep ring with 3 steps ahead
+// needed a second round trip, ~2 us, for items past 384 tokens).
 constexpr int kRingOne = 3;
-constexpr int kRingGroups = 4;
+constexpr int kRingGroups = 5;
 constexpr int ring_depth(int KS) { return KS == 1 ? kRingOne : kRingGroups; }
-// KV groups per workgroup in the latency regime: as many 4-deep rings as
-// fit 128 KB of LDS (8 KB per step at head_dim 64, 16 KB at 128).
+// KV groups per workgroup in the latency regime: as many 5-deep rings as fit
+// 160 KB of LDS (8 KB per step at head_dim 64, 16 KB at 128).
 constexpr int kv_groups_max(int D) { return D == 64 ? 4 : 2; }
+constexpr int kLdsBytes = 160 * 1024;
 constexpr int kMaxItemPages = 1024; // page ids one work item may span
+// Pages of at least 16 tokens for several KV groups: a 32-token step then
+// spans at most two pages, looked up with two scalar loads.
+constexpr int kMinGroupPage = 16;
 
 // One workgroup = one work item x one KV head.  Its KS * RT waves form KS
 // groups of RT; group g takes the g-th contiguous share of the item's 32-token
@@ -144,13 +204,17 @@ constexpr int kMaxItemPages = 1024; // page ids one work item may span
 // verify and draft steps of a decode batch): the groups run side by side and
 // their partial results meet in LDS, so the item needs neither a second
 // launch nor more sequential steps per wave.
-// The item's page ids are staged in LDS once.  K and V rows of each step go
+// With one KV group the item's page ids are staged in LDS once; with
+// several the rings fill the LDS, and each DMA instruction's page id (one
+// page per instruction: its token rows are 8 (head dim 64) or 4 (128)
+// consecutive tokens of a 32-aligned step) is a wave-uniform scalar load,
+// issued for all first steps before any copy.  K and V rows of each step go
 // straight from HBM to a ring slot of the group with global_load_lds_dwordx4
-// (no staging registers), ring_depth - 1 steps ahead of the math; an explicit
-// vmcnt wait per step (plus a raw s_barrier when a group has several waves)
-// keeps the ring full (__syncthreads would drain it).  Every group iterates
-// the same number of steps (idle ones do nothing but the barrier), so the
-// workgroup-wide barrier stays matched.
+// (no staging registers) ahead of the math; an explicit vmcnt wait per step
+// (plus a raw s_barrier when a group has several waves) keeps the ring full
+// (__syncthreads would drain it).  Every group iterates the same number of
+// steps (idle ones do nothing but the barrier), so the workgroup-wide barrier
+// stays matched.
 template <int D, int RT, int KS>
 __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p) {
   constexpr int KC = D / 32;              // K-dim chunks of QK^T
@@ -170,8 +234,15 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
   // groups) -- but the default policy for the four groups of head dim 64,
   // where non-temporal measured 9.8 -> 10.7 us at the verify shape.
   constexpr int kDmaPolicy = KS <= 2 ? 2 : 0;  // 2: the nt bit
-  __shared__ __attribute__((aligned(16))) bf16 ring[KS][kNBuf][2][TILE];
-  __shared__ int s_pages[kMaxItemPages];
+  // steps issued before the first wait: all ring slots with several groups,
+  // all but one with one group (that slot is filled at the first iteration)
+  constexpr int PF = KS > 1 ? kNBuf : kNBuf - 1;
+  constexpr int kRingBytes = KS * kNBuf * 2 * TILE * 2;
+  constexpr int kPageBytes = KS == 1 ? kMaxItemPages * 4 : 0;
+  static_assert(kRingBytes + kPageBytes <= kLdsBytes, "LDS budget");
+  __shared__ __attribute__((aligned(16))) unsigned char smem[kRingBytes + kPageBytes];
+  auto ring = reinterpret_cast<bf16 (*)[kNBuf][2][TILE]>(smem);
+  int* s_pages = reinterpret_cast<int*>(smem + kRingBytes);  // one KV group only
 
   // blockIdx.x = KV head (fastest), so the Hkv workgroups of one work item
   // are dispatched together and read the interleaved head slices of the same
@@ -197,10 +268,18 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
   const int r16 = lane & 15;
   const int g4 = lane >> 4;
 
-  // ---- stage the item's page ids in LDS ----
+  // ---- one KV group: stage the item's page ids in LDS ----
   const int page0 = kvb >> p.log2P;
   const int npages = kve > kvb ? ((kve - 1) >> p.log2P) - page0 + 1 : 0;
-  for (int i = tid; i < npages; i += NTHR) s_pages[i] = p.kv_indices[pb + page0 + i];
+  if constexpr (KS == 1)
+    for (int i = tid; i < npages; i += NTHR) s_pages[i] = p.kv_indices[pb + page0 + i];
+
+  // ---- this group's share of the item's 32-token steps ----
+  const int n_all = (kve - kvb + kTokIt - 1) / kTokIt;  // steps of the item
+  const int per = (n_all + KS - 1) / KS;                // steps per group (loop count)
+  const int n_it = max(0, min(per, n_all - grp * per)); // this group's real steps
+  const int gkvb = kvb + grp * per * kTokIt;            // this group's first token
+  const int last_tok = kve - 1;
 
   // ---- this lane's query row (B operand of S^T = K Q^T) and causal limit ----
   const int row = wave * 16 + r16;
@@ -210,13 +289,28 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
   const int lim = row_ok ? lim0 + (p.causal ? tau : 0) : -1;
   bf16x8 qf[KC];
   {
-    const bf16* qrow = p.q + ((size_t)(qs + tau) * p.Hq + h * G + gam) * D;
+    // (padding rows load the tile's first row -- real data, their scores are
+    // all masked: lim = -1 -- so that every lane loads unconditionally)
+    const bf16* qrow = p.q + (row_ok ? ((size_t)(qs + tau) * p.Hq + h * G + gam) * D
+                                     : ((size_t)qs * p.Hq + h * G) * D);
 #pragma unroll
-    for (int c = 0; c < KC; ++c)
-      qf[c] = row_ok ? load_bf16x8(qrow + 32 * c + 8 * g4)
-                     : __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+    for (int c = 0; c < KC; ++c) qf[c] = load_bf16x8(qrow + 32 * c + 8 * g4);
   }
-  __syncthreads();  // page ids visible; nothing is in flight yet besides Q
+  // Several KV groups: the page ids of the group's first 64 pages, one per
+  // lane (lookups past the item's range read its last page), in one vector
+  // load beside Q's; the copies take them with v_readlane.
+  const int gpage0 = min(gkvb, last_tok) >> p.log2P;
+  int vpages = 0;
+  if constexpr (KS > 1) vpages = p.kv_indices[pb + min(gpage0 + lane, last_tok >> p.log2P)];
+  // Q must have landed before the first copy is issued, and the compiler
+  // must see it: an empty asm statement that reads Q makes it wait here (Q and
+  // the page ids arrive in the same round trip).  Left to itself it keeps Q
+  // pending and, since the copies issued after Q vary by path, waits for
+  // every copy in flight (vmcnt 0) before each step's first MFMA -- which
+  // turned the ring into one memory round trip per step.
+#pragma unroll
+  for (int c = 0; c < KC; ++c) asm volatile("" ::"v"(__builtin_bit_cast(u32x4, qf[c])));
+  if constexpr (KS == 1) __syncthreads();  // page ids visible; nothing is in flight besides Q
 
   floatx4 oacc[DT];
 #pragma unroll
@@ -225,14 +319,12 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
 
   const size_t head_off = (size_t)h * D;
   const size_t tok_stride = (size_t)p.Hkv * D;
-  const int n_all = (kve - kvb + kTokIt - 1) / kTokIt;  // steps of the item
-  const int per = (n_all + KS - 1) / KS;                // steps per group (loop count)
-  const int n_it = max(0, min(per, n_all - grp * per)); // this group's real steps
-  const int gkvb = kvb + grp * per * kTokIt;            // this group's first token
   bool bad_page = false;
   // Dummy source for lanes past the item's end or with a bad page id: the
   // item's first token row (real, finite data); its value is masked out.
-  const int pg_first = npages > 0 ? s_pages[0] : 0;
+  // (one KV group only; with several, lanes past the end copy the item's
+  // last token row instead -- see issue_pages)
+  const int pg_first = KS == 1 && npages > 0 ? s_pages[0] : 0;
   const bf16* dummy_k = p.kc + ((size_t)((unsigned)pg_first < (unsigned)p.num_pages ? pg_first : 0) * P +
                                 (kvb & (P - 1))) * tok_stride + head_off;
   const bf16* dummy_v = p.vc + (dummy_k - p.kc);
@@ -292,7 +384,62 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
     d_inpage[i] = (int64_t)(d_t[i] & (P - 1)) * (int64_t)tok_stride + (int64_t)head_off + d_off[i];
   }
   const int64_t page_elems = (int64_t)P * (int64_t)tok_stride;
-  // Issue this wave's DMA instructions for step `it` into ring slot `slot`.
+  // Several KV groups (pages of 16+ tokens, which the planner requires for
+  // them): a 32-token step spans at most two pages, the pages of its first
+  // and second 16 tokens (equal for pages of 32+).  Past the group's first 64
+  // pages (items over 4096 tokens at head dim 64, 2048 at 128: long
+  // fixed-bound plans only) a wave-uniform scalar load reads them.
+  auto page_at = [&](int t) {
+    const int pg = min(t, last_tok) >> p.log2P;
+    const int idx = pg - gpage0;
+    if (idx < 64) return __builtin_amdgcn_readlane(vpages, idx);
+    // an explicit scalar load: as a plain load the compiler would hoist it
+    // above the branch and wait for it on every refill
+    // (the address through readfirstlane: uniform by construction, which an
+    // "s" operand needs even where the compiler cannot prove it)
+    const uint64_t a = reinterpret_cast<uint64_t>(p.kv_indices + pb + pg);
+    const uint64_t au = (uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)a) |
+                        ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32);
+    int v;
+    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(au) : "memory");
+    return v;
+  };
+  // ... and the copies themselves, given those page ids.  The page part of
+  // each address is wave-uniform (scalar arithmetic, once per step); a lane
+  // adds its fixed byte offset inside the step (row d_t & (P - 1) of its page:
+  // the step starts at a multiple of 32, so rows 16..31 fall on the second
+  // page exactly when pages hold 16 tokens).  A lane past the item's end
+  // copies the step's first row instead: real, finite data, masked out (a
+  // P = 0 weight on a non-finite V row would still give NaN).  A bad page id
+  // copies from the pool's first page and raises the flag.
+  uint32_t lo_row[NI], lo_end[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    lo_row[i] = (uint32_t)((((size_t)(d_t[i] & (P - 1))) * tok_stride + head_off + d_off[i]) * 2);
+    lo_end[i] = (uint32_t)((head_off + d_off[i]) * 2);
+  }
+  const uint64_t page_bytes = (uint64_t)P * tok_stride * 2;
+  auto issue_pages = [&](int it, int slot, int pga, int pgb) {
+    const int t0 = gkvb + it * kTokIt;
+    const bool oka = (unsigned)pga < (unsigned)p.num_pages;
+    const bool okb = (unsigned)pgb < (unsigned)p.num_pages;
+    bad_page |= !oka || !okb;  // both ids are of tokens in the range
+    const uint32_t rowb = (uint32_t)(t0 & (P - 1)) * (uint32_t)(tok_stride * 2);  // < one page
+    const uint64_t offa = oka ? (uint64_t)(uint32_t)pga * page_bytes : 0;
+    const uint64_t offb = okb ? (uint64_t)(uint32_t)pgb * page_bytes : 0;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const char* base = reinterpret_cast<const char*>(d_v[i] ? p.vc : p.kc);
+      const bool in = t0 + d_t[i] <= last_tok;
+      const char* src =
+          base + ((in && d_t[i] >= 16) ? offb : offa) + ((in ? lo_row[i] : lo_end[i]) + rowb);
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+                                       static_cast<void*>(&ring[grp][slot][0][0] + d_lds[i]), 16,
+                                       0, kDmaPolicy);
+    }
+  };
+  // One KV group: issue this wave's DMA instructions for step `it` into ring
+  // slot `slot`, page ids from LDS.
   auto issue = [&](int it, int slot) {
     const int t0 = gkvb + it * kTokIt;
     const bool full = t0 + kTokIt <= kve;  // no token of the step past the range
@@ -334,9 +481,26 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
     }
   };
 
+  if constexpr (KS > 1) {
+    // the first PF steps lie within the first 64 pages (PF * 32 tokens in
+    // pages of 16+)
+    static_assert(PF * kTokIt / kMinGroupPage <= 64, "prefetched steps within the lane pages");
+    // (all ids read before any copy: one wait for the page-id load on every path)
+    int pga[PF], pgb[PF];
 #pragma unroll
-  for (int it = 0; it < kNBuf - 1; ++it)
-    if (it < n_it) issue(it, it);
+    for (int it = 0; it < PF; ++it) {
+      const int t0 = gkvb + it * kTokIt;
+      pga[it] = __builtin_amdgcn_readlane(vpages, (min(t0, last_tok) >> p.log2P) - gpage0);
+      pgb[it] = __builtin_amdgcn_readlane(vpages, (min(t0 + 16, last_tok) >> p.log2P) - gpage0);
+    }
+#pragma unroll
+    for (int it = 0; it < PF; ++it)
+      if (it < n_it) issue_pages(it, it, pga[it], pgb[it]);
+  } else {
+#pragma unroll
+    for (int it = 0; it < PF; ++it)
+      if (it < n_it) issue(it, it);
+  }
 
   for (int it0 = 0; it0 < per; it0 += kNBuf) {
 #pragma unroll
@@ -345,8 +509,9 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
       if (it >= per) break;
       const bool real = it < n_it;
       if (real) {
-        // steps issued after `it` by this wave: min(kNBuf - 2, n_it - 1 - it)
-        wait_steps<NI, kNBuf - 2>(min(kNBuf - 2, n_it - 1 - it));
+        // steps issued so far: min(n_it, max(PF, it + kNBuf - 1)); wait
+        // until at most those after `it` are in flight
+        wait_steps<NI, PF - 1>(min(n_it, max(PF, it + kNBuf - 1)) - 1 - it);
       }
       if constexpr (RT > 1) {
         // step `it` landed for every wave of the group and slot (it - 1) is
@@ -357,7 +522,15 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
       }
-      if (it + kNBuf - 1 < n_it) issue(it + kNBuf - 1, (slot + kNBuf - 1) % kNBuf);
+      // refill the slot consumed at iteration it - 1 (free after the barrier)
+      if (it + kNBuf - 1 >= PF && it + kNBuf - 1 < n_it) {
+        if constexpr (KS > 1) {
+          const int t0 = gkvb + (it + kNBuf - 1) * kTokIt;
+          issue_pages(it + kNBuf - 1, (slot + kNBuf - 1) % kNBuf, page_at(t0), page_at(t0 + 16));
+        } else {
+          issue(it + kNBuf - 1, (slot + kNBuf - 1) % kNBuf);
+        }
+      }
       if (!real) continue;
 
       const int t0 = gkvb + it * kTokIt;
@@ -377,103 +550,126 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
         sacc[s2] = acc;
       }
 
-      // ---- online softmax (base 2) with lazy rescaling ----
-      float sv[8];
-      if (t0 + kTokIt - 1 <= lim0 && t0 + kTokIt <= kve) {
-        // every row of the tile sees every token of the step (lim0 is the
-        // tile's smallest causal limit): no mask
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sv[4 * s2 + i] = sacc[s2][i] * p.scale_log2;
-      } else {
+      // ---- online softmax (base 2) with lazy rescaling.  The max is taken
+      //      over the raw scores and scaled once (the scale is positive); the
+      //      scale folds into the exponent's FMA.  Masked scores get P = 0
+      //      outright, and a row with nothing visible leaves its max alone
+      //      (an FMA of a sentinel against a rounded sentinel max could give
+      //      exp2 of a huge residue) ----
+      float pv[8];
+      auto softmax = [&](auto masked) {
+        constexpr bool MASKED = decltype(masked)::value;
+        float sv[8];
+        bool vis[8];
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int j = t0 + 16 * s2 + 4 * g4 + i;
-            sv[4 * s2 + i] = (j <= lim && j < kve) ? sacc[s2][i] * p.scale_log2 : kMaskVal;
+            vis[4 * s2 + i] = !MASKED || (j <= lim && j < kve);
+            sv[4 * s2 + i] = vis[4 * s2 + i] ? sacc[s2][i] : kMaskVal;
           }
         }
-      }
-      float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                       fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      // Raise the exponent base only when a row max exceeds it by > 2^8, and
-      // skip the O rescale entirely when no row of the wave needs it.
-      const bool grow = mx > m_run + kLazyRescale;
-      if (__builtin_amdgcn_ballot_w64(grow)) {
-        const float mnew = grow ? mx : m_run;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);
-        m_run = mnew;
-        l_run *= alpha;
+        float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                         fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+        mx = max_xor16_32(mx);
+        mx = (MASKED && mx == kMaskVal) ? kMaskVal : mx * p.scale_log2;
+        // Raise the exponent base only when a row max exceeds it by > 2^8, and
+        // skip the O rescale entirely when no row of the wave needs it.
+        const bool grow = mx > m_run + kLazyRescale;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+          const float mnew = grow ? mx : m_run;
+          const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);
+          m_run = mnew;
+          l_run *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
-      }
-      float pv[8];
-      float ps = 0.f;
+          for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+        }
+        float ps = 0.f;
 #pragma unroll
-      for (int x = 0; x < 8; ++x) {
-        pv[x] = __builtin_amdgcn_exp2f(sv[x] - m_run);
-        ps += pv[x];
+        for (int x = 0; x < 8; ++x) {
+          const float e = __builtin_amdgcn_exp2f(fmaf(sv[x], p.scale_log2, -m_run));
+          pv[x] = MASKED && !vis[x] ? 0.f : e;
+          ps += pv[x];
+        }
+        l_run += ps;
+      };
+      if (t0 + kTokIt - 1 <= lim0 && t0 + kTokIt <= kve) {
+        // every row of the tile sees every token of the step (lim0 is the
+        // tile's smallest causal limit): no mask
+        softmax(std::false_type{});
+      } else {
+        softmax(std::true_type{});
       }
-      l_run += ps;
       const bf16x8 pf = __builtin_bit_cast(
           bf16x8, u32x4{cvt_pk_bf16(pv[0], pv[1]), cvt_pk_bf16(pv[2], pv[3]),
                         cvt_pk_bf16(pv[4], pv[5]), cvt_pk_bf16(pv[6], pv[7])});
 
       // ---- O^T += V^T P^T; element e of lane group g4 is token
       //      4*g4 + e (e < 4) or 16 + 4*g4 + (e - 4), matching pf ----
+      static_assert(DT % 4 == 0, "V^T fragments come in groups of four d tiles");
+      const uint32_t vbase = lds_addr(Vt);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        // (C-style casts: the only way to name the LDS address space here)
-        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) v4i16*)(Vt + vtr[dt][0]));
-        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) v4i16*)(Vt + vtr[dt][1]));
-        const v8i16 w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w), pf,
-                                                           oacc[dt], 0, 0, 0);
+      for (int d4 = 0; d4 < DT; d4 += 4) {
+        uint32_t a[8];
+        v4i16 r[8];
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          a[2 * x] = vbase + 2 * vtr[d4 + x][0];
+          a[2 * x + 1] = vbase + 2 * vtr[d4 + x][1];
+        }
+        ds_read_tr8(r, a);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          const v8i16 w = __builtin_shufflevector(r[2 * x], r[2 * x + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+          oacc[d4 + x] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w), pf,
+                                                                 oacc[d4 + x], 0, 0, 0);
+        }
       }
     }
   }
 
   if (bad_page) atomicOr(p.flags, 1);
   // ---- the 4 lane groups sharing query row r16 hold partial sums ----
-  float l = l_run;
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
+  float l = sum_xor16_32(l_run);
+  // d tiles this wave finishes: all of them with one KV group; with several,
+  // group g finishes the tiles dt = g (mod KS) of its rows, so every wave
+  // shares the combine and the output stores
+  auto own = [&](int dt) { return KS == 1 || dt % KS == grp; };
   if constexpr (KS > 1) {
     // ---- combine the KV groups through LDS (the rings are idle: every
     //      group's last real step waited for all of its copies) ----
     constexpr int SROW = D + 4;  // O[D], m, l, 2 pad
-    float* sc = reinterpret_cast<float*>(&ring[0][0][0][0]);
-    static_assert((size_t)KS * ROWS * SROW * 4 <= sizeof(ring), "combine scratch fits the rings");
+    float* sc = reinterpret_cast<float*>(smem);
+    static_assert((size_t)KS * ROWS * SROW * 4 <= (size_t)kRingBytes,
+                  "combine scratch fits the rings");
     __syncthreads();
     float* mine = sc + ((size_t)grp * ROWS + row) * SROW;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<floatx4*>(mine + dt * 16 + 4 * g4) = oacc[dt];
+    for (int dt = 0; dt < DT; ++dt)
+      if (!own(dt)) *reinterpret_cast<floatx4*>(mine + dt * 16 + 4 * g4) = oacc[dt];
     if (g4 == 0) {
       mine[D] = m_run;
       mine[D + 1] = l;
     }
     __syncthreads();
-    if (grp != 0) return;
     float M = kMaskVal;
 #pragma unroll
     for (int g = 0; g < KS; ++g) M = fmaxf(M, sc[((size_t)g * ROWS + row) * SROW + D]);
-    l = 0.f;
+    const float wself = __builtin_amdgcn_exp2f(m_run - M);
+    l *= wself;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) oacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < DT; ++dt)
+      if (own(dt)) oacc[dt] *= wself;
 #pragma unroll
     for (int g = 0; g < KS; ++g) {
+      if (g == grp) continue;
       const float* o = sc + ((size_t)g * ROWS + row) * SROW;
       const float wgt = __builtin_amdgcn_exp2f(o[D] - M);
       l += wgt * o[D + 1];
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
-        oacc[dt] += wgt * *reinterpret_cast<const floatx4*>(o + dt * 16 + 4 * g4);
+        if (own(dt)) oacc[dt] += wgt * *reinterpret_cast<const floatx4*>(o + dt * 16 + 4 * g4);
     }
     m_run = M;
   }
@@ -483,6 +679,7 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
     bf16* orow = p.out + ((size_t)(qs + tau) * p.Hq + h * G + gam) * D + 4 * g4;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
+      if (!own(dt)) continue;
       const floatx4 o = oacc[dt];
       *reinterpret_cast<u32x2*>(orow + dt * 16) =
           u32x2{cvt_pk_bf16(o[0] * inv, o[1] * inv), cvt_pk_bf16(o[2] * inv, o[3] * inv)};
@@ -490,8 +687,9 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
   } else {
     float* prow = p.partials + ((size_t)wi * p.Hkv + h) * ROWS * PSTRIDE + (size_t)row * PSTRIDE;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<floatx4*>(prow + dt * 16 + 4 * g4) = oacc[dt];
-    if (g4 == 0) {
+    for (int dt = 0; dt < DT; ++dt)
+      if (own(dt)) *reinterpret_cast<floatx4*>(prow + dt * 16 + 4 * g4) = oacc[dt];
+    if (g4 == 0 && grp == 0) {
       prow[D] = m_run;
       prow[D + 1] = l;
     }
@@ -714,8 +912,9 @@ int32_t plan_impl(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
   // fixed_capacity).  A split is at least kMinSplitSteps steps per group: its
   // partial rows cost about as much traffic as one step of K and V.
   const long long t1 = target_items(1, num_cus, num_kv_heads);
-  const bool latency = fixed_work >= 0 ? fixed_kv_len > 0
-                                       : (total_it + t1 - 1) / t1 <= kMinSplitSteps;
+  const bool latency = page_size >= kMinGroupPage &&
+                       (fixed_work >= 0 ? fixed_kv_len > 0
+                                        : (total_it + t1 - 1) / t1 <= kMinSplitSteps);
   const int KS = latency ? kv_groups_max(head_dim) : 1;
   const long long tgt = target_items(KS, num_cus, num_kv_heads);
   long long chunk_it = std::max<long long>(
@@ -861,6 +1060,10 @@ extern "C" int32_t nsg_attn_run(const nsg_attn_plan_t* plan, const int32_t* work
   const int log2P = ilog2_exact(page_size);
   NSG_CHECK_ARG(log2P >= 0, "page_size %d must be a power of two", page_size);
   NSG_CHECK_ARG(num_pages > 0, "num_pages %d", num_pages);
+  NSG_CHECK_ARG(sm_scale > 0.f, "sm_scale %g must be positive", (double)sm_scale);
+  NSG_CHECK_ARG(plan->kv_groups == 1 || page_size >= kMinGroupPage,
+                "page_size %d: the plan's %d KV groups need pages of %d+ tokens (plan and run "
+                "with the same page size)", page_size, plan->kv_groups, kMinGroupPage);
   if (workspace_bytes < plan->workspace_bytes) {
     set_error("workspace has %lld bytes, plan needs %lld", (long long)workspace_bytes,
               (long long)plan->workspace_bytes);

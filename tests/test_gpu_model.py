@@ -5,7 +5,12 @@
   (bf16 tolerance) on a tiny random model;
 * the speculative engine: greedy output equals plain greedy decoding
   (k = 0, one verify token per step) on the GPU -- the speculative-sampling
-  invariant; the first divergence from the CPU fp32 oracle is reported.
+  invariant -- up to exact bf16 ties: the verify step (k + 1 query rows) and
+  the decode step (one row) run the attention with different tiles, so
+  their bf16 logits may differ by an ulp, and where two tokens' logits are
+  that close the argmax may go either way; such a divergence must sit on a
+  near-tie (within 2 bf16 ulps) of both engines' logits.  The first
+  divergence from the CPU fp32 oracle is reported.
 """
 import numpy as np
 import pytest
@@ -43,6 +48,46 @@ def test_rope_kv_write_bit_exact():
     flat_v = vc.view(-1, Hkv, D).cpu()
     assert torch.equal(flat_k[slots], ref[:, Hq:Hq + Hkv])
     assert torch.equal(flat_v[slots], qkv.view(T, -1, D)[:, Hq + Hkv:])
+
+
+def _logit_rows(trace, max_new):
+    """Per request, the verify-logits row (float32, CPU) behind each emitted
+    token position (token 0 comes from the prefill).  The engines keep the
+    unfinished requests in submission order, one batch row each."""
+    cnt = [1] * len(max_new)
+    rows = [dict() for _ in max_new]
+    for rec in trace:
+        active = [r for r in range(len(max_new)) if cnt[r] < max_new[r]]
+        n = rec["num_emitted"]
+        assert len(n) == len(active)
+        for i, r in enumerate(active):
+            for j in range(int(n[i])):
+                rows[r][cnt[r] + j] = rec["verify_logits"][i, j].float()
+            cnt[r] += int(n[i])
+    return rows
+
+
+def _assert_equal_up_to_bf16_ties(spec, plain, max_new, out_spec, out_plain):
+    """out_spec == out_plain, or each request's first divergence is a
+    near-tie: the two chosen tokens' logits within 2 bf16 ulps in both
+    engines' own logits at that position.  Returns the number of ties."""
+    rs, rp = _logit_rows(spec.trace, max_new), _logit_rows(plain.trace, max_new)
+    ties = 0
+    for r, (a, b) in enumerate(zip(out_spec, out_plain)):
+        assert len(a) == len(b) == max_new[r]
+        d = next((i for i, (x, y) in enumerate(zip(a, b)) if x != y), None)
+        if d is None:
+            continue
+        assert d >= 1, f"request {r}: prefill tokens differ"
+        for name, lg in (("spec", rs[r][d]), ("plain", rp[r][d])):
+            top = lg.abs().max().item()
+            ulp = 2.0 ** (np.floor(np.log2(top)) - 7)
+            gap = abs(lg[a[d]].item() - lg[b[d]].item())
+            print(f"  request {r}: first divergence at {d}: tokens {a[d]} / {b[d]}, {name} "
+                  f"logits {lg[a[d]].item():.6g} / {lg[b[d]].item():.6g}", flush=True)
+            assert gap <= 2 * ulp, (r, d, name, gap, ulp)
+        ties += 1
+    return ties
 
 
 def _tiny_models(scale=8.0, dtype=torch.float32):
@@ -114,12 +159,14 @@ def test_spec_engine_greedy_equals_plain_greedy_and_oracle(graphs):
     max_new = [24, 17, 30, 9]
     spec = SpecEngine(gpu, draft_layers=2, num_speculative=4, num_blocks=64, use_graphs=graphs,
                       max_batch=4)
+    spec.trace = []
     out_spec = spec.generate(prompts, max_new)
     st = spec.stats
     print(f"  spec: acceptance {st['acceptance_rate']:.2f} tokens/step {st['tokens_per_step']:.2f}"
           f" graphs {st['graphs']}", flush=True)
     plain = SpecEngine(gpu, draft_layers=2, num_speculative=0, num_blocks=64, use_graphs=graphs,
                        max_batch=4)
+    plain.trace = []
     out_plain = plain.generate(prompts, max_new)
     assert [len(o) for o in out_spec] == max_new
     reserved = 1 if graphs else 0                       # the graphs' dummy padding page
@@ -127,7 +174,8 @@ def test_spec_engine_greedy_equals_plain_greedy_and_oracle(graphs):
     assert plain.bm.num_free_blocks == 64 - reserved
     same = sum(a == b for a, b in zip(out_spec, out_plain))
     print(f"  spec == plain greedy for {same}/{len(prompts)} requests", flush=True)
-    assert same == len(prompts)
+    ties = _assert_equal_up_to_bf16_ties(spec, plain, max_new, out_spec, out_plain)
+    assert same + ties == len(prompts)
     # CPU fp32 oracle on the same weights: reported, not asserted -- with 8x
     # weights bf16 and fp32 logits disagree on ~9% of argmaxes even between
     # the oracle's own bf16 and fp32 runs, so token streams part early.
@@ -155,8 +203,12 @@ def test_spec_engine_fp8_weights_greedy_equals_plain_greedy():
     max_new = [20, 12, 25, 8]
     spec = SpecEngine(gpu, draft_layers=2, num_speculative=4, num_blocks=64, max_batch=4)
     plain = SpecEngine(gpu, draft_layers=2, num_speculative=0, num_blocks=64, max_batch=4)
+    spec.trace, plain.trace = [], []
     out_spec, out_plain = spec.generate(prompts, max_new), plain.generate(prompts, max_new)
-    assert out_spec == out_plain
+    same = sum(a == b for a, b in zip(out_spec, out_plain))
+    ties = _assert_equal_up_to_bf16_ties(spec, plain, max_new, out_spec, out_plain)
+    print(f"  spec == plain greedy for {same}/{len(prompts)} requests, {ties} bf16 ties", flush=True)
+    assert same + ties == len(prompts)
     # packed forward (init-scale weights) vs the CPU fp32 oracle on the
     # dequantised weights: the bf16 tolerance of the bf16 model's test
     from nanosglang_amd.engine.paged_kv_cache import BlockManager, PagedKVCache

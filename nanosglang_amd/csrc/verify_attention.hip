@@ -129,27 +129,25 @@ __device__ __forceinline__ float sum_xor16_32(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// Eight transposing LDS reads (V^T fragments of four d tiles) and the wait
-// for them, as one asm block.  Written through the builtin, every such read
-// after a global_load_lds gets a conservative vmcnt(0) from the compiler (it
-// cannot tell the read from the ring slots still being filled), which stalls
-// each step until every copy in flight has landed; the ring's own waits
-// (vmcnt per step plus the barrier) already order these reads.
-__device__ __forceinline__ void ds_read_tr8(v4i16 (&r)[8], const uint32_t (&a)[8]) {
-  asm volatile(
-      "ds_read_b64_tr_b16 %0, %8\n\t"
-      "ds_read_b64_tr_b16 %1, %9\n\t"
-      "ds_read_b64_tr_b16 %2, %10\n\t"
-      "ds_read_b64_tr_b16 %3, %11\n\t"
-      "ds_read_b64_tr_b16 %4, %12\n\t"
-      "ds_read_b64_tr_b16 %5, %13\n\t"
-      "ds_read_b64_tr_b16 %6, %14\n\t"
-      "ds_read_b64_tr_b16 %7, %15\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]),
-        "=&v"(r[6]), "=&v"(r[7])
-      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7])
-      : "memory");
+// Transposing LDS reads of the V^T fragments, in asm.  Written through the
+// builtin, every such read after a global_load_lds gets a conservative
+// vmcnt(0) from the compiler (it cannot tell the read from the ring slots
+// still being filled), which stalls each step until every copy in flight has
+// landed; the ring's own waits (vmcnt per step plus the barrier) already
+// order these reads.  tr_issue starts the two reads of one d tile; tr_wait
+// waits until at most N LDS operations are outstanding, after which the
+// tile's registers (tied operands, so that the compiler reads them only
+// after the wait) hold the data.  LDS operations complete in order, so the
+// reads of tile dt are done once those of tile dt + 1 are the only ones left.
+__device__ __forceinline__ void tr_issue(v4i16& lo, v4i16& hi, uint32_t a0, uint32_t a1) {
+  asm volatile("ds_read_b64_tr_b16 %0, %2\n\tds_read_b64_tr_b16 %1, %3"
+               : "=&v"(lo), "=&v"(hi)
+               : "v"(a0), "v"(a1)
+               : "memory");
+}
+template <int N>
+__device__ __forceinline__ void tr_wait(v4i16& lo, v4i16& hi) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(lo), "+v"(hi) : "n"(N) : "memory");
 }
 
 // 32-bit LDS address of a pointer into __shared__ memory.
@@ -240,9 +238,25 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
   constexpr int kRingBytes = KS * kNBuf * 2 * TILE * 2;
   constexpr int kPageBytes = KS == 1 ? kMaxItemPages * 4 : 0;
   static_assert(kRingBytes + kPageBytes <= kLdsBytes, "LDS budget");
-  __shared__ __attribute__((aligned(16))) unsigned char smem[kRingBytes + kPageBytes];
-  auto ring = reinterpret_cast<bf16 (*)[kNBuf][2][TILE]>(smem);
-  int* s_pages = reinterpret_cast<int*>(smem + kRingBytes);  // one KV group only
+  // One KV group: typed arrays.  Several: one 160 KB block (rings only, no
+  // room for the 4-byte minimum of a second array).  With the block, the
+  // compiler cannot tell the rings' reads from their pending copies and
+  // waits for every copy before each transposing read; the typed rings of
+  // one group keep it from doing so (measured: the one-group kernel at the
+  // large shape 307 us typed, 351 us with the block), and the several-group
+  // kernel reads V^T in asm instead.
+  bf16 (*ring)[kNBuf][2][TILE];
+  int* s_pages;
+  if constexpr (KS == 1) {
+    __shared__ __attribute__((aligned(16))) bf16 ring1[1][kNBuf][2][TILE];
+    __shared__ int pages1[kMaxItemPages];
+    ring = ring1;
+    s_pages = pages1;
+  } else {
+    __shared__ __attribute__((aligned(16))) unsigned char ringg[kRingBytes];
+    ring = reinterpret_cast<bf16 (*)[kNBuf][2][TILE]>(ringg);
+    s_pages = nullptr;
+  }
 
   // blockIdx.x = KV head (fastest), so the Hkv workgroups of one work item
   // are dispatched together and read the interleaved head slices of the same
@@ -550,32 +564,31 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
         sacc[s2] = acc;
       }
 
-      // ---- online softmax (base 2) with lazy rescaling.  The max is taken
-      //      over the raw scores and scaled once (the scale is positive); the
-      //      scale folds into the exponent's FMA.  Masked scores get P = 0
-      //      outright, and a row with nothing visible leaves its max alone
-      //      (an FMA of a sentinel against a rounded sentinel max could give
-      //      exp2 of a huge residue) ----
       float pv[8];
-      auto softmax = [&](auto masked) {
-        constexpr bool MASKED = decltype(masked)::value;
+      if constexpr (KS == 1) {
+        // ---- online softmax (base 2) with lazy rescaling (one KV group: the
+        //      plain form, which keeps the head-dim-128 kernel at 3 waves per
+        //      SIMD; the form below needs more registers) ----
         float sv[8];
-        bool vis[8];
+        if (t0 + kTokIt - 1 <= lim0 && t0 + kTokIt <= kve) {
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
+          for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int j = t0 + 16 * s2 + 4 * g4 + i;
-            vis[4 * s2 + i] = !MASKED || (j <= lim && j < kve);
-            sv[4 * s2 + i] = vis[4 * s2 + i] ? sacc[s2][i] : kMaskVal;
+            for (int i = 0; i < 4; ++i) sv[4 * s2 + i] = sacc[s2][i] * p.scale_log2;
+        } else {
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int j = t0 + 16 * s2 + 4 * g4 + i;
+              sv[4 * s2 + i] = (j <= lim && j < kve) ? sacc[s2][i] * p.scale_log2 : kMaskVal;
+            }
           }
         }
         float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
                          fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-        mx = max_xor16_32(mx);
-        mx = (MASKED && mx == kMaskVal) ? kMaskVal : mx * p.scale_log2;
-        // Raise the exponent base only when a row max exceeds it by > 2^8, and
-        // skip the O rescale entirely when no row of the wave needs it.
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const bool grow = mx > m_run + kLazyRescale;
         if (__builtin_amdgcn_ballot_w64(grow)) {
           const float mnew = grow ? mx : m_run;
@@ -588,18 +601,61 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
         float ps = 0.f;
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
-          const float e = __builtin_amdgcn_exp2f(fmaf(sv[x], p.scale_log2, -m_run));
-          pv[x] = MASKED && !vis[x] ? 0.f : e;
+          pv[x] = __builtin_amdgcn_exp2f(sv[x] - m_run);
           ps += pv[x];
         }
         l_run += ps;
-      };
-      if (t0 + kTokIt - 1 <= lim0 && t0 + kTokIt <= kve) {
-        // every row of the tile sees every token of the step (lim0 is the
-        // tile's smallest causal limit): no mask
-        softmax(std::false_type{});
       } else {
-        softmax(std::true_type{});
+        // ---- online softmax (base 2) with lazy rescaling.  The max is taken
+        //      over the raw scores and scaled once (the scale is positive); the
+        //      scale folds into the exponent's FMA.  Masked scores get P = 0
+        //      outright, and a row with nothing visible leaves its max alone
+        //      (an FMA of a sentinel against a rounded sentinel max could give
+        //      exp2 of a huge residue) ----
+        auto softmax = [&](auto masked) {
+          constexpr bool MASKED = decltype(masked)::value;
+          float sv[8];
+          bool vis[8];
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int j = t0 + 16 * s2 + 4 * g4 + i;
+              vis[4 * s2 + i] = !MASKED || (j <= lim && j < kve);
+              sv[4 * s2 + i] = vis[4 * s2 + i] ? sacc[s2][i] : kMaskVal;
+            }
+          }
+          float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                           fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+          mx = max_xor16_32(mx);
+          mx = (MASKED && mx == kMaskVal) ? kMaskVal : mx * p.scale_log2;
+          // Raise the exponent base only when a row max exceeds it by > 2^8, and
+          // skip the O rescale entirely when no row of the wave needs it.
+          const bool grow = mx > m_run + kLazyRescale;
+          if (__builtin_amdgcn_ballot_w64(grow)) {
+            const float mnew = grow ? mx : m_run;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);
+            m_run = mnew;
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+          }
+          float ps = 0.f;
+#pragma unroll
+          for (int x = 0; x < 8; ++x) {
+            const float e = __builtin_amdgcn_exp2f(fmaf(sv[x], p.scale_log2, -m_run));
+            pv[x] = MASKED && !vis[x] ? 0.f : e;
+            ps += pv[x];
+          }
+          l_run += ps;
+        };
+        if (t0 + kTokIt - 1 <= lim0 && t0 + kTokIt <= kve) {
+          // every row of the tile sees every token of the step (lim0 is the
+          // tile's smallest causal limit): no mask
+          softmax(std::false_type{});
+        } else {
+          softmax(std::true_type{});
+        }
       }
       const bf16x8 pf = __builtin_bit_cast(
           bf16x8, u32x4{cvt_pk_bf16(pv[0], pv[1]), cvt_pk_bf16(pv[2], pv[3]),
@@ -607,24 +663,36 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
 
       // ---- O^T += V^T P^T; element e of lane group g4 is token
       //      4*g4 + e (e < 4) or 16 + 4*g4 + (e - 4), matching pf ----
-      static_assert(DT % 4 == 0, "V^T fragments come in groups of four d tiles");
+      if constexpr (KS == 1) {
+        // (the builtin: with typed rings the compiler adds no wait, and
+        // interleaves the reads with the MFMAs itself)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) v4i16*)(Vt + vtr[dt][0]));
+          const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) v4i16*)(Vt + vtr[dt][1]));
+          const v8i16 w = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+          oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w), pf,
+                                                             oacc[dt], 0, 0, 0);
+        }
+        continue;
+      }
+      // (reads of tile dt + 1 in flight while tile dt's MFMA issues)
       const uint32_t vbase = lds_addr(Vt);
+      v4i16 rl[DT], rh[DT];
+      tr_issue(rl[0], rh[0], vbase + 2 * vtr[0][0], vbase + 2 * vtr[0][1]);
 #pragma unroll
-      for (int d4 = 0; d4 < DT; d4 += 4) {
-        uint32_t a[8];
-        v4i16 r[8];
-#pragma unroll
-        for (int x = 0; x < 4; ++x) {
-          a[2 * x] = vbase + 2 * vtr[d4 + x][0];
-          a[2 * x + 1] = vbase + 2 * vtr[d4 + x][1];
+      for (int dt = 0; dt < DT; ++dt) {
+        if (dt + 1 < DT) {
+          tr_issue(rl[dt + 1], rh[dt + 1], vbase + 2 * vtr[dt + 1][0], vbase + 2 * vtr[dt + 1][1]);
+          tr_wait<2>(rl[dt], rh[dt]);
+        } else {
+          tr_wait<0>(rl[dt], rh[dt]);
         }
-        ds_read_tr8(r, a);
-#pragma unroll
-        for (int x = 0; x < 4; ++x) {
-          const v8i16 w = __builtin_shufflevector(r[2 * x], r[2 * x + 1], 0, 1, 2, 3, 4, 5, 6, 7);
-          oacc[d4 + x] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w), pf,
-                                                                 oacc[d4 + x], 0, 0, 0);
-        }
+        const v8i16 w = __builtin_shufflevector(rl[dt], rh[dt], 0, 1, 2, 3, 4, 5, 6, 7);
+        oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w), pf,
+                                                           oacc[dt], 0, 0, 0);
       }
     }
   }
@@ -640,7 +708,7 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
     // ---- combine the KV groups through LDS (the rings are idle: every
     //      group's last real step waited for all of its copies) ----
     constexpr int SROW = D + 4;  // O[D], m, l, 2 pad
-    float* sc = reinterpret_cast<float*>(smem);
+    float* sc = reinterpret_cast<float*>(&ring[0][0][0][0]);
     static_assert((size_t)KS * ROWS * SROW * 4 <= (size_t)kRingBytes,
                   "combine scratch fits the rings");
     __syncthreads();

@@ -206,11 +206,20 @@ int32_t nsg_spec_step_fill(const int32_t* page_table, int64_t page_table_stride,
  * k may be 0: the call then samples one token per request from row 0
  *   (argmax when greedy), which is the reference's sample_token
  *   (sampling.py:25-50) without top-k / top-p (nsg_sample has them).
+ * Workspace: zero when first used, and for acceptance calls only (not shared
+ *   with nsg_sample).  Past its 256-byte flag header it holds hand-off slots
+ *   through which a request's workgroups pass records to the one that
+ *   finishes the request; every slot is zero between calls (the readers clear
+ *   what the writers published), so one workspace serves calls of any (B, k)
+ *   in turn.  Calls sharing a workspace must not overlap.
  * Bad inputs found on the device leave well-defined outputs and set bits of
  *   an error-flag word at the start of the workspace (which should start at
  *   zero), read with nsg_spec_accept_check_flags: bit 1, a rolled-back
  *   position past the request's pages (its slot is -1); bit 2, a draft token
- *   outside [0, vocab) (rejected, as a draft the target never proposes).
+ *   outside [0, vocab) (rejected, as a draft the target never proposes);
+ *   bit 3, a hand-off wait that ran out its bounded spin (a workspace that was
+ *   not zero, or shared with an overlapping call; outputs then undefined, and
+ *   nsg_spec_accept_check_flags zeroes the whole header).
  * ---------------------------------------------------------------------- */
 int64_t nsg_spec_accept_workspace_bytes(int32_t batch, int32_t k, int32_t vocab);
 

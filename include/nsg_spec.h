@@ -43,7 +43,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 12
+#define NSG_ABI_VERSION 13
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -406,6 +406,45 @@ int32_t nsg_linear_rope_kv(const void* x, int64_t ldx, const void* w, int64_t ld
                            int32_t max_position, const int64_t* slots, void* q_out,
                            void* k_cache, void* v_cache, int64_t num_slots, int32_t* flags,
                            nsg_stream_t stream);
+
+/* RMSNorm folded into the linears around it (bf16 weights, M up to 160,
+ * hidden up to 1024).  No counterpart entry in the reference, whose decoder
+ * layer runs residual add + RMSNorm (causal_lm.py:133-154) between the
+ * projections; here that norm costs no launch of its own:
+ *  - the norm weight w_ln is folded into the columns of the next linear's
+ *    weight once (W'[n, k] = bf16(w_ln[k] * W[n, k])), and that linear (the
+ *    consumer: q/k/v with RoPE, or gate/up with SwiGLU) takes the
+ *    un-normalised rows x and scales row m of x W'^T by
+ *    rsqrt(S_m / norm_dim + eps) before its epilogue, where S_m, the sum of
+ *    squares of x's row m, arrives as sumsq_parts partial sums
+ *    sumsq_in[c * M + m] added in a fixed order;
+ *  - the linear before it (the producer: o_proj, down_proj, bias epilogue)
+ *    adds its result to the residual stream in bf16 (y = bf16(residual +
+ *    bf16(x W^T + bias)), y may be the residual buffer itself) and writes
+ *    sumsq_out[(n / 16) * M + m], the sum of squares of y's row m over
+ *    columns n .. n + 15 (N / 16 partials per row, N % 16 == 0);
+ *  - nsg_row_sumsq writes the same partials for the first layer's input.
+ * Rounding differs from the reference's norm in two places: w_ln * W is
+ * rounded to bf16 instead of w_ln * bf16(x * r), and x * r is not rounded.
+ * nsg_linear_fold: the consumer side when sumsq_in is given, the producer
+ * side when residual and sumsq_out are (NSG_LINEAR_BIAS only), else
+ * nsg_linear. */
+int32_t nsg_linear_fold(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias,
+                        void* y, int64_t ldy, int32_t M, int32_t N, int32_t K, int32_t epilogue,
+                        const float* sumsq_in, int32_t sumsq_parts, int32_t norm_dim, float eps,
+                        const void* residual, int64_t ldr, float* sumsq_out,
+                        nsg_stream_t stream);
+int32_t nsg_linear_rope_kv_fold(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                const void* bias, int32_t M, int32_t K, int32_t num_qo_heads,
+                                int32_t num_kv_heads, int32_t head_dim,
+                                const int64_t* positions, const float* cos_table,
+                                const float* sin_table, int32_t max_position,
+                                const int64_t* slots, void* q_out, void* k_cache,
+                                void* v_cache, int64_t num_slots, int32_t* flags,
+                                const float* sumsq_in, int32_t sumsq_parts, int32_t norm_dim,
+                                float eps, nsg_stream_t stream);
+int32_t nsg_row_sumsq(const void* x, int64_t ldx, int32_t num_tokens, int32_t hidden,
+                      float* sumsq_out, nsg_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Philox4x32-10 uniforms: out[i] = u(seed, stream_id, offset + i) with

@@ -129,6 +129,39 @@ void launch_rmsnorm(const uint16_t* x, uint16_t* residual, const uint16_t* w, ui
                        out, T, H, eps);
 }
 
+// Partial sums of squares of bf16 rows for a folded-RMSNorm consumer:
+// out[g * T + t] = sum over columns 16 g .. 16 g + 15 of x[t, :]^2 (one wave
+// per row; lane l holds 8-column chunks l + 64 c, and the two chunks of a
+// 16-column group sit on lanes 2 i, 2 i + 1).  The layout a producing linear
+// writes (nsg_linear_fold), for the first layer's input.
+template <int C>
+__global__ __launch_bounds__(kNormThreads) void row_sumsq_kernel(const uint16_t* __restrict__ x,
+                                                                  int64_t ldx, int T, int H,
+                                                                  float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * (kNormThreads / 64) + (threadIdx.x >> 6);
+  if (t >= T) return;  // wave-uniform
+  const int nch = H >> 3;
+  u32x4 a[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c)
+    a[c] = *reinterpret_cast<const u32x4*>(x + (int64_t)t * ldx + min(lane + 64 * c, nch - 1) * 8);
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int ch = lane + 64 * c;
+    float sq = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lo = bf16_bits_to_float(a[c][i] & 0xffffu);
+      const float hi = bf16_bits_to_float(a[c][i] >> 16);
+      sq = __builtin_fmaf(lo, lo, sq);
+      sq = __builtin_fmaf(hi, hi, sq);
+    }
+    sq += __shfl_xor(sq, 1, 64);
+    if (ch < nch && (ch & 1) == 0) out[(int64_t)(ch >> 1) * T + t] = sq;
+  }
+}
+
 // out[t, j] = bf16(bf16(silu(gu[t, j])) * gu[t, I + j]) for j < I.
 __global__ void silu_mul_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ out,
                                 int64_t T, int I) {
@@ -180,6 +213,25 @@ extern "C" int32_t nsg_rmsnorm(const void* x, void* residual, const void* weight
                           static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out),
                           num_tokens, hidden, eps, s);
   return launch_status("rmsnorm_kernel");
+}
+
+extern "C" int32_t nsg_row_sumsq(const void* x, int64_t ldx, int32_t num_tokens, int32_t hidden,
+                                 float* sumsq_out, nsg_stream_t stream) {
+  NSG_CHECK_ARG(num_tokens >= 0, "num_tokens %d < 0", num_tokens);
+  if (num_tokens == 0) {
+    clear_error();
+    return NSG_OK;
+  }
+  NSG_CHECK_ARG(x && sumsq_out, "null pointer argument");
+  NSG_CHECK_ARG(hidden > 0 && hidden % 16 == 0 && hidden <= 1024,
+                "hidden %d must be a multiple of 16 and at most 1024", hidden);
+  NSG_CHECK_ARG(ldx >= hidden && ldx % 8 == 0 && (uintptr_t)x % 16 == 0,
+                "x rows must be 16-byte aligned (ldx %lld)", (long long)ldx);
+  const dim3 grid((num_tokens + kNormThreads / 64 - 1) / (kNormThreads / 64));
+  hipLaunchKernelGGL((row_sumsq_kernel<2>), grid, dim3(kNormThreads), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), ldx,
+                     num_tokens, hidden, sumsq_out);
+  return launch_status("row_sumsq_kernel");
 }
 
 extern "C" int32_t nsg_silu_mul(const void* gate_up, void* out, int64_t num_tokens,

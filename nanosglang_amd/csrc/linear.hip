@@ -36,6 +36,9 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kChunk = 64;  // K elements per wave step (two MFMA k-slices)
 constexpr int kMaxMT = 10;  // up to 160 rows of x
+// Partial sums of squares a folded-RMSNorm consumer reads per row: one per
+// 16 columns of the producer's output, hidden sizes up to 1024.
+constexpr int kMaxSumsqParts = 64;
 
 struct LinParams {
   const bf16* x;
@@ -63,6 +66,22 @@ struct LinParams {
   bf16* vc;
   int64_t num_slots;
   int* flags;
+  // RMSNorm folded into the layer's linears (the norm weight folded into the
+  // consumer's W columns):
+  //  consumer -- x rows are un-normalised; row m's result is scaled by
+  //    rsqrt(S_m / norm_dim + norm_eps) before the epilogue, where S_m is
+  //    the sum of sumsq_in[c * M + m] over c < sumsq_parts (fixed order);
+  //  producer (bias epilogue) -- y = bf16(residual + bf16(x W^T + bias)),
+  //    and sumsq_out[(n / 16) * M + m] = the sum of squares of y's row m
+  //    over columns n .. n + 15 (one partial per 16 columns: deterministic,
+  //    whatever the tile shape).
+  const float* sumsq_in;
+  int sumsq_parts;
+  int norm_dim;
+  float norm_eps;
+  const bf16* residual;
+  int64_t ldr;
+  float* sumsq_out;
 };
 
 
@@ -274,6 +293,35 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
   // before the current chunk's MFMAs.
   const int n = (nchunks - wave + NW - 1) / NW;
   if (n > 0) load(wave, wa, xa);
+  // Folded RMSNorm (consumer): the scale of each of this workgroup's rows,
+  // summed from the producer's partials (in a fixed order) while the first
+  // chunk's loads are in flight, and kept in LDS for the epilogue.
+  // Wave 0 does it: row r of the R rows on R-lane groups of the wave, each
+  // lane summing every (64 / R)-th partial (at most kMaxSumsqParts in all,
+  // every load issued before the first add), then an xor butterfly over the
+  // row's lanes -- one fixed order, so the scale is the same on every call.
+  constexpr int R = MG * MT * 16;
+  static_assert(R <= 64 && 64 % R == 0, "rows of a workgroup on one wave");
+  constexpr int LPR = 64 / R;                    // lanes per row
+  constexpr int PPL = kMaxSumsqParts / LPR;      // partials per lane
+  __shared__ float rscale[R];
+  if (p.sumsq_in && wid == 0) {
+    const int r = lane % R;
+    const int m = m0 + min(r, M - 1);
+    float part[PPL];
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) {
+      const int c = lane / R + LPR * j;
+      part[j] = c < p.sumsq_parts ? p.sumsq_in[(int64_t)c * p.M + m] : 0.f;
+    }
+    float ssum = 0.f;
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) ssum += part[j];
+#pragma unroll
+    for (int o = R; o < 64; o <<= 1) ssum += __shfl_xor(ssum, o, 64);
+    if (lane < R) rscale[r] = 1.f / sqrtf(ssum / (float)p.norm_dim + p.norm_eps);
+  }
+
   if constexpr (kRope) {
 #pragma unroll
     for (int j = 0; j < kIpt; ++j) {
@@ -334,6 +382,7 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
         const uint2 bb = e_bias[j];
         const float b4[4] = {bf16_bits_to_float(bb.x & 0xffffu), bf16_bits_to_float(bb.x >> 16),
                              bf16_bits_to_float(bb.y & 0xffffu), bf16_bits_to_float(bb.y >> 16)};
+        if (p.sumsq_in) sum *= rscale[mt * 16 + (l & 15)];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           hv[mt * 16 + (l & 15)][q * 16 + 4 * (l >> 4) + i] = bf16_round(sum[i] + b4[i]);
@@ -407,9 +456,13 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
         n = (tile * (NT / 2) + t0 / 2) * 16 + 4 * (l >> 4);
       else
         n = (tile * NT + t0) * 16 + 4 * (l >> 4);
-      if (m >= M || n >= p.N) continue;
+      const bool ok = m < M && n < p.N;
       float v[4];
       if constexpr (EPI == kEpiSilu) {
+        if (p.sumsq_in) {
+#pragma unroll
+          for (int q = 0; q < NP; ++q) s[q] *= rscale[m];
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float g = bf16_bits_to_float(float_to_bf16_bits(s[0][i]));
@@ -419,14 +472,34 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = s[0][i];
-        if (p.bias) {
+        if (p.bias && ok) {
           const u32x2 b = *reinterpret_cast<const u32x2*>(p.bias + n);
           v[0] += bf16_bits_to_float(b[0] & 0xffff);
           v[1] += bf16_bits_to_float(b[0] >> 16);
           v[2] += bf16_bits_to_float(b[1] & 0xffff);
           v[3] += bf16_bits_to_float(b[1] >> 16);
         }
+        if (p.residual) {
+          // producer of a folded RMSNorm: the bf16 residual add, then the
+          // partial sum of squares of the 16 columns n & ~15 .. + 15 of row
+          // m (the four lanes l, l ^ 16, l ^ 32, l ^ 48 hold them)
+          float sq = 0.f;
+          if (ok) {
+            const u32x2 r = *reinterpret_cast<const u32x2*>(p.residual + (int64_t)(m0 + m) * p.ldr + n);
+            const float rv[4] = {bf16_bits_to_float(r[0] & 0xffff), bf16_bits_to_float(r[0] >> 16),
+                                 bf16_bits_to_float(r[1] & 0xffff), bf16_bits_to_float(r[1] >> 16)};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              v[i] = bf16_round(rv[i] + bf16_round(v[i]));
+              sq = __builtin_fmaf(v[i], v[i], sq);
+            }
+          }
+          sq += __shfl_xor(sq, 16, 64);
+          sq += __shfl_xor(sq, 32, 64);
+          if (ok && (l >> 4) == 0) p.sumsq_out[(int64_t)(n >> 4) * p.M + m0 + m] = sq;
+        }
       }
+      if (!ok) continue;
       *reinterpret_cast<u32x2*>(yg + (int64_t)m * p.ldy + n) =
           u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
     }
@@ -528,9 +601,47 @@ namespace {
 
 // Shared by the bf16 and FP8-weight entry points: exactly one of w / w8 is
 // given; w8 rows are ldw bytes apart and w_scale holds one f32 per W row.
+// Folded-RMSNorm arguments of the *_fold entry points (see LinParams).
+struct NormFold {
+  const float* sumsq_in;
+  int32_t parts;
+  int32_t dim;
+  float eps;
+  const void* residual;
+  int64_t ldr;
+  float* sumsq_out;
+};
+
+// Checks the folded-norm arguments and copies them into p.
+int32_t apply_fold(LinParams& p, const NormFold* nf, int32_t M, int32_t N, bool producer_ok) {
+  if (!nf) return NSG_OK;
+  if (nf->sumsq_in) {
+    NSG_CHECK_ARG(nf->parts >= 1 && nf->parts <= kMaxSumsqParts && nf->dim > 0 && nf->eps >= 0.f,
+                  "folded norm: %d partials (1 .. %d), dim %d, eps %g", nf->parts, kMaxSumsqParts,
+                  nf->dim, (double)nf->eps);
+    p.sumsq_in = nf->sumsq_in;
+    p.sumsq_parts = nf->parts;
+    p.norm_dim = nf->dim;
+    p.norm_eps = nf->eps;
+  }
+  if (nf->residual || nf->sumsq_out) {
+    NSG_CHECK_ARG(producer_ok, "the residual add takes the bias epilogue");
+    NSG_CHECK_ARG(nf->residual && nf->sumsq_out && N % 16 == 0 && nf->ldr >= N && nf->ldr % 4 == 0 &&
+                      (uintptr_t)nf->residual % 8 == 0,
+                  "folded norm producer: residual (8-byte aligned rows, ldr %lld >= N %d) and "
+                  "sumsq_out needed, N a multiple of 16", (long long)nf->ldr, N);
+    p.residual = static_cast<const bf16*>(nf->residual);
+    p.ldr = nf->ldr;
+    p.sumsq_out = nf->sumsq_out;
+  }
+  (void)M;
+  return NSG_OK;
+}
+
 int32_t linear_impl(const void* x, int64_t ldx, const void* w, const void* w8, int64_t ldw,
                     const float* w_scale, const void* bias, void* y, int64_t ldy, int32_t M,
-                    int32_t N, int32_t K, int32_t epilogue, nsg_stream_t stream) {
+                    int32_t N, int32_t K, int32_t epilogue, nsg_stream_t stream,
+                    const NormFold* nf = nullptr) {
   NSG_CHECK_ARG(M >= 0 && N > 0 && K > 0, "M %d, N %d, K %d", M, N, K);
   if (M == 0) {
     clear_error();
@@ -567,6 +678,7 @@ int32_t linear_impl(const void* x, int64_t ldx, const void* w, const void* w8, i
   p.N = N;
   p.K = K;
   p.w_rows = epilogue == NSG_LINEAR_SILU_MUL ? 2 * N : N;
+  if (int32_t rc = apply_fold(p, nf, M, N, epilogue == NSG_LINEAR_BIAS)) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   return epilogue == NSG_LINEAR_SILU_MUL ? launch_epi<kEpiSilu>(p, s) : launch_epi<kEpiBias>(p, s);
 }
@@ -576,7 +688,8 @@ int32_t rope_impl(const void* x, int64_t ldx, const void* w, const void* w8, int
                   int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                   const int64_t* positions, const float* cos_table, const float* sin_table,
                   int32_t max_position, const int64_t* slots, void* q_out, void* k_cache,
-                  void* v_cache, int64_t num_slots, int32_t* flags, nsg_stream_t stream) {
+                  void* v_cache, int64_t num_slots, int32_t* flags, nsg_stream_t stream,
+                  const NormFold* nf = nullptr) {
   NSG_CHECK_ARG(M >= 0 && K > 0, "M %d, K %d", M, K);
   if (M == 0) {
     clear_error();
@@ -627,6 +740,7 @@ int32_t rope_impl(const void* x, int64_t ldx, const void* w, const void* w8, int
   p.vc = static_cast<bf16*>(v_cache);
   p.num_slots = num_slots;
   p.flags = flags;
+  if (int32_t rc = apply_fold(p, nf, M, N, false)) return rc;
   return launch_rope(p, static_cast<hipStream_t>(stream));
 }
 
@@ -674,6 +788,33 @@ extern "C" int32_t nsg_linear_rope_kv_fp8(const void* x, int64_t ldx, const void
   return rope_impl(x, ldx, nullptr, w8, ldw8, w_scale, bias, M, K, num_qo_heads, num_kv_heads,
                    head_dim, positions, cos_table, sin_table, max_position, slots, q_out, k_cache,
                    v_cache, num_slots, flags, stream);
+}
+
+// ---- RMSNorm folded into the linears around it (bf16 weights) ----
+extern "C" int32_t nsg_linear_fold(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                   const void* bias, void* y, int64_t ldy, int32_t M, int32_t N,
+                                   int32_t K, int32_t epilogue, const float* sumsq_in,
+                                   int32_t sumsq_parts, int32_t norm_dim, float eps,
+                                   const void* residual, int64_t ldr, float* sumsq_out,
+                                   nsg_stream_t stream) {
+  NSG_CHECK_ARG(w, "null weight");
+  const NormFold nf{sumsq_in, sumsq_parts, norm_dim, eps, residual, ldr, sumsq_out};
+  return linear_impl(x, ldx, w, nullptr, ldw, nullptr, bias, y, ldy, M, N, K, epilogue, stream,
+                     &nf);
+}
+
+extern "C" int32_t nsg_linear_rope_kv_fold(
+    const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias, int32_t M,
+    int32_t K, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+    const int64_t* positions, const float* cos_table, const float* sin_table,
+    int32_t max_position, const int64_t* slots, void* q_out, void* k_cache, void* v_cache,
+    int64_t num_slots, int32_t* flags, const float* sumsq_in, int32_t sumsq_parts,
+    int32_t norm_dim, float eps, nsg_stream_t stream) {
+  NSG_CHECK_ARG(w && sumsq_in, "null weight or sums of squares");
+  const NormFold nf{sumsq_in, sumsq_parts, norm_dim, eps, nullptr, 0, nullptr};
+  return rope_impl(x, ldx, w, nullptr, ldw, nullptr, bias, M, K, num_qo_heads, num_kv_heads,
+                   head_dim, positions, cos_table, sin_table, max_position, slots, q_out, k_cache,
+                   v_cache, num_slots, flags, stream, &nf);
 }
 
 // ---- FP8 weights for a library GEMM (many rows, prefill) ----

@@ -587,6 +587,37 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
     return out
 
 
+def row_sumsq(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Partial sums of squares of (T, H) bf16 rows for a folded-RMSNorm
+    consumer: out[g, t] = sum of x[t, 16 g : 16 g + 16]^2, float32 (H / 16, T)
+    (C ABI: nsg_row_sumsq; the layout a producing ``linear(..., residual=,
+    sumsq_out=)`` writes)."""
+    _require_gpu(x, "x")
+    T, H = x.shape
+    if x.dtype != torch.bfloat16 or x.stride(1) != 1:
+        raise ValueError("x must be bf16 rows with unit inner stride")
+    if out is None:
+        out = torch.empty(H // 16, T, dtype=torch.float32, device=x.device)
+    check(_lib().nsg_row_sumsq(x.data_ptr(), x.stride(0), T, H, out.data_ptr(),
+                               _stream_ptr(x.device)), "nsg_row_sumsq")
+    return out
+
+
+def _fold_args(x, sumsq_in, norm_eps, residual, sumsq_out):
+    """C-ABI arguments of the folded RMSNorm (see nsg_linear_fold)."""
+    if sumsq_in is not None and (sumsq_in.dtype != torch.float32 or not sumsq_in.is_contiguous()
+                                 or sumsq_in.shape[1] != x.shape[0]):
+        raise ValueError("sumsq_in must be contiguous float32 (parts, M)")
+    if residual is not None and (residual.dtype != torch.bfloat16 or residual.stride(1) != 1):
+        raise ValueError("residual must be bf16 rows with unit inner stride")
+    if sumsq_out is not None and (sumsq_out.dtype != torch.float32
+                                  or not sumsq_out.is_contiguous()):
+        raise ValueError("sumsq_out must be contiguous float32")
+    return (_ptr(sumsq_in), 0 if sumsq_in is None else sumsq_in.shape[0], x.shape[1],
+            float(norm_eps), _ptr(residual), 0 if residual is None else residual.stride(0),
+            _ptr(sumsq_out))
+
+
 def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """(T, 2I) bf16 [gate | up] -> (T, I) silu(gate) * up (C ABI: nsg_silu_mul)."""
     _require_gpu(gate_up, "gate_up")
@@ -647,7 +678,9 @@ def _check_dequant(w_dequant: torch.Tensor, weight: torch.Tensor) -> None:
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
            swiglu: bool = False, out: torch.Tensor | None = None,
            force: bool = False, w_scale: torch.Tensor | None = None,
-           w_dequant: torch.Tensor | None = None) -> torch.Tensor:
+           w_dequant: torch.Tensor | None = None, sumsq_in: torch.Tensor | None = None,
+           norm_eps: float = 1e-6, residual: torch.Tensor | None = None,
+           sumsq_out: torch.Tensor | None = None) -> torch.Tensor:
     """y = x @ weight.T (+ bias) for bf16 (M, K) rows (C ABI: nsg_linear).
 
     ``swiglu``: weight holds the fused [gate; up] rows (2I, K) and the
@@ -657,13 +690,33 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     library is faster (``nsg_linear_preferred``: many rows, prefill) go to
     hipBLASLt via F.linear (on the dequantised weights), plus the SwiGLU
     kernel; ``force`` runs the HIP kernel whenever it supports the shape
-    (tests)."""
+    (tests).
+
+    Folded RMSNorm (C ABI: nsg_linear_fold; bf16 weights, the HIP kernel
+    only): ``sumsq_in`` (parts, M) float32 makes this the consumer -- x holds
+    un-normalised rows and ``weight`` the norm weight folded into its
+    columns; ``residual`` and ``sumsq_out`` (N / 16, M) make it the producer
+    -- the result is added to ``residual`` in bf16 and written there (when
+    ``out`` is None) with the rows' partial sums of squares."""
     _require_gpu(x, "x")
     M, K = x.shape
     rows = weight.shape[0]
     N = rows // 2 if swiglu else rows
     lib = _lib()
     fp8 = _check_fp8(weight, w_scale, K)
+    if sumsq_in is not None or residual is not None:
+        if fp8 or weight.dtype != torch.bfloat16 or M > lib.nsg_linear_max_rows():
+            raise ValueError("the folded RMSNorm takes bf16 weights and at most "
+                             f"{lib.nsg_linear_max_rows()} rows")
+        if out is None:
+            out = residual if residual is not None else torch.empty(
+                M, N, dtype=torch.bfloat16, device=x.device)
+        check(lib.nsg_linear_fold(x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
+                                  _ptr(bias), out.data_ptr(), out.stride(0), M, N, K,
+                                  LINEAR_SILU_MUL if swiglu else LINEAR_BIAS,
+                                  *_fold_args(x, sumsq_in, norm_eps, residual, sumsq_out),
+                                  _stream_ptr(x.device)), "nsg_linear_fold")
+        return out
     fits = (M <= lib.nsg_linear_max_rows() and K % 64 == 0 and N % 4 == 0 and x.stride(1) == 1
             and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0 and x.dtype == torch.bfloat16)
     # FP8 weights stay on the kernel whenever it fits: the library path would
@@ -709,23 +762,32 @@ def linear_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | N
                    slots: torch.Tensor | None, k_cache: torch.Tensor | None,
                    v_cache: torch.Tensor | None, q_out: torch.Tensor | None = None,
                    force: bool = False, w_scale: torch.Tensor | None = None,
-                   w_dequant: torch.Tensor | None = None) -> torch.Tensor:
+                   w_dequant: torch.Tensor | None = None,
+                   sumsq_in: torch.Tensor | None = None,
+                   norm_eps: float = 1e-6) -> torch.Tensor:
     """q/k/v projection + RoPE + KV-slot write (C ABI: nsg_linear_rope_kv, or
     nsg_linear_rope_kv_fp8 for float8_e4m3fn weights with per-row w_scale).
 
     Same result as ``rope_kv_write(linear(x, weight, bias), ...)``; at row
     counts where the library GEMM is the faster projection (prefill), or for
     shapes the fused kernel does not take, it runs exactly that pair.
-    Returns rotated q (M, Hq, D)."""
+    ``sumsq_in``: the folded RMSNorm's consumer side (nsg_linear_rope_kv_fold,
+    see ``linear``; the fused kernel only).  Returns rotated q (M, Hq, D)."""
     _require_gpu(x, "x")
     M, K = x.shape
     lib = _lib()
     N = weight.shape[0]
     fp8 = _check_fp8(weight, w_scale, K)
+    if sumsq_in is not None and (fp8 or M > lib.nsg_linear_max_rows()):
+        raise ValueError("the folded RMSNorm takes bf16 weights and at most "
+                         f"{lib.nsg_linear_max_rows()} rows")
     fits = (M <= lib.nsg_linear_max_rows() and K % 64 == 0 and head_dim in (64, 128)
             and N == (num_qo_heads + 2 * num_kv_heads) * head_dim and x.stride(1) == 1
             and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0 and x.dtype == torch.bfloat16)
-    if not fits or not (force or fp8 or lib.nsg_linear_preferred(M, N, K)):
+    if sumsq_in is not None and not fits:
+        raise ValueError("the folded RMSNorm needs the fused kernel's shapes")
+    if not fits or not (force or fp8 or sumsq_in is not None
+                        or lib.nsg_linear_preferred(M, N, K)):
         qkv = linear(x, weight, bias, w_scale=w_scale, w_dequant=w_dequant)
         return rope_kv_write(qkv, num_qo_heads, num_kv_heads, head_dim, positions, cos_table,
                              sin_table, slots, k_cache, v_cache, q_out)
@@ -745,7 +807,12 @@ def linear_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | N
     tail = (num_qo_heads, num_kv_heads, head_dim, positions.data_ptr(), cos_table.data_ptr(),
             sin_table.data_ptr(), cos_table.shape[0], _ptr(slots), q_out.data_ptr(),
             _ptr(k_cache), _ptr(v_cache), num_slots, None, _stream_ptr(x.device))
-    if fp8:
+    if sumsq_in is not None:
+        check(lib.nsg_linear_rope_kv_fold(x.data_ptr(), x.stride(0), weight.data_ptr(),
+                                          weight.stride(0), _ptr(bias), M, K, *tail[:-1],
+                                          *_fold_args(x, sumsq_in, norm_eps, None, None)[:4],
+                                          tail[-1]), "nsg_linear_rope_kv_fold")
+    elif fp8:
         check(lib.nsg_linear_rope_kv_fp8(x.data_ptr(), x.stride(0), weight.data_ptr(),
                                          weight.stride(0), w_scale.data_ptr(), _ptr(bias), M, K,
                                          *tail), "nsg_linear_rope_kv_fp8")

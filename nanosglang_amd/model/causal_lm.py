@@ -20,7 +20,14 @@ MI355X-side choices:
   the HIP verify-attention kernel behind
   ``BatchPrefillWithPagedKVCacheWrapper``;
 * RMSNorm (and residual add + RMSNorm) and the SwiGLU gate are HIP kernels
-  with the reference's fp32-variance arithmetic (:142-154, :482);
+  with the reference's fp32-variance arithmetic (:142-154, :482); with bf16
+  weights, hidden <= 1024 and at most 160 rows (decode / verify steps), the
+  two norms of every layer run inside the linears around them instead: the
+  norm weight is folded into the q/k/v and gate/up weight columns once, the
+  o_proj and down_proj kernels add their result to the residual stream and
+  write the rows' partial sums of squares, and the q/k/v and gate/up kernels
+  scale each row by rsqrt(mean(x^2) + eps) before their epilogues -- two
+  launches fewer per layer;
 * a draft made of the first ``n`` layers plus the shared embedding, final
   norm and lm_head is ``forward_packed(..., num_layers=n)`` on the same
   weights.
@@ -123,6 +130,22 @@ class CausalLM:
             self.norm = d(weights["norm"])
         self.lm_head = self.embed  # tie_word_embeddings
         self.rope_cos, self.rope_sin = rope_tables(c, self.device)
+        self._fold = self._fold_norm_weights()
+
+    def _fold_norm_weights(self) -> bool:
+        """RMSNorm folded into the linears after it (bf16 weights, hidden a
+        multiple of 16 and at most 1024): each layer gets copies of its q/k/v
+        and gate/up weights with its norm weight folded into their columns,
+        ``qkv_g`` / ``gate_up_g`` = bf16(w_ln[k] * W[n, k]); the forward then
+        runs the folded path (``forward_packed``).  Returns whether it did."""
+        H = self.config.hidden_size
+        if self.dtype != torch.bfloat16 or H % 16 or H > 1024:
+            return False
+        for L in self.layers:
+            L["qkv_g"] = (L["qkv"].float() * L["ln1"].float()[None, :]).to(torch.bfloat16)
+            L["gate_up_g"] = (L["gate_up"].float() * L["ln2"].float()[None, :]).to(torch.bfloat16)
+        self._ones = torch.ones(H, device=self.device, dtype=torch.bfloat16)
+        return True
 
     def quantize_fp8(self, resident_dequant: bool = False) -> "CausalLM":
         """FP8 (E4M3) weights for every decoder layer's q/k/v, o_proj,
@@ -139,6 +162,12 @@ class CausalLM:
         HBM."""
         from .quantization import fp8_quantize_rows
         c = self.config
+        # FP8 weights keep the norms as kernels of their own (a per-row FP8
+        # scale cannot absorb a per-column norm weight)
+        self._fold = False
+        for L in self.layers:
+            L.pop("qkv_g", None)
+            L.pop("gate_up_g", None)
         Hq, Hkv, D, I = (c.num_attention_heads, c.num_key_value_heads, c.head_dim,
                          c.intermediate_size)
         for L in self.layers:
@@ -175,25 +204,49 @@ class CausalLM:
         nl = self.num_layers if num_layers is None else num_layers
         eps = c.rms_norm_eps
         residual = F.embedding(input_ids, self.embed)    # owned: updated in place below
-        x = None
-        for li in range(nl):
-            L = self.layers[li]
-            # residual += x (causal_lm.py:505, 531), then RMSNorm -- one kernel
-            h = kernels.rmsnorm(residual if x is None else x, L["ln1"], eps,
-                                residual=None if x is None else residual)
-            q = kernels.linear_rope_kv(h, L["qkv"], L["qkv_b"], Hq, Hkv, D, positions,
-                                       self.rope_cos, self.rope_sin, write_indices,
-                                       k_pool[li], v_pool[li], w_scale=L.get("qkv_s"),
-                                       w_dequant=L.get("qkv_d"))
-            attn = attn_wrapper.run(q, (k_pool[li], v_pool[li]))
-            x = kernels.linear(attn.view(-1, Hq * D), L["o"], w_scale=L.get("o_s"),
-                               w_dequant=L.get("o_d"))
-            h = kernels.rmsnorm(x, L["ln2"], eps, residual=residual)   # causal_lm.py:147-154
-            x = kernels.linear(kernels.linear(h, L["gate_up"], swiglu=True,
-                                              w_scale=L.get("gate_up_s"),
-                                              w_dequant=L.get("gate_up_d")),
-                               L["down"], w_scale=L.get("down_s"), w_dequant=L.get("down_d"))
-        h = kernels.rmsnorm(x, self.norm, eps, residual=residual)
+        if self._fold and input_ids.shape[0] <= kernels._lib().nsg_linear_max_rows():
+            # folded norms: residual += o_proj(.) and += down_proj(.) in those
+            # kernels, which also write the rows' partial sums of squares
+            # (ssb, ssa); q/k/v and gate/up read them (causal_lm.py:505-531)
+            ssa = kernels.row_sumsq(residual)
+            ssb = torch.empty_like(ssa)
+            for li in range(nl):
+                L = self.layers[li]
+                q = kernels.linear_rope_kv(residual, L["qkv_g"], L["qkv_b"], Hq, Hkv, D,
+                                           positions, self.rope_cos, self.rope_sin,
+                                           write_indices, k_pool[li], v_pool[li],
+                                           sumsq_in=ssa, norm_eps=eps)
+                attn = attn_wrapper.run(q, (k_pool[li], v_pool[li]))
+                kernels.linear(attn.view(-1, Hq * D), L["o"], residual=residual, sumsq_out=ssb)
+                g = kernels.linear(residual, L["gate_up_g"], swiglu=True, sumsq_in=ssb,
+                                   norm_eps=eps)
+                kernels.linear(g, L["down"], residual=residual, sumsq_out=ssa)
+            h = kernels.rmsnorm(residual, self.norm, eps)
+        else:
+            # separate norm kernels; with folded weights (many rows: prefill)
+            # the norms run with unit weights
+            qkv_k, gu_k = ("qkv_g", "gate_up_g") if self._fold else ("qkv", "gate_up")
+            x = None
+            for li in range(nl):
+                L = self.layers[li]
+                ln1, ln2 = (self._ones, self._ones) if self._fold else (L["ln1"], L["ln2"])
+                # residual += x (causal_lm.py:505, 531), then RMSNorm -- one kernel
+                h = kernels.rmsnorm(residual if x is None else x, ln1, eps,
+                                    residual=None if x is None else residual)
+                q = kernels.linear_rope_kv(h, L[qkv_k], L["qkv_b"], Hq, Hkv, D, positions,
+                                           self.rope_cos, self.rope_sin, write_indices,
+                                           k_pool[li], v_pool[li], w_scale=L.get("qkv_s"),
+                                           w_dequant=L.get("qkv_d"))
+                attn = attn_wrapper.run(q, (k_pool[li], v_pool[li]))
+                x = kernels.linear(attn.view(-1, Hq * D), L["o"], w_scale=L.get("o_s"),
+                                   w_dequant=L.get("o_d"))
+                h = kernels.rmsnorm(x, ln2, eps, residual=residual)   # causal_lm.py:147-154
+                x = kernels.linear(kernels.linear(h, L[gu_k], swiglu=True,
+                                                  w_scale=L.get("gate_up_s"),
+                                                  w_dequant=L.get("gate_up_d")),
+                                   L["down"], w_scale=L.get("down_s"),
+                                   w_dequant=L.get("down_d"))
+            h = kernels.rmsnorm(x, self.norm, eps, residual=residual)
         if logit_indices is not None:
             h = h[logit_indices]
         return kernels.linear(h, self.lm_head)

@@ -416,7 +416,7 @@ int32_t nsg_linear_rope_kv(const void* x, int64_t ldx, const void* w, int64_t ld
  *    consumer: q/k/v with RoPE, or gate/up with SwiGLU) takes the
  *    un-normalised rows x and scales row m of x W'^T by
  *    rsqrt(S_m / norm_dim + eps) before its epilogue, where S_m, the sum of
- *    squares of x's row m, arrives as sumsq_parts partial sums
+ *    squares of x's row m, arrives as sumsq_parts (1 .. 64) partial sums
  *    sumsq_in[c * M + m] added in a fixed order;
  *  - the linear before it (the producer: o_proj, down_proj, bias epilogue)
  *    adds its result to the residual stream in bf16 (y = bf16(residual +

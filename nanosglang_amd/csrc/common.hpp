@@ -126,4 +126,33 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// 32-bit LDS address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Max / sum over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four 16-lane groups
+// of a 16 x 16 MFMA result that share a row or column) with gfx950's row
+// swaps, which stay in the VALU:
+// v_permlane32_swap with both operands x leaves lane l holding x[l % 32] in
+// the first result and x[l % 32 + 32] in the second, v_permlane16_swap the
+// same for the even and odd 16-lane rows.  Sums pair the same two lanes in
+// both halves, so every lane ends with the same value.
+__device__ __forceinline__ float max_xor16_32(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_xor16_32(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 }  // namespace nsg

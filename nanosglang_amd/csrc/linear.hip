@@ -24,6 +24,7 @@
 //   fused [gate; up] rows, and y = bf16(bf16(silu(bf16(g))) * bf16(u)), the
 //   rounding order of F.silu(gate) * up on bf16 tensors (causal_lm.py:482).
 #include <algorithm>
+#include <cstddef>
 #include <type_traits>
 
 #include "common.hpp"
@@ -85,7 +86,63 @@ struct LinParams {
 };
 
 
-enum { kEpiBias = 0, kEpiSilu = 1, kEpiRope = 2 };
+// The folded-RMSNorm fields of LinParams (its last 48 bytes), read from the
+// kernel argument segment (the kernels here take one LinParams, at offset
+// 0) by scalar loads issued where the call is and waited for at once.  The
+// residual and sumsq_out pointers are accessed through the global address
+// space (GlobalPtr): through a generic pointer of unknown origin the
+// compiler emits flat accesses, which its wait-count pass must also take
+// for LDS accesses, and every ds_bpermute of the K sweep then waits for
+// every load in flight.
+#define NSG_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ NSG_GLOBAL T* global_ptr(uint64_t addr) {
+  return (NSG_GLOBAL T*)addr;
+}
+struct FoldArgs {
+  const float* sumsq_in;
+  int parts;
+  int dim;
+  float eps;
+  uint64_t residual;   // bf16 rows, ldr elements apart
+  int64_t ldr;
+  uint64_t sumsq_out;  // float
+};
+typedef uint32_t u32x8_t __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kFoldOff = offsetof(LinParams, sumsq_in);
+static_assert(offsetof(LinParams, sumsq_parts) == kFoldOff + 8 &&
+                  offsetof(LinParams, norm_dim) == kFoldOff + 12 &&
+                  offsetof(LinParams, norm_eps) == kFoldOff + 16 &&
+                  offsetof(LinParams, residual) == kFoldOff + 24 &&
+                  offsetof(LinParams, ldr) == kFoldOff + 32 &&
+                  offsetof(LinParams, sumsq_out) == kFoldOff + 40 &&
+                  sizeof(LinParams) == kFoldOff + 48,
+              "FoldArgs mirrors the tail of LinParams");
+__device__ __forceinline__ FoldArgs fold_args_here() {
+  u32x8_t a;
+  u32x4_t b;
+  asm volatile("s_load_dwordx8 %0, %2, %3\n\ts_load_dwordx4 %1, %2, %4\n\ts_waitcnt lgkmcnt(0)"
+               : "=&s"(a), "=&s"(b)
+               : "s"(__builtin_amdgcn_kernarg_segment_ptr()), "n"(kFoldOff), "n"(kFoldOff + 32));
+  FoldArgs f;
+  f.sumsq_in = reinterpret_cast<const float*>(((uint64_t)a[1] << 32) | a[0]);
+  f.parts = (int)a[2];
+  f.dim = (int)a[3];
+  f.eps = __uint_as_float(a[4]);
+  f.residual = ((uint64_t)a[7] << 32) | a[6];
+  f.ldr = (int64_t)(((uint64_t)b[1] << 32) | b[0]);
+  f.sumsq_out = ((uint64_t)b[3] << 32) | b[2];
+  return f;
+}
+
+// kEpiRes: the bias epilogue of a folded-RMSNorm producer (residual add and
+// partial sums of squares, see LinParams); kEpiSiluN / kEpiRopeN: the SwiGLU
+// and RoPE epilogues of a folded-RMSNorm consumer (rows scaled first).
+enum { kEpiBias = 0, kEpiSilu = 1, kEpiRope = 2, kEpiRes = 3, kEpiSiluN = 4, kEpiRopeN = 5 };
+constexpr bool epi_silu(int e) { return e == kEpiSilu || e == kEpiSiluN; }
+constexpr bool epi_rope(int e) { return e == kEpiRope || e == kEpiRopeN; }
+constexpr bool epi_norm(int e) { return e == kEpiSiluN || e == kEpiRopeN; }
 
 __device__ __forceinline__ float bf16_round(float x) {
   return bf16_bits_to_float(float_to_bf16_bits(x));
@@ -114,8 +171,8 @@ __device__ __forceinline__ u32x4 dequant_fp8x8(u32x2 v, float s) {
 
 template <int MT, int MG, int NT, int NW, int EPI, bool W8 = false>
 __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
-  static_assert(EPI != kEpiSilu || NT % 2 == 0, "SwiGLU pairs gate and up tiles");
-  constexpr int NP = EPI == kEpiSilu ? 2 : 1;  // physical tiles reduced together
+  static_assert(!epi_silu(EPI) || NT % 2 == 0, "SwiGLU pairs gate and up tiles");
+  constexpr int NP = epi_silu(EPI) ? 2 : 1;  // physical tiles reduced together
   __shared__ floatx4 red[MG][NP][NW][MT][64];
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -158,10 +215,10 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     int row;
-    if constexpr (EPI == kEpiSilu) {
+    if constexpr (epi_silu(EPI)) {
       const int col_tile = tile * (NT / 2) + (nt >> 1);
       row = ((nt & 1) ? p.N : 0) + col_tile * 16 + lrow;
-    } else if constexpr (EPI == kEpiRope) {
+    } else if constexpr (epi_rope(EPI)) {
       // tile = (head, s): columns 16 s .. + 16 of the head and their RoPE
       // partners head_dim / 2 further on
       const int tph = p.head_dim / 32;  // tiles per half head
@@ -256,7 +313,7 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
   // j * threads is row m = idx / 16, pair i = 16 s + idx % 16; rows past M
   // are clamped and not stored.  The loads go before the K sweep, so that
   // their latency (position, then cos / sin at that position) hides under it.
-  constexpr bool kRope = EPI == kEpiRope;
+  constexpr bool kRope = epi_rope(EPI);
   constexpr int kThreads = NW * 64;
   constexpr int kItems = MT * 16 * 16;
   constexpr int kIpt = kRope ? (kItems + kThreads - 1) / kThreads : 1;  // items per thread
@@ -293,33 +350,63 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
   // before the current chunk's MFMAs.
   const int n = (nchunks - wave + NW - 1) / NW;
   if (n > 0) load(wave, wa, xa);
+  // Folded RMSNorm (producer): the residual values this thread adds in the
+  // epilogue (its items there, rows and columns clamped), loaded before the
+  // K sweep so that their latency hides under it, but after the first
+  // chunk's loads.  The fold arguments (here and in the consumer's copy
+  // wave below) are read with explicit scalar loads issued after the first
+  // chunk's: as ordinary argument reads the compiler hoists them to the
+  // kernel's start, where every wave's first chunk waits for them.
+  __builtin_amdgcn_sched_barrier(0);
+  constexpr bool kRes = EPI == kEpiRes;
+  constexpr bool kNorm = epi_norm(EPI);
+  constexpr int kEpiIt = (MT + NW - 1) / NW;     // epilogue items per thread and tile
+  FoldArgs fa{};
+  u32x2 e_res[kRes ? NT : 1][kEpiIt];
+  if constexpr (kRes) {
+    fa = fold_args_here();
+#pragma unroll
+    for (int t0 = 0; t0 < NT; ++t0)
+#pragma unroll
+      for (int it = 0; it < kEpiIt; ++it) {
+        const int idx = min((int)threadIdx.x + it * MG * NW * 64, MG * MT * 64 - 1);
+        const int l = idx & 63;
+        const int m = min((idx / (MT * 64) * MT + (idx >> 6) % MT) * 16 + (l & 15), M - 1);
+        const int c = min((tile * NT + t0) * 16 + 4 * (l >> 4), p.N - 4);
+        e_res[t0][it] = *global_ptr<const u32x2>(fa.residual + 2 * ((int64_t)(m0 + m) * fa.ldr + c));
+      }
+  }
   // Folded RMSNorm (consumer): the scale of each of this workgroup's rows,
-  // summed from the producer's partials (in a fixed order) while the first
-  // chunk's loads are in flight, and kept in LDS for the epilogue.
-  // Wave 0 does it: row r of the R rows on R-lane groups of the wave, each
-  // lane summing every (64 / R)-th partial (at most kMaxSumsqParts in all,
-  // every load issued before the first add), then an xor butterfly over the
-  // row's lanes -- one fixed order, so the scale is the same on every call.
+  // from the producer's partial sums of squares, kept in LDS for the
+  // epilogue.  The last wave copies the partials into LDS, and after its K
+  // sweep sums them in one fixed order, so the scale is the same on every
+  // call: row r of the R rows on R-lane groups, each lane summing every
+  // (64 / R)-th partial, then an xor butterfly over the row's lanes.  The
+  // copies are issued in asm, unseen by the compiler's wait-count pass:
+  // through the builtin, that pass takes every later LDS operation of the K
+  // sweep (the ds_bpermute shuffles) for a read of the copied words and
+  // waits for every load in flight before it.  Unseen, they only make the
+  // pass's wait for the first chunk wait for them as well.  (s_nop: the one
+  // wait state an LDS DMA needs after an SALU write of M0.)
   constexpr int R = MG * MT * 16;
   static_assert(R <= 64 && 64 % R == 0, "rows of a workgroup on one wave");
   constexpr int LPR = 64 / R;                    // lanes per row
   constexpr int PPL = kMaxSumsqParts / LPR;      // partials per lane
   __shared__ float rscale[R];
-  if (p.sumsq_in && wid == 0) {
-    const int r = lane % R;
-    const int m = m0 + min(r, M - 1);
-    float part[PPL];
+  __shared__ float spart[kNorm ? PPL : 1][64];
+  const bool copy_wave = kNorm && wid == MG * NW - 1;
+  if (copy_wave) {
+    fa = fold_args_here();
+    const int m = m0 + min(lane % R, M - 1);
 #pragma unroll
     for (int j = 0; j < PPL; ++j) {
-      const int c = lane / R + LPR * j;
-      part[j] = c < p.sumsq_parts ? p.sumsq_in[(int64_t)c * p.M + m] : 0.f;
+      if (LPR * j >= fa.parts) break;  // wave-uniform
+      const int c = min(lane / R + LPR * j, fa.parts - 1);
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+                   :
+                   : "s"(lds_addr(&spart[j][0])), "v"(fa.sumsq_in + (int64_t)c * p.M + m)
+                   : "memory", "m0");
     }
-    float ssum = 0.f;
-#pragma unroll
-    for (int j = 0; j < PPL; ++j) ssum += part[j];
-#pragma unroll
-    for (int o = R; o < 64; o <<= 1) ssum += __shfl_xor(ssum, o, 64);
-    if (lane < R) rscale[r] = 1.f / sqrtf(ssum / (float)p.norm_dim + p.norm_eps);
   }
 
   if constexpr (kRope) {
@@ -354,7 +441,20 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
     mma(wa, xa);
   }
 
-  if constexpr (EPI == kEpiRope) {
+  if (copy_wave) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the copies above (the sweep's loads are done)
+    float ssum = 0.f;
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) {
+      const float v = spart[j][lane];
+      ssum += lane / R + LPR * j < fa.parts ? v : 0.f;
+    }
+#pragma unroll
+    for (int o = R; o < 64; o <<= 1) ssum += __shfl_xor(ssum, o, 64);
+    if (lane < R) rscale[lane] = 1.f / sqrtf(ssum / (float)fa.dim + fa.eps);
+  }
+
+  if constexpr (kRope) {
     // ---- 16 rotation pairs of one head for this row group ----
     // 1. partial sums to LDS; 2. reduce over the waves, add the bias, round
     // to bf16 (the projection's output); 3. rotate q and k heads with
@@ -382,7 +482,7 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
         const uint2 bb = e_bias[j];
         const float b4[4] = {bf16_bits_to_float(bb.x & 0xffffu), bf16_bits_to_float(bb.x >> 16),
                              bf16_bits_to_float(bb.y & 0xffffu), bf16_bits_to_float(bb.y >> 16)};
-        if (p.sumsq_in) sum *= rscale[mt * 16 + (l & 15)];
+        if constexpr (kNorm) sum *= rscale[mt * 16 + (l & 15)];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           hv[mt * 16 + (l & 15)][q * 16 + 4 * (l >> 4) + i] = bf16_round(sum[i] + b4[i]);
@@ -439,7 +539,10 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) red[grp][q][wave][mt][lane] = acc[t0 + q][mt];
     __syncthreads();
-    for (int idx = threadIdx.x; idx < MG * MT * 64; idx += MG * NW * 64) {
+#pragma unroll
+    for (int it = 0; it < kEpiIt; ++it) {
+      const int idx = threadIdx.x + it * MG * NW * 64;
+      if (idx >= MG * MT * 64) continue;  // wave-uniform
       const int g = idx / (MT * 64);
       const int mt = (idx >> 6) % MT;
       const int l = idx & 63;
@@ -452,14 +555,14 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
         for (int w = 1; w < NW; ++w) s[q] += red[g][q][w][mt][l];
       }
       int n;
-      if constexpr (EPI == kEpiSilu)
+      if constexpr (epi_silu(EPI))
         n = (tile * (NT / 2) + t0 / 2) * 16 + 4 * (l >> 4);
       else
         n = (tile * NT + t0) * 16 + 4 * (l >> 4);
       const bool ok = m < M && n < p.N;
       float v[4];
-      if constexpr (EPI == kEpiSilu) {
-        if (p.sumsq_in) {
+      if constexpr (epi_silu(EPI)) {
+        if constexpr (kNorm) {
 #pragma unroll
           for (int q = 0; q < NP; ++q) s[q] *= rscale[m];
         }
@@ -479,13 +582,13 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
           v[2] += bf16_bits_to_float(b[1] & 0xffff);
           v[3] += bf16_bits_to_float(b[1] >> 16);
         }
-        if (p.residual) {
+        if constexpr (kRes) {
           // producer of a folded RMSNorm: the bf16 residual add, then the
           // partial sum of squares of the 16 columns n & ~15 .. + 15 of row
           // m (the four lanes l, l ^ 16, l ^ 32, l ^ 48 hold them)
           float sq = 0.f;
           if (ok) {
-            const u32x2 r = *reinterpret_cast<const u32x2*>(p.residual + (int64_t)(m0 + m) * p.ldr + n);
+            const u32x2 r = e_res[t0][it];
             const float rv[4] = {bf16_bits_to_float(r[0] & 0xffff), bf16_bits_to_float(r[0] >> 16),
                                  bf16_bits_to_float(r[1] & 0xffff), bf16_bits_to_float(r[1] >> 16)};
 #pragma unroll
@@ -494,9 +597,8 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
               sq = __builtin_fmaf(v[i], v[i], sq);
             }
           }
-          sq += __shfl_xor(sq, 16, 64);
-          sq += __shfl_xor(sq, 32, 64);
-          if (ok && (l >> 4) == 0) p.sumsq_out[(int64_t)(n >> 4) * p.M + m0 + m] = sq;
+          sq = sum_xor16_32(sq);
+          if (ok && (l >> 4) == 0) *global_ptr<float>(fa.sumsq_out + 4 * ((int64_t)(n >> 4) * p.M + m0 + m)) = sq;
         }
       }
       if (!ok) continue;
@@ -513,16 +615,18 @@ template <int MT, int MG, int NT, int NW, int EPI>
 int32_t launch_cfg(LinParams p, hipStream_t s) {
   constexpr int kRows = MG * MT * 16;  // rows per workgroup
   p.row_groups = p.M > kRows ? (p.M + kRows - 1) / kRows : 1;
-  if (p.w8) {
-    const int cols_per_wg = 16 * (EPI == kEpiSilu ? NT / 2 : NT);
-    p.col_tiles = (p.N + cols_per_wg - 1) / cols_per_wg;
-    int grid = p.col_tiles;
-    if (p.row_groups > 1) grid = p.row_groups * 8 * ((p.col_tiles + 7) / 8);
-    hipLaunchKernelGGL((linear_kernel<MT, MG, NT, NW, EPI, true>), dim3(grid), dim3(MG * NW * 64),
-                       0, s, p);
-    return launch_status("linear_kernel");
+  if constexpr (!epi_norm(EPI) && EPI != kEpiRes) {  // the folded norm takes bf16 weights only
+    if (p.w8) {
+      const int cols_per_wg = 16 * (epi_silu(EPI) ? NT / 2 : NT);
+      p.col_tiles = (p.N + cols_per_wg - 1) / cols_per_wg;
+      int grid = p.col_tiles;
+      if (p.row_groups > 1) grid = p.row_groups * 8 * ((p.col_tiles + 7) / 8);
+      hipLaunchKernelGGL((linear_kernel<MT, MG, NT, NW, EPI, true>), dim3(grid),
+                         dim3(MG * NW * 64), 0, s, p);
+      return launch_status("linear_kernel");
+    }
   }
-  const int cols_per_wg = 16 * (EPI == kEpiSilu ? NT / 2 : NT);
+  const int cols_per_wg = 16 * (epi_silu(EPI) ? NT / 2 : NT);
   p.col_tiles = (p.N + cols_per_wg - 1) / cols_per_wg;
   int grid = p.col_tiles;
   if (p.row_groups > 1) grid = p.row_groups * 8 * ((p.col_tiles + 7) / 8);
@@ -541,7 +645,7 @@ constexpr int kWideN = 65536;
 
 template <int EPI>
 int32_t launch_epi(LinParams p, hipStream_t s) {
-  if constexpr (EPI == kEpiSilu) {
+  if constexpr (epi_silu(EPI)) {
     // NT counts gate and up tiles: NT = 2 is one output column tile
     if (p.M <= 16) return launch_cfg<1, 1, 2, 2, EPI>(p, s);
     if (p.M <= 32) return launch_cfg<2, 1, 2, 2, EPI>(p, s);
@@ -550,15 +654,17 @@ int32_t launch_epi(LinParams p, hipStream_t s) {
     if (p.M <= 128) return launch_cfg<2, 1, 2, 4, EPI>(p, s);
     return launch_cfg<2, 1, 4, 2, EPI>(p, s);
   } else {
-    if (p.N >= kWideN) {  // lm_head
-      if (p.M == 1) return launch_cfg<1, 1, 1, 8, EPI>(p, s);
-      if (p.M <= 8) return launch_cfg<1, 1, 2, 8, EPI>(p, s);
-      if (p.K >= 2048) {  // long rows (8B-class lm_head): eight column tiles
-        if (p.M <= 16) return launch_cfg<2, 1, 8, 4, EPI>(p, s);
-        return launch_cfg<2, 1, 8, 2, EPI>(p, s);
+    if constexpr (EPI == kEpiBias) {
+      if (p.N >= kWideN) {  // lm_head
+        if (p.M == 1) return launch_cfg<1, 1, 1, 8, EPI>(p, s);
+        if (p.M <= 8) return launch_cfg<1, 1, 2, 8, EPI>(p, s);
+        if (p.K >= 2048) {  // long rows (8B-class lm_head): eight column tiles
+          if (p.M <= 16) return launch_cfg<2, 1, 8, 4, EPI>(p, s);
+          return launch_cfg<2, 1, 8, 2, EPI>(p, s);
+        }
+        if (p.M <= 16) return launch_cfg<1, 1, 4, 1, EPI>(p, s);
+        return launch_cfg<2, 1, 4, 2, EPI>(p, s);
       }
-      if (p.M <= 16) return launch_cfg<1, 1, 4, 1, EPI>(p, s);
-      return launch_cfg<2, 1, 4, 2, EPI>(p, s);
     }
     if (p.M <= 16) return launch_cfg<1, 1, 1, 8, EPI>(p, s);
     if (p.M <= 128) return launch_cfg<2, 1, 1, 4, EPI>(p, s);
@@ -568,9 +674,10 @@ int32_t launch_epi(LinParams p, hipStream_t s) {
 
 // RoPE epilogue: a workgroup per (head, 16 rotation pairs) -- two column
 // tiles -- and row group.
+template <int EPI>
 int32_t launch_rope(LinParams p, hipStream_t s) {
-  if (p.M <= 16) return launch_cfg<1, 1, 2, 8, kEpiRope>(p, s);
-  return launch_cfg<2, 1, 2, 8, kEpiRope>(p, s);
+  if (p.M <= 16) return launch_cfg<1, 1, 2, 8, EPI>(p, s);
+  return launch_cfg<2, 1, 2, 8, EPI>(p, s);
 }
 
 }  // namespace
@@ -613,9 +720,11 @@ struct NormFold {
 };
 
 // Checks the folded-norm arguments and copies them into p.
-int32_t apply_fold(LinParams& p, const NormFold* nf, int32_t M, int32_t N, bool producer_ok) {
+int32_t apply_fold(LinParams& p, const NormFold* nf, int32_t N, bool consumer_ok,
+                   bool producer_ok) {
   if (!nf) return NSG_OK;
   if (nf->sumsq_in) {
+    NSG_CHECK_ARG(consumer_ok, "the row scale takes the SwiGLU or RoPE epilogue");
     NSG_CHECK_ARG(nf->parts >= 1 && nf->parts <= kMaxSumsqParts && nf->dim > 0 && nf->eps >= 0.f,
                   "folded norm: %d partials (1 .. %d), dim %d, eps %g", nf->parts, kMaxSumsqParts,
                   nf->dim, (double)nf->eps);
@@ -634,7 +743,6 @@ int32_t apply_fold(LinParams& p, const NormFold* nf, int32_t M, int32_t N, bool 
     p.ldr = nf->ldr;
     p.sumsq_out = nf->sumsq_out;
   }
-  (void)M;
   return NSG_OK;
 }
 
@@ -678,9 +786,12 @@ int32_t linear_impl(const void* x, int64_t ldx, const void* w, const void* w8, i
   p.N = N;
   p.K = K;
   p.w_rows = epilogue == NSG_LINEAR_SILU_MUL ? 2 * N : N;
-  if (int32_t rc = apply_fold(p, nf, M, N, epilogue == NSG_LINEAR_BIAS)) return rc;
+  if (int32_t rc = apply_fold(p, nf, N, epilogue == NSG_LINEAR_SILU_MUL, epilogue == NSG_LINEAR_BIAS))
+    return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return epilogue == NSG_LINEAR_SILU_MUL ? launch_epi<kEpiSilu>(p, s) : launch_epi<kEpiBias>(p, s);
+  if (epilogue == NSG_LINEAR_SILU_MUL)
+    return p.sumsq_in ? launch_epi<kEpiSiluN>(p, s) : launch_epi<kEpiSilu>(p, s);
+  return p.residual ? launch_epi<kEpiRes>(p, s) : launch_epi<kEpiBias>(p, s);
 }
 
 int32_t rope_impl(const void* x, int64_t ldx, const void* w, const void* w8, int64_t ldw,
@@ -740,8 +851,9 @@ int32_t rope_impl(const void* x, int64_t ldx, const void* w, const void* w8, int
   p.vc = static_cast<bf16*>(v_cache);
   p.num_slots = num_slots;
   p.flags = flags;
-  if (int32_t rc = apply_fold(p, nf, M, N, false)) return rc;
-  return launch_rope(p, static_cast<hipStream_t>(stream));
+  if (int32_t rc = apply_fold(p, nf, N, true, false)) return rc;
+  return p.sumsq_in ? launch_rope<kEpiRopeN>(p, static_cast<hipStream_t>(stream))
+                    : launch_rope<kEpiRope>(p, static_cast<hipStream_t>(stream));
 }
 
 }  // namespace

@@ -106,29 +106,6 @@ __device__ __forceinline__ void wait_steps(int later) {
   }
 }
 
-// Max / sum over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four lane groups
-// holding one query row) with gfx950's row swaps, which stay in the VALU:
-// v_permlane32_swap with both operands x leaves lane l holding x[l % 32] in
-// the first result and x[l % 32 + 32] in the second, v_permlane16_swap the
-// same for the even and odd 16-lane rows.  Sums pair the same two lanes in
-// both halves, so every lane ends with the same value.
-__device__ __forceinline__ float max_xor16_32(float x) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float sum_xor16_32(float x) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
 // Transposing LDS reads of the V^T fragments, in asm.  Written through the
 // builtin, every such read after a global_load_lds gets a conservative
 // vmcnt(0) from the compiler (it cannot tell the read from the ring slots
@@ -150,10 +127,6 @@ __device__ __forceinline__ void tr_wait(v4i16& lo, v4i16& hi) {
   asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(lo), "+v"(hi) : "n"(N) : "memory");
 }
 
-// 32-bit LDS address of a pointer into __shared__ memory.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
 
 // LDS tile swizzles: 16-byte chunk c of token row t is stored at physical
 // chunk c ^ swz(t).  K fragments read one logical chunk of 16 consecutive

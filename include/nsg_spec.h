@@ -43,7 +43,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 13
+#define NSG_ABI_VERSION 14
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -445,6 +445,21 @@ int32_t nsg_linear_rope_kv_fold(const void* x, int64_t ldx, const void* w, int64
                                 float eps, nsg_stream_t stream);
 int32_t nsg_row_sumsq(const void* x, int64_t ldx, int32_t num_tokens, int32_t hidden,
                       float* sumsq_out, nsg_stream_t stream);
+
+/* Greedy token of each row of the bf16 logits x W^T (+ bias) without
+ * storing them: tokens[m] = the lowest column n at which bf16(x_m . W_n +
+ * bias_n) is largest (-0 and +0 equal), the same value and rounding as the
+ * row nsg_linear writes, the tie rule of sample_token's greedy branch
+ * (torch.argmax, nano_sglang/engine/sampling.py:44-45).  It replaces
+ * lm_head (causal_lm.py:643-645) + the argmax at the draft model's greedy
+ * call site (speculative.py:95-100), whose logits nothing else reads.
+ * M <= nsg_linear_max_rows(), K % 64 == 0, N % 4 == 0, bf16 weights; the
+ * workspace (8-byte aligned, nsg_linear_argmax_workspace_bytes(M, N)) holds
+ * one key per row and workgroup, written before it is read. */
+int64_t nsg_linear_argmax_workspace_bytes(int32_t M, int32_t N);
+int32_t nsg_linear_argmax(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                          const void* bias, int32_t M, int32_t N, int32_t K, void* workspace,
+                          int64_t workspace_bytes, int64_t* tokens, nsg_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Philox4x32-10 uniforms: out[i] = u(seed, stream_id, offset + i) with

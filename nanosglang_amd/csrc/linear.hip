@@ -139,7 +139,12 @@ __device__ __forceinline__ FoldArgs fold_args_here() {
 // kEpiRes: the bias epilogue of a folded-RMSNorm producer (residual add and
 // partial sums of squares, see LinParams); kEpiSiluN / kEpiRopeN: the SwiGLU
 // and RoPE epilogues of a folded-RMSNorm consumer (rows scaled first).
-enum { kEpiBias = 0, kEpiSilu = 1, kEpiRope = 2, kEpiRes = 3, kEpiSiluN = 4, kEpiRopeN = 5 };
+// kEpiArgmax: the bias epilogue's bf16 values, reduced to one (value,
+// column) key per row and workgroup instead of being stored.
+enum {
+  kEpiBias = 0, kEpiSilu = 1, kEpiRope = 2, kEpiRes = 3, kEpiSiluN = 4, kEpiRopeN = 5,
+  kEpiArgmax = 6
+};
 constexpr bool epi_silu(int e) { return e == kEpiSilu || e == kEpiSiluN; }
 constexpr bool epi_rope(int e) { return e == kEpiRope || e == kEpiRopeN; }
 constexpr bool epi_norm(int e) { return e == kEpiSiluN || e == kEpiRopeN; }
@@ -540,6 +545,9 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
     return;
   }
 
+  // kEpiArgmax: this thread's best key over the tiles, per epilogue item
+  constexpr bool kArg = EPI == kEpiArgmax;
+  uint64_t best[kArg ? kEpiIt : 1] = {};
   // cross-wave reduction and epilogue, NP physical tiles at a time.  Lane l
   // of tile (nt, mt) holds y rows m = 16 mt + l % 16, columns 4 (l / 16) + i.
 #pragma unroll
@@ -611,21 +619,80 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
           if (ok && (l >> 4) == 0) *global_ptr<float>(fa.sumsq_out + 4 * ((int64_t)(n >> 4) * p.M + m0 + m)) = sq;
         }
       }
+      if constexpr (kArg) {
+        // key = (order-preserving bits of the bf16 value, ~column): the max
+        // key is the largest value at its lowest column (-0 counts as +0)
+        if (ok) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            uint32_t b = float_to_bf16_bits(v[i]);
+            b = b == 0x8000u ? 0u : b;
+            const uint32_t ord = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+            const uint64_t key = ((uint64_t)ord << 32) | (0xffffffffu - (uint32_t)(n + i));
+            best[it] = key > best[it] ? key : best[it];
+          }
+        }
+        continue;
+      }
       if (!ok) continue;
       *reinterpret_cast<u32x2*>(yg + (int64_t)m * p.ldy + n) =
           u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
     }
     __syncthreads();
   }
+  if constexpr (kArg) {
+    // the four lanes of a row's 16 columns meet, then one lane stores the
+    // row's key for this workgroup's columns: keys[row * col_tiles + tile]
+    uint64_t* keys = reinterpret_cast<uint64_t*>(p.y);
+#pragma unroll
+    for (int it = 0; it < kEpiIt; ++it) {
+      const int idx = threadIdx.x + it * MG * NW * 64;
+      if (idx >= MG * MT * 64) continue;  // wave-uniform
+      const int l = idx & 63;
+      const int m = (idx / (MT * 64) * MT + (idx >> 6) % MT) * 16 + (l & 15);
+      uint64_t k = best[it];
+#pragma unroll
+      for (int o = 16; o < 64; o <<= 1) {
+        const uint64_t other = ((uint64_t)(uint32_t)__shfl_xor((int)(k >> 32), o, 64) << 32) |
+                               (uint32_t)__shfl_xor((int)(uint32_t)k, o, 64);
+        k = other > k ? other : k;
+      }
+      if ((l >> 4) == 0 && m < M) keys[(int64_t)(m0 + m) * p.col_tiles + tile] = k;
+    }
+  }
+}
+
+// Per row, the largest of the lm_head workgroups' keys -> the column (token):
+// one workgroup per row.
+__global__ __launch_bounds__(256) void argmax_keys_kernel(const uint64_t* __restrict__ keys,
+                                                          int tiles, int64_t* __restrict__ out) {
+  const uint64_t* row = keys + (int64_t)blockIdx.x * tiles;
+  uint64_t k = 0;
+  for (int t = threadIdx.x; t < tiles; t += 256) k = row[t] > k ? row[t] : k;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t other = ((uint64_t)(uint32_t)__shfl_xor((int)(k >> 32), o, 64) << 32) |
+                           (uint32_t)__shfl_xor((int)(uint32_t)k, o, 64);
+    k = other > k ? other : k;
+  }
+  __shared__ uint64_t wk[4];
+  if ((threadIdx.x & 63) == 0) wk[threadIdx.x >> 6] = k;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    k = wk[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) k = wk[w] > k ? wk[w] : k;
+    out[blockIdx.x] = (int64_t)(0xffffffffu - (uint32_t)k);
+  }
 }
 
 // Tile shape per row count: more W rows per workgroup as M grows, so that x
 // (read from L2 once per workgroup) stays a small multiple of W's bytes.
 template <int MT, int MG, int NT, int NW, int EPI>
-int32_t launch_cfg(LinParams p, hipStream_t s) {
+int32_t launch_cfg(LinParams& p, hipStream_t s) {
   constexpr int kRows = MG * MT * 16;  // rows per workgroup
   p.row_groups = p.M > kRows ? (p.M + kRows - 1) / kRows : 1;
-  if constexpr (!epi_norm(EPI) && EPI != kEpiRes) {  // the folded norm takes bf16 weights only
+  if constexpr (!epi_norm(EPI) && EPI != kEpiRes && EPI != kEpiArgmax) {  // bf16 weights only
     if (p.w8) {
       const int cols_per_wg = 16 * (epi_silu(EPI) ? NT / 2 : NT);
       p.col_tiles = (p.N + cols_per_wg - 1) / cols_per_wg;
@@ -654,7 +721,7 @@ int32_t launch_cfg(LinParams p, hipStream_t s) {
 constexpr int kWideN = 65536;
 
 template <int EPI>
-int32_t launch_epi(LinParams p, hipStream_t s) {
+int32_t launch_epi(LinParams& p, hipStream_t s) {
   if constexpr (epi_silu(EPI)) {
     // NT counts gate and up tiles: NT = 2 is one output column tile
     if (p.M <= 16) return launch_cfg<1, 1, 2, 2, EPI>(p, s);
@@ -664,7 +731,7 @@ int32_t launch_epi(LinParams p, hipStream_t s) {
     if (p.M <= 128) return launch_cfg<2, 1, 2, 4, EPI>(p, s);
     return launch_cfg<2, 1, 4, 2, EPI>(p, s);
   } else {
-    if constexpr (EPI == kEpiBias) {
+    if constexpr (EPI == kEpiBias || EPI == kEpiArgmax) {
       if (p.N >= kWideN) {  // lm_head
         if (p.M == 1) return launch_cfg<1, 1, 1, 8, EPI>(p, s);
         if (p.M <= 8) return launch_cfg<1, 1, 2, 8, EPI>(p, s);
@@ -685,7 +752,7 @@ int32_t launch_epi(LinParams p, hipStream_t s) {
 // RoPE epilogue: a workgroup per (head, 16 rotation pairs) -- two column
 // tiles -- and row group.
 template <int EPI>
-int32_t launch_rope(LinParams p, hipStream_t s) {
+int32_t launch_rope(LinParams& p, hipStream_t s) {
   if (p.M <= 16) return launch_cfg<1, 1, 2, 8, EPI>(p, s);
   return launch_cfg<2, 1, 2, 8, EPI>(p, s);
 }
@@ -937,6 +1004,55 @@ extern "C" int32_t nsg_linear_rope_kv_fold(
   return rope_impl(x, ldx, w, nullptr, ldw, nullptr, bias, M, K, num_qo_heads, num_kv_heads,
                    head_dim, positions, cos_table, sin_table, max_position, slots, q_out, k_cache,
                    v_cache, num_slots, flags, stream, &nf);
+}
+
+// ---- lm_head + greedy token: argmax of the bf16 logits, never stored ----
+extern "C" int64_t nsg_linear_argmax_workspace_bytes(int32_t M, int32_t N) {
+  if (M <= 0 || N <= 0) return 0;
+  return (int64_t)M * ((N + 15) / 16) * (int64_t)sizeof(uint64_t);
+}
+
+extern "C" int32_t nsg_linear_argmax(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                     const void* bias, int32_t M, int32_t N, int32_t K,
+                                     void* workspace, int64_t workspace_bytes, int64_t* tokens,
+                                     nsg_stream_t stream) {
+  NSG_CHECK_ARG(M >= 0 && N > 0 && K > 0, "M %d, N %d, K %d", M, N, K);
+  if (M == 0) {
+    clear_error();
+    return NSG_OK;
+  }
+  NSG_CHECK_ARG(x && w && workspace && tokens, "null pointer argument");
+  if (M > kMaxMT * 16) {
+    set_error("M %d > %d rows", M, kMaxMT * 16);
+    return NSG_ERR_UNSUPPORTED;
+  }
+  if (K % kChunk != 0 || N % 4 != 0) {
+    set_error("K %d must be a multiple of %d and N %d of 4", K, kChunk, N);
+    return NSG_ERR_UNSUPPORTED;
+  }
+  NSG_CHECK_ARG(ldx >= K && ldw >= K && ldx % 8 == 0 && ldw % 8 == 0 && (uintptr_t)x % 16 == 0 &&
+                    (uintptr_t)w % 16 == 0 && (uintptr_t)bias % 8 == 0 &&
+                    (uintptr_t)workspace % 8 == 0,
+                "x and w rows must be 16-byte aligned, bias and workspace 8-byte");
+  NSG_CHECK_ARG(workspace_bytes >= nsg_linear_argmax_workspace_bytes(M, N),
+                "workspace %lld bytes < %lld", (long long)workspace_bytes,
+                (long long)nsg_linear_argmax_workspace_bytes(M, N));
+  LinParams p{};
+  p.x = static_cast<const bf16*>(x);
+  p.w = static_cast<const bf16*>(w);
+  p.bias = static_cast<const bf16*>(bias);
+  p.y = static_cast<bf16*>(workspace);  // the per-workgroup keys
+  p.ldx = ldx;
+  p.ldw = ldw;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.w_rows = N;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (int32_t rc = launch_epi<kEpiArgmax>(p, s)) return rc;
+  hipLaunchKernelGGL(argmax_keys_kernel, dim3(M), dim3(256), 0, s,
+                     static_cast<const uint64_t*>(workspace), p.col_tiles, tokens);
+  return launch_status("argmax_keys_kernel");
 }
 
 // ---- FP8 weights for a library GEMM (many rows, prefill) ----

@@ -208,6 +208,10 @@ class SpecEngine:
         self._graphs: dict[int, _StepGraph] = {}
         self._accept_ws = kernels.AcceptWorkspace(self.device)
         self._sample_ws = kernels.AcceptWorkspace(self.device)   # the sampler's own
+        # greedy drafts: lm_head + argmax in one pass (kernels.linear_argmax),
+        # the draft logits are never stored; its workspace is written before
+        # it is read, so every call may share it
+        self._argmax_ws = kernels.AcceptWorkspace(self.device)
         self._dummy_block = None
         self._tab = np.zeros((0, 0), np.int32)     # page-table mirror of graph mode
         # decode / verify contexts never exceed the position table: the
@@ -278,6 +282,12 @@ class SpecEngine:
         _, em, _ = kernels.spec_accept(logits.view(B, 1, -1), None, None, u, self.temperature)
         return em[:, 0]
 
+    def _argmax_drafts(self, rows: int) -> bool:
+        """Greedy draft tokens straight from the lm_head kernel (the argmax of
+        the same bf16 logits spec_accept's k = 0 call would take)."""
+        return (self.greedy and self.model.dtype == torch.bfloat16
+                and rows <= kernels._lib().nsg_linear_max_rows())
+
     def _bonus(self, tl: torch.Tensor, u: torch.Tensor | None, workspace=None, out=None):
         """speculative.py:174-182: the bonus after k accepted drafts is
         sample_token(target row k) with top-k / top-p; None without filters
@@ -310,6 +320,7 @@ class SpecEngine:
         self._accept_ws.get(max(lib.nsg_spec_accept_workspace_bytes(self.max_batch, self.k, V),
                                 lib.nsg_spec_accept_workspace_bytes(self.max_batch, 0, V)))
         self._sample_ws.get(lib.nsg_sample_workspace_bytes(self.max_batch, V))
+        self._argmax_ws.get(lib.nsg_linear_argmax_workspace_bytes(self.max_batch, V))
         pool = torch.cuda.graph_pool_handle()
         for bs in graph_batch_sizes(self.max_batch):
             if bs in self._graphs:
@@ -343,6 +354,13 @@ class SpecEngine:
         pool = self._pool()
         tok = A["tok0"]
         for i in range(k):
+            if self._argmax_drafts(bs):
+                m.forward_packed(tok, g.pos[i], pool, g.attn[i], g.slot[i], None,
+                                 self.draft_layers, argmax_out=g.em1[:, 0],
+                                 argmax_ws=self._argmax_ws)
+                g.drafts[:, i].copy_(g.em1[:, 0])
+                tok = g.em1[:, 0]
+                continue
             lg = m.forward_packed(tok, g.pos[i], pool, g.attn[i], g.slot[i], None,
                                   self.draft_layers)
             if g.dlog is not None:
@@ -453,6 +471,14 @@ class SpecEngine:
         for i in range(k):
             self._plan(active, ones, [s + i + 1 for s in starts])
             sl = self._to_dev(self._slots(active, [s + i for s in starts], ones))
+            if self._argmax_drafts(B):
+                tok = self.model.forward_packed(tok, self._to_dev(start_pos + i), self._pool(),
+                                                self.attn, sl, None, self.draft_layers,
+                                                argmax_out=torch.empty(B, dtype=torch.int64,
+                                                                       device=dev),
+                                                argmax_ws=self._argmax_ws)
+                drafts[:, i] = tok
+                continue
             lg = self.model.forward_packed(tok, self._to_dev(start_pos + i), self._pool(),
                                            self.attn, sl, None, self.draft_layers)
             if not self.greedy:

@@ -603,6 +603,34 @@ def row_sumsq(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     return out
 
 
+def linear_argmax(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
+                  out: torch.Tensor | None = None,
+                  workspace: AcceptWorkspace | None = None) -> torch.Tensor:
+    """Greedy token of each row of the bf16 logits x @ weight.T (+ bias),
+    never stored: the lowest column of the row's largest bf16 value -- the
+    argmax of exactly the rows :func:`linear` would return (C ABI:
+    nsg_linear_argmax).  (M,) int64; M up to nsg_linear_max_rows()."""
+    _require_gpu(x, "x")
+    M, K = x.shape
+    N = weight.shape[0]
+    lib = _lib()
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or x.stride(1) != 1 \
+            or weight.stride(1) != 1 or weight.shape[1] != K:
+        raise ValueError("x (M, K) and weight (N, K) must be bf16 rows with unit inner stride")
+    if bias is not None and (bias.dtype != torch.bfloat16 or not bias.is_contiguous()):
+        raise ValueError("bias must be contiguous bf16")
+    if out is None:
+        out = torch.empty(M, dtype=torch.int64, device=x.device)
+    if out.dtype != torch.int64 or not out.is_contiguous() or out.numel() != M:
+        raise ValueError("out must be contiguous int64 (M,)")
+    ws = (workspace or _accept_ws(x.device, "argmax")).get(
+        lib.nsg_linear_argmax_workspace_bytes(M, N))
+    check(lib.nsg_linear_argmax(x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
+                                _ptr(bias), M, N, K, ws.data_ptr(), ws.numel(), out.data_ptr(),
+                                _stream_ptr(x.device)), "nsg_linear_argmax")
+    return out
+
+
 def _fold_args(x, sumsq_in, norm_eps, residual, sumsq_out):
     """C-ABI arguments of the folded RMSNorm (see nsg_linear_fold)."""
     if sumsq_in is not None and (sumsq_in.dtype != torch.float32 or not sumsq_in.is_contiguous()

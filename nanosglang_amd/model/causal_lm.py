@@ -191,12 +191,16 @@ class CausalLM:
     def forward_packed(self, input_ids: torch.Tensor, positions: torch.Tensor, kv_cache,
                        attn_wrapper, write_indices: torch.Tensor,
                        logit_indices: torch.Tensor | None = None,
-                       num_layers: int | None = None) -> torch.Tensor:
+                       num_layers: int | None = None, argmax_out: torch.Tensor | None = None,
+                       argmax_ws=None) -> torch.Tensor:
         """Packed forward over ``T`` tokens of several requests.
 
         kv_cache: (k_cache, v_cache) pools (L, N, P, Hkv, D); attn_wrapper: a
         planned ``BatchPrefillWithPagedKVCacheWrapper``; write_indices: int64
-        flat slots (T,).  Returns logits (len(logit_indices) or T, V)."""
+        flat slots (T,).  Returns logits (len(logit_indices) or T, V), or,
+        with ``argmax_out`` (int64, one per row), each row's greedy token
+        written there (``kernels.linear_argmax``: the logits are never
+        stored)."""
         c = self.config
         Hq, Hkv, D, I = (c.num_attention_heads, c.num_key_value_heads, c.head_dim,
                          c.intermediate_size)
@@ -249,4 +253,6 @@ class CausalLM:
             h = kernels.rmsnorm(x, self.norm, eps, residual=residual)
         if logit_indices is not None:
             h = h[logit_indices]
+        if argmax_out is not None:
+            return kernels.linear_argmax(h, self.lm_head, out=argmax_out, workspace=argmax_ws)
         return kernels.linear(h, self.lm_head)

@@ -412,3 +412,45 @@ def test_fp8linear_module_matches_reference_arithmetic():
     net = torch.nn.ModuleDict({"mlp": torch.nn.Linear(64, 64), "lm_head": torch.nn.Linear(64, 10)})
     quantize_model(net)
     assert isinstance(net["mlp"], FP8Linear) and isinstance(net["lm_head"], torch.nn.Linear)
+
+
+@pytest.mark.parametrize("M", [1, 5, 8, 16, 17, 32, 33, 100, 160])
+@pytest.mark.parametrize("N,K,bias", [(151936, 896, False), (4096, 512, True), (1000, 128, False)])
+def test_linear_argmax_equals_argmax_of_linear(M, N, K, bias):
+    """nsg_linear_argmax: the greedy token of each row is the first-index
+    argmax of exactly the bf16 rows the HIP linear kernel writes (same tile
+    shapes, same accumulation order), bit for bit."""
+    from nanosglang_amd import kernels
+    print(f"case: linear_argmax M={M} N={N} K={K} bias={bias}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(M * 7 + N)
+    x = torch.randn(M, K, generator=g, device="cuda").bfloat16()
+    w = (torch.randn(N, K, generator=g, device="cuda") * K ** -0.5).bfloat16()
+    b = torch.randn(N, generator=g, device="cuda").bfloat16() if bias else None
+    tok = kernels.linear_argmax(x, w, b)
+    y = kernels.linear(x, w, b, force=True)
+    torch.cuda.synchronize()
+    assert torch.equal(tok, y.float().argmax(dim=1))
+
+
+def test_linear_argmax_ties_take_the_lowest_column():
+    """Equal maxima (duplicated weight rows, in one workgroup's columns and in
+    different workgroups', and +0 against -0) resolve to the lowest column,
+    as torch.argmax and the reference's greedy sample_token do."""
+    from nanosglang_amd import kernels
+    print("case: linear_argmax ties", flush=True)
+    N, K, M = 151936, 896, 6
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(M, K, generator=g, device="cuda").bfloat16()
+    w = (torch.randn(N, K, generator=g, device="cuda") * K ** -0.5).bfloat16()
+    # rows 0-1: a large row duplicated at columns 70001 and 9 (other tiles);
+    # rows 2-3: duplicated at 40 and 41 (one tile)
+    big = (x[0].float() * 0.5).bfloat16()
+    w[9] = big
+    w[70001] = big
+    w[41] = (x[2].float() * 0.5).bfloat16()
+    w[40] = w[41]
+    # rows 4-5: x = 0 -> every logit is +0 or -0: the first column wins
+    x[4:] = 0
+    tok = kernels.linear_argmax(x, w).cpu().tolist()
+    torch.cuda.synchronize()
+    assert tok[0] == 9 and tok[2] == 40 and tok[4] == 0 and tok[5] == 0

@@ -43,7 +43,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 14
+#define NSG_ABI_VERSION 15
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -447,7 +447,8 @@ int32_t nsg_row_sumsq(const void* x, int64_t ldx, int32_t num_tokens, int32_t hi
                       float* sumsq_out, nsg_stream_t stream);
 
 /* Greedy token of each row of the bf16 logits x W^T (+ bias) without
- * storing them: tokens[m] = the lowest column n at which bf16(x_m . W_n +
+ * storing them: tokens[m * token_stride] = the lowest column n at which
+ * bf16(x_m . W_n +
  * bias_n) is largest (-0 and +0 equal), the same value and rounding as the
  * row nsg_linear writes, the tie rule of sample_token's greedy branch
  * (torch.argmax, nano_sglang/engine/sampling.py:44-45).  It replaces
@@ -459,7 +460,19 @@ int32_t nsg_row_sumsq(const void* x, int64_t ldx, int32_t num_tokens, int32_t hi
 int64_t nsg_linear_argmax_workspace_bytes(int32_t M, int32_t N);
 int32_t nsg_linear_argmax(const void* x, int64_t ldx, const void* w, int64_t ldw,
                           const void* bias, int32_t M, int32_t N, int32_t K, void* workspace,
-                          int64_t workspace_bytes, int64_t* tokens, nsg_stream_t stream);
+                          int64_t workspace_bytes, int64_t* tokens, int64_t token_stride,
+                          nsg_stream_t stream);
+
+/* Embedding rows: out[r] = table[ids[b * id_stride_b + j * id_stride_j]] for
+ * r = b * per_batch + j (embed_tokens(input_ids), causal_lm.py:613, on an index view
+ * of any strides); ids outside [0, vocab) read the nearest valid row (the
+ * reference's lookup would fault).  With sumsq_out, also the per-16-column
+ * sums of squares of every row in nsg_row_sumsq's layout, for a folded
+ * RMSNorm's first consumer. */
+int32_t nsg_embed_rows(const int64_t* ids, int64_t id_stride_b, int64_t id_stride_j,
+                       int32_t batch, int32_t per_batch, const void* table, int64_t ld_table,
+                       int32_t vocab, int32_t hidden, void* out, int64_t ld_out,
+                       float* sumsq_out, nsg_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Philox4x32-10 uniforms: out[i] = u(seed, stream_id, offset + i) with

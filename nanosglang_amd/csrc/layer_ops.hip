@@ -162,6 +162,42 @@ __global__ __launch_bounds__(kNormThreads) void row_sumsq_kernel(const uint16_t*
   }
 }
 
+// Embedding rows: out[r] = table[ids[b sb + j sj]] for r = b J + j (ids
+// outside [0, vocab) read the nearest valid row), one wave per row, and, when
+// sumsq is given, the row's per-16-column sums of squares
+// sumsq[(c / 16) rows + r] (the layout row_sumsq_kernel writes).
+__global__ __launch_bounds__(kNormThreads) void embed_rows_kernel(
+    const int64_t* __restrict__ ids, int64_t sb, int64_t sj, int J, int rows,
+    const uint16_t* __restrict__ table, int64_t ldt, int vocab, int H,
+    uint16_t* __restrict__ out, int64_t ldo, float* __restrict__ sumsq) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * (kNormThreads / 64) + (threadIdx.x >> 6);
+  if (r >= rows) return;  // wave-uniform
+  const int b = r / J, j = r - b * J;
+  const int64_t id = min(max(ids[b * sb + j * sj], (int64_t)0), (int64_t)vocab - 1);
+  const uint16_t* src = table + id * ldt;
+  uint16_t* dst = out + (int64_t)r * ldo;
+  const int nseg = H >> 3;  // 16-byte segments of a row
+  for (int s0 = 0; s0 < nseg; s0 += 64) {
+    const int sg = s0 + lane;
+    const bool ok = sg < nseg;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(src + min(sg, nseg - 1) * 8);
+    if (ok) *reinterpret_cast<u32x4*>(dst + sg * 8) = v;
+    if (sumsq) {  // kernel-uniform
+      float sq = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float lo = bf16_bits_to_float(v[i] & 0xffffu);
+        const float hi = bf16_bits_to_float(v[i] >> 16);
+        sq = __builtin_fmaf(lo, lo, sq);
+        sq = __builtin_fmaf(hi, hi, sq);
+      }
+      sq += __shfl_xor(sq, 1, 64);
+      if (ok && (sg & 1) == 0) sumsq[(int64_t)(sg >> 1) * rows + r] = sq;
+    }
+  }
+}
+
 // out[t, j] = bf16(bf16(silu(gu[t, j])) * gu[t, I + j]) for j < I.
 __global__ void silu_mul_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ out,
                                 int64_t T, int I) {
@@ -232,6 +268,30 @@ extern "C" int32_t nsg_row_sumsq(const void* x, int64_t ldx, int32_t num_tokens,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), ldx,
                      num_tokens, hidden, sumsq_out);
   return launch_status("row_sumsq_kernel");
+}
+
+extern "C" int32_t nsg_embed_rows(const int64_t* ids, int64_t id_stride_b, int64_t id_stride_j,
+                                  int32_t batch, int32_t per_batch, const void* table,
+                                  int64_t ld_table, int32_t vocab, int32_t hidden, void* out,
+                                  int64_t ld_out, float* sumsq_out, nsg_stream_t stream) {
+  NSG_CHECK_ARG(batch >= 0 && per_batch >= 0, "batch %d, per_batch %d", batch, per_batch);
+  const int64_t rows = (int64_t)batch * per_batch;
+  if (rows == 0) {
+    clear_error();
+    return NSG_OK;
+  }
+  NSG_CHECK_ARG(ids && table && out, "null pointer argument");
+  NSG_CHECK_ARG(rows <= INT32_MAX && vocab > 0 && hidden > 0 && hidden % 16 == 0,
+                "rows %lld, vocab %d, hidden %d (a multiple of 16)", (long long)rows, vocab, hidden);
+  NSG_CHECK_ARG(ld_table >= hidden && ld_out >= hidden && ld_table % 8 == 0 && ld_out % 8 == 0 &&
+                    (uintptr_t)table % 16 == 0 && (uintptr_t)out % 16 == 0,
+                "table and out rows must be 16-byte aligned");
+  const dim3 grid((unsigned)((rows + kNormThreads / 64 - 1) / (kNormThreads / 64)));
+  hipLaunchKernelGGL(embed_rows_kernel, grid, dim3(kNormThreads), 0,
+                     static_cast<hipStream_t>(stream), ids, id_stride_b, id_stride_j, per_batch,
+                     (int)rows, static_cast<const uint16_t*>(table), ld_table, vocab, hidden,
+                     static_cast<uint16_t*>(out), ld_out, sumsq_out);
+  return launch_status("embed_rows_kernel");
 }
 
 extern "C" int32_t nsg_silu_mul(const void* gate_up, void* out, int64_t num_tokens,

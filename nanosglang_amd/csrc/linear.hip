@@ -665,7 +665,8 @@ __global__ __launch_bounds__(MG * NW * 64) void linear_kernel(LinParams p) {
 // Per row, the largest of the lm_head workgroups' keys -> the column (token):
 // one workgroup per row.
 __global__ __launch_bounds__(256) void argmax_keys_kernel(const uint64_t* __restrict__ keys,
-                                                          int tiles, int64_t* __restrict__ out) {
+                                                          int tiles, int64_t* __restrict__ out,
+                                                          int64_t out_stride) {
   const uint64_t* row = keys + (int64_t)blockIdx.x * tiles;
   uint64_t k = 0;
   for (int t = threadIdx.x; t < tiles; t += 256) k = row[t] > k ? row[t] : k;
@@ -682,7 +683,7 @@ __global__ __launch_bounds__(256) void argmax_keys_kernel(const uint64_t* __rest
     k = wk[0];
 #pragma unroll
     for (int w = 1; w < 4; ++w) k = wk[w] > k ? wk[w] : k;
-    out[blockIdx.x] = (int64_t)(0xffffffffu - (uint32_t)k);
+    out[(int64_t)blockIdx.x * out_stride] = (int64_t)(0xffffffffu - (uint32_t)k);
   }
 }
 
@@ -1015,13 +1016,13 @@ extern "C" int64_t nsg_linear_argmax_workspace_bytes(int32_t M, int32_t N) {
 extern "C" int32_t nsg_linear_argmax(const void* x, int64_t ldx, const void* w, int64_t ldw,
                                      const void* bias, int32_t M, int32_t N, int32_t K,
                                      void* workspace, int64_t workspace_bytes, int64_t* tokens,
-                                     nsg_stream_t stream) {
+                                     int64_t token_stride, nsg_stream_t stream) {
   NSG_CHECK_ARG(M >= 0 && N > 0 && K > 0, "M %d, N %d, K %d", M, N, K);
   if (M == 0) {
     clear_error();
     return NSG_OK;
   }
-  NSG_CHECK_ARG(x && w && workspace && tokens, "null pointer argument");
+  NSG_CHECK_ARG(x && w && workspace && tokens && token_stride >= 1, "null pointer argument or token stride < 1");
   if (M > kMaxMT * 16) {
     set_error("M %d > %d rows", M, kMaxMT * 16);
     return NSG_ERR_UNSUPPORTED;
@@ -1051,7 +1052,7 @@ extern "C" int32_t nsg_linear_argmax(const void* x, int64_t ldx, const void* w, 
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (int32_t rc = launch_epi<kEpiArgmax>(p, s)) return rc;
   hipLaunchKernelGGL(argmax_keys_kernel, dim3(M), dim3(256), 0, s,
-                     static_cast<const uint64_t*>(workspace), p.col_tiles, tokens);
+                     static_cast<const uint64_t*>(workspace), p.col_tiles, tokens, token_stride);
   return launch_status("argmax_keys_kernel");
 }
 

@@ -353,13 +353,15 @@ class SpecEngine:
         bs = g.bs
         pool = self._pool()
         tok = A["tok0"]
+        direct = self._argmax_drafts(bs)
         for i in range(k):
-            if self._argmax_drafts(bs):
-                m.forward_packed(tok, g.pos[i], pool, g.attn[i], g.slot[i], None,
-                                 self.draft_layers, argmax_out=g.em1[:, 0],
+            if direct:
+                # the token lands in its verify column, which is the next
+                # draft's input (a strided view: the lookup takes any strides)
+                tok = g.vids[:, i + 1]
+                m.forward_packed(A["tok0"] if i == 0 else g.vids[:, i], g.pos[i], pool, g.attn[i],
+                                 g.slot[i], None, self.draft_layers, argmax_out=tok,
                                  argmax_ws=self._argmax_ws)
-                g.drafts[:, i].copy_(g.em1[:, 0])
-                tok = g.em1[:, 0]
                 continue
             lg = m.forward_packed(tok, g.pos[i], pool, g.attn[i], g.slot[i], None,
                                   self.draft_layers)
@@ -375,7 +377,10 @@ class SpecEngine:
             g.drafts[:, i].copy_(g.em1[:, 0])
             tok = g.em1[:, 0]
         g.vids[:, 0].copy_(A["tok0"])
-        g.vids[:, 1:].copy_(g.drafts)
+        if direct:
+            g.drafts.copy_(g.vids[:, 1:])
+        else:
+            g.vids[:, 1:].copy_(g.drafts)
         tl = m.forward_packed(g.vids.view(-1), A["vpos"], pool, g.attn[k], A["vslot"])
         g.tl = tl        # allocated from the graph's pool: every replay rewrites it
         bonus = self._bonus(tl.view(bs, k + 1, -1), g.u, workspace=self._sample_ws,
@@ -467,17 +472,17 @@ class SpecEngine:
         tok = self._to_dev(np.asarray([r.out[-1] for r in active], np.int64))
         ones = [1] * B
         drafts = torch.empty(B, k, dtype=torch.int64, device=dev)
+        vids = torch.empty(B, k + 1, dtype=torch.int64, device=dev)
+        direct = self._argmax_drafts(B)
         dlog = None
         for i in range(k):
             self._plan(active, ones, [s + i + 1 for s in starts])
             sl = self._to_dev(self._slots(active, [s + i for s in starts], ones))
-            if self._argmax_drafts(B):
+            if direct:
                 tok = self.model.forward_packed(tok, self._to_dev(start_pos + i), self._pool(),
                                                 self.attn, sl, None, self.draft_layers,
-                                                argmax_out=torch.empty(B, dtype=torch.int64,
-                                                                       device=dev),
+                                                argmax_out=vids[:, i + 1],
                                                 argmax_ws=self._argmax_ws)
-                drafts[:, i] = tok
                 continue
             lg = self.model.forward_packed(tok, self._to_dev(start_pos + i), self._pool(),
                                            self.attn, sl, None, self.draft_layers)
@@ -489,9 +494,11 @@ class SpecEngine:
             drafts[:, i] = tok
         # verify: [last, d_0 .. d_{k-1}] at start .. start+k
         kvp, idx = self._plan(active, [k + 1] * B, [s + k + 1 for s in starts])
-        vids = torch.empty(B, k + 1, dtype=torch.int64, device=dev)
         vids[:, 0] = self._to_dev(np.asarray([r.out[-1] for r in active], np.int64))
-        vids[:, 1:] = drafts
+        if direct:
+            drafts = vids[:, 1:].contiguous()
+        else:
+            vids[:, 1:] = drafts
         vpos = self._to_dev((start_pos[:, None] + np.arange(k + 1)[None]).reshape(-1))
         sl = self._to_dev(self._slots(active, starts, [k + 1] * B))
         tl = self.model.forward_packed(vids.view(-1), vpos, self._pool(), self.attn, sl)

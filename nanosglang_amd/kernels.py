@@ -621,13 +621,42 @@ def linear_argmax(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | No
         raise ValueError("bias must be contiguous bf16")
     if out is None:
         out = torch.empty(M, dtype=torch.int64, device=x.device)
-    if out.dtype != torch.int64 or not out.is_contiguous() or out.numel() != M:
-        raise ValueError("out must be contiguous int64 (M,)")
+    if out.dtype != torch.int64 or out.dim() != 1 or out.numel() != M or out.stride(0) < 1:
+        raise ValueError("out must be int64 (M,) with a positive stride")
     ws = (workspace or _accept_ws(x.device, "argmax")).get(
         lib.nsg_linear_argmax_workspace_bytes(M, N))
     check(lib.nsg_linear_argmax(x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
                                 _ptr(bias), M, N, K, ws.data_ptr(), ws.numel(), out.data_ptr(),
-                                _stream_ptr(x.device)), "nsg_linear_argmax")
+                                out.stride(0), _stream_ptr(x.device)), "nsg_linear_argmax")
+    return out
+
+
+def embed_rows(ids: torch.Tensor, table: torch.Tensor, out: torch.Tensor | None = None,
+               sumsq_out: torch.Tensor | None = None) -> torch.Tensor:
+    """table[ids] for int64 ids of shape (T,) or (B, J), any strides, as
+    (T or B * J, H) rows (C ABI: nsg_embed_rows); with ``sumsq_out``
+    ((H / 16, rows) float32) also the rows' partial sums of squares, the
+    layout :func:`row_sumsq` writes.  Ids outside [0, vocab) read the
+    nearest valid row."""
+    _require_gpu(table, "table")
+    _require_gpu(ids, "ids")
+    if ids.dtype != torch.int64 or ids.dim() not in (1, 2):
+        raise ValueError("ids must be int64 (T,) or (B, J)")
+    B, J = (ids.shape[0], 1) if ids.dim() == 1 else tuple(ids.shape)
+    sb = ids.stride(0)
+    sj = ids.stride(1) if ids.dim() == 2 else 0
+    V, H = table.shape
+    if table.dtype != torch.bfloat16 or table.stride(1) != 1:
+        raise ValueError("table must be bf16 rows with unit inner stride")
+    rows = B * J
+    if out is None:
+        out = torch.empty(rows, H, dtype=table.dtype, device=table.device)
+    if sumsq_out is not None and (sumsq_out.dtype != torch.float32 or not sumsq_out.is_contiguous()
+                                  or tuple(sumsq_out.shape) != (H // 16, rows)):
+        raise ValueError("sumsq_out must be contiguous float32 (H / 16, rows)")
+    check(_lib().nsg_embed_rows(ids.data_ptr(), sb, sj, B, J, table.data_ptr(), table.stride(0), V,
+                                H, out.data_ptr(), out.stride(0), _ptr(sumsq_out),
+                                _stream_ptr(table.device)), "nsg_embed_rows")
     return out
 
 

@@ -207,12 +207,25 @@ class CausalLM:
         k_pool, v_pool = kv_cache
         nl = self.num_layers if num_layers is None else num_layers
         eps = c.rms_norm_eps
-        residual = F.embedding(input_ids, self.embed)    # owned: updated in place below
-        if self._fold and input_ids.shape[0] <= kernels._lib().nsg_linear_max_rows():
+        T = input_ids.numel()
+        folded = self._fold and T <= kernels._lib().nsg_linear_max_rows()
+        ssa = None
+        if self.embed.dtype == torch.bfloat16 and c.hidden_size % 16 == 0:
+            # causal_lm.py:613 -- ids may be any (T,) or (B, J) view; with the
+            # folded norms the lookup also writes the first partial sums
+            if folded:
+                ssa = torch.empty(c.hidden_size // 16, T, dtype=torch.float32,
+                                  device=self.device)
+            residual = kernels.embed_rows(input_ids, self.embed, sumsq_out=ssa)
+        else:
+            residual = F.embedding(input_ids.reshape(-1), self.embed)
+        # residual: owned, updated in place below
+        if folded:
             # folded norms: residual += o_proj(.) and += down_proj(.) in those
             # kernels, which also write the rows' partial sums of squares
             # (ssb, ssa); q/k/v and gate/up read them (causal_lm.py:505-531)
-            ssa = kernels.row_sumsq(residual)
+            if ssa is None:
+                ssa = kernels.row_sumsq(residual)
             ssb = torch.empty_like(ssa)
             for li in range(nl):
                 L = self.layers[li]

@@ -454,3 +454,20 @@ def test_linear_argmax_ties_take_the_lowest_column():
     tok = kernels.linear_argmax(x, w).cpu().tolist()
     torch.cuda.synchronize()
     assert tok[0] == 9 and tok[2] == 40 and tok[4] == 0 and tok[5] == 0
+
+
+def test_linear_argmax_writes_a_strided_column():
+    """The tokens may go straight into a column of a (B, k+1) id buffer: the
+    other columns stay untouched."""
+    from nanosglang_amd import kernels
+    print("case: linear_argmax strided out", flush=True)
+    M, N, K = 32, 151936, 896
+    g = torch.Generator(device="cuda").manual_seed(11)
+    x = torch.randn(M, K, generator=g, device="cuda").bfloat16()
+    w = (torch.randn(N, K, generator=g, device="cuda") * K ** -0.5).bfloat16()
+    buf = torch.full((M, 5), -7, dtype=torch.int64, device="cuda")
+    kernels.linear_argmax(x, w, out=buf[:, 2])
+    ref = kernels.linear_argmax(x, w)
+    torch.cuda.synchronize()
+    assert torch.equal(buf[:, 2], ref)
+    assert (buf[:, [0, 1, 3, 4]] == -7).all()

@@ -177,3 +177,29 @@ def test_folded_linears_are_deterministic_and_graph_safe():
         again = step(res2, torch.empty_like(ss), torch.empty_like(out))
         torch.cuda.synchronize()
         assert torch.equal(again, ref)
+
+
+@pytest.mark.parametrize("shape", [(1,), (37,), (32, 5), (8, 5)])
+def test_embed_rows_equals_lookup_and_writes_partials(shape):
+    """nsg_embed_rows: the rows of F.embedding on an index view of any
+    strides (a column of a (B, k+1) buffer, its transpose), bit for bit, and
+    the partial sums of squares row_sumsq writes for the same rows."""
+    from nanosglang_amd import kernels
+    print(f"case: embed_rows ids {shape}", flush=True)
+    V, H = 151936, 896
+    g = torch.Generator(device="cuda").manual_seed(len(shape) * 100 + shape[0])
+    table = torch.randn(V, H, generator=g, device="cuda").bfloat16()
+    base = torch.randint(0, V, (shape[0], 7), generator=g, device="cuda")
+    ids = base[:, 3] if len(shape) == 1 else base[:, :shape[1]].t().contiguous().t()
+    rows = ids.numel()
+    ss = torch.full((H // 16, rows), -1.0, device="cuda")
+    out = kernels.embed_rows(ids, table, sumsq_out=ss)
+    ref = torch.nn.functional.embedding(ids.reshape(-1), table)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    assert torch.equal(ss, kernels.row_sumsq(ref))
+    # ids out of range read the nearest valid row
+    bad = torch.tensor([-5, V + 3], device="cuda")
+    got = kernels.embed_rows(bad, table)
+    torch.cuda.synchronize()
+    assert torch.equal(got[0], table[0]) and torch.equal(got[1], table[V - 1])

@@ -1146,7 +1146,12 @@ Layout layout(int B, int k, int V, bool greedy) {
   L.rows = B * rpr;
   // a request's chunk records fit one wave's two registers per lane
   const int max_ch = std::max(1, std::min({kMaxChunks, (V + 2047) / 2048, kRecCap / rpr}));
-  L.nch = std::max(1, std::min(max_ch, (kTargetWgs + L.rows - 1) / std::max(1, L.rows)));
+  // at least kTargetWgs workgroups, and chunks of at most about one batch
+  // of loads per thread (greedy) or two (stochastic): measured best at
+  // B 64, k 4 and k 8 (V 151,936 and 128,256)
+  const int cs_target = greedy ? 12288 : 20480;
+  L.nch = std::max(1, std::min(max_ch, std::max((V + cs_target - 1) / cs_target,
+                                               (kTargetWgs + L.rows - 1) / std::max(1, L.rows))));
   L.cs = ((V + L.nch - 1) / L.nch + 7) / 8 * 8;
   L.nch = (V + L.cs - 1) / L.cs;
   L.nch2 = std::max(1, std::min(max_ch, (kTargetWgs + B - 1) / std::max(1, B)));

@@ -43,7 +43,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 15
+#define NSG_ABI_VERSION 16
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -235,6 +235,22 @@ int32_t nsg_spec_accept(const void* target_logits, int64_t target_req_stride,
                         int64_t* rollback_slots, void* workspace, int64_t workspace_bytes,
                         nsg_stream_t stream);
 
+/* Greedy acceptance from the target rows' tokens: nsg_spec_accept at
+ * temperature 0 with target_tokens[b * (k + 1) + i] = the first argmax of
+ * target row i of request b (computed without storing the logits, e.g. by
+ * nsg_linear_argmax in the verify forward's lm_head, causal_lm.py:643-645).
+ * Same rule, outputs, rollback slots and error bits as nsg_spec_accept's
+ * greedy form (speculative.py:130-141, 174-182, 186-196); the bits go to
+ * *flags (a device int32, may be NULL), e.g. an acceptance workspace's
+ * flag word.  No workspace. */
+int32_t nsg_spec_accept_greedy_tokens(const int64_t* target_tokens,
+                                      const int64_t* draft_tokens, int32_t batch, int32_t k,
+                                      int32_t vocab, const int32_t* kv_indptr,
+                                      const int32_t* kv_indices, const int32_t* start_pos,
+                                      int32_t page_size, int32_t* num_emitted, int64_t* emitted,
+                                      int64_t* rollback_slots, int32_t* flags,
+                                      nsg_stream_t stream);
+
 /* Copies the acceptance workspace's error flags (bits as above) to *flags_h
  * after synchronising the stream, and clears them. */
 int32_t nsg_spec_accept_check_flags(void* workspace, int32_t* flags_h, nsg_stream_t stream);
@@ -349,7 +365,12 @@ int32_t nsg_silu_mul(const void* gate_up, void* out, int64_t num_tokens,
  *                        y = bf16(bf16(silu(bf16(g))) * bf16(u)), the gate_proj /
  *                        up_proj pair plus F.silu(gate) * up (causal_lm.py:481-482).
  * K must be a multiple of 64 and N of 4; x and w rows 16-byte aligned.  Larger
- * M returns NSG_ERR_UNSUPPORTED (a library GEMM serves prefill). */
+ * M returns NSG_ERR_UNSUPPORTED (a library GEMM serves prefill).  Wide
+ * outputs (N >= 65536: lm_head) with more than 32 rows, no bias and K >= 192
+ * run on a kernel that shares x across 128 output columns; there every
+ * output's K sum runs in k order in one wave, so the values do not depend on
+ * M or the grid (they may differ from those of the 32-row shape in the last
+ * bf16 bit). */
 #define NSG_LINEAR_BIAS 0
 #define NSG_LINEAR_SILU_MUL 1
 int32_t nsg_linear_max_rows(void);
@@ -456,7 +477,10 @@ int32_t nsg_row_sumsq(const void* x, int64_t ldx, int32_t num_tokens, int32_t hi
  * call site (speculative.py:95-100), whose logits nothing else reads.
  * M <= nsg_linear_max_rows(), K % 64 == 0, N % 4 == 0, bf16 weights; the
  * workspace (8-byte aligned, nsg_linear_argmax_workspace_bytes(M, N)) holds
- * one key per row and workgroup, written before it is read. */
+ * one key per row and workgroup (or wave), written before it is read.  At
+ * the verify forward's row counts this is also the target's greedy token
+ * per verify row (speculative.py:130-141 at temperature 0), for
+ * nsg_spec_accept_greedy_tokens. */
 int64_t nsg_linear_argmax_workspace_bytes(int32_t M, int32_t N);
 int32_t nsg_linear_argmax(const void* x, int64_t ldx, const void* w, int64_t ldw,
                           const void* bias, int32_t M, int32_t N, int32_t K, void* workspace,

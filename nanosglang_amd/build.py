@@ -32,10 +32,11 @@ HIPCC_FLAGS = [
 # Per-file additions.  spec_accept.hip: logits are never NaN (a NaN logit
 # makes the reference's softmax NaN too), so max/min need no NaN
 # canonicalisation -- it doubled the cost of the per-logit max in the
-# acceptance pass.  linear.hip: its one asm copy into LDS sets m0 and says
-# so in its clobber list, which the compiler warns about for every kernel
-# instance (the file's kernels use m0 for nothing else).
-FILE_FLAGS = {"spec_accept.hip": ["-fno-honor-nans"], "linear.hip": ["-Wno-inline-asm"]}
+# acceptance pass.  linear.hip, lm_head.hip: their asm copies into LDS set
+# m0 and say so in their clobber lists, which the compiler warns about for
+# every kernel instance (the files' kernels use m0 for nothing else).
+FILE_FLAGS = {"spec_accept.hip": ["-fno-honor-nans"], "linear.hip": ["-Wno-inline-asm"],
+              "lm_head.hip": ["-Wno-inline-asm"]}
 
 
 def _hipcc() -> str:

@@ -28,6 +28,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "lm_head.hpp"
 
 namespace nsg {
 namespace {
@@ -763,13 +764,14 @@ int32_t launch_rope(LinParams& p, hipStream_t s) {
 
 using namespace nsg;
 
-// Where this kernel beats hipBLASLt on MI355X (measured per shape, weights
+// Where these kernels beat hipBLASLt on MI355X (measured per shape, weights
 // streamed from HBM): up to 160 rows for the 0.5B-class q/k/v, o_proj,
-// gate/up and down_proj shapes (weights up to 17 MB), up to 32 for very wide
-// outputs (lm_head) and for weights of 16 M elements or more (8B-class
-// layers, where the library's tiles win from about 64 rows).
+// gate/up and down_proj shapes (weights up to 17 MB) and for very wide
+// outputs (lm_head: more than 32 rows without a bias run on lm_head.hip's
+// kernel), up to 32 for weights of 16 M elements or more (8B-class layers,
+// where the library's tiles win from about 64 rows).
 constexpr int kFastRows = 160;
-constexpr int kFastRowsWide = 32;
+constexpr int kFastRowsWide = 160;
 constexpr int kFastRowsBig = 32;
 constexpr int64_t kBigWeight = 16ll << 20;
 
@@ -824,6 +826,15 @@ int32_t apply_fold(LinParams& p, const NormFold* nf, int32_t N, bool consumer_ok
   return NSG_OK;
 }
 
+// Wide outputs (lm_head) without a bias or folded norm, bf16 weights, more
+// than 32 rows: lm_head.hip's kernel (x shared by 128 output columns).
+constexpr int kHeadRouteRows = 32;
+bool head_route(const LinParams& p) {
+  return p.w && !p.bias && p.w_rows == p.N && !p.sumsq_in && !p.residual && p.N >= kWideN &&
+         p.M > kHeadRouteRows && p.M <= kHeadMaxRows && p.K % kHeadStep == 0 &&
+         p.K >= 3 * kHeadStep;
+}
+
 int32_t linear_impl(const void* x, int64_t ldx, const void* w, const void* w8, int64_t ldw,
                     const float* w_scale, const void* bias, void* y, int64_t ldy, int32_t M,
                     int32_t N, int32_t K, int32_t epilogue, nsg_stream_t stream,
@@ -867,6 +878,11 @@ int32_t linear_impl(const void* x, int64_t ldx, const void* w, const void* w8, i
   if (int32_t rc = apply_fold(p, nf, N, epilogue == NSG_LINEAR_SILU_MUL, epilogue == NSG_LINEAR_BIAS))
     return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (head_route(p)) {
+    const HeadParams hp{p.x, p.w, p.y, p.ldx, p.ldw, p.ldy, M, N, K};
+    int key_cols = 0;
+    return launch_lm_head(hp, false, s, &key_cols);
+  }
   if (epilogue == NSG_LINEAR_SILU_MUL)
     return p.sumsq_in ? launch_epi<kEpiSiluN>(p, s) : launch_epi<kEpiSilu>(p, s);
   return p.residual ? launch_epi<kEpiRes>(p, s) : launch_epi<kEpiBias>(p, s);
@@ -1050,9 +1066,16 @@ extern "C" int32_t nsg_linear_argmax(const void* x, int64_t ldx, const void* w, 
   p.K = K;
   p.w_rows = N;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (int32_t rc = launch_epi<kEpiArgmax>(p, s)) return rc;
+  int key_cols = 0;
+  if (head_route(p)) {
+    const HeadParams hp{p.x, p.w, workspace, p.ldx, p.ldw, 0, M, N, K};
+    if (int32_t rc = launch_lm_head(hp, true, s, &key_cols)) return rc;
+  } else {
+    if (int32_t rc = launch_epi<kEpiArgmax>(p, s)) return rc;
+    key_cols = p.col_tiles;
+  }
   hipLaunchKernelGGL(argmax_keys_kernel, dim3(M), dim3(256), 0, s,
-                     static_cast<const uint64_t*>(workspace), p.col_tiles, tokens, token_stride);
+                     static_cast<const uint64_t*>(workspace), key_cols, tokens, token_stride);
   return launch_status("argmax_keys_kernel");
 }
 

@@ -1,0 +1,284 @@
+// lm_head at verify row counts on gfx950.
+//
+// The vocabulary projection of the verify forward (nano_sglang/model/
+// causal_lm.py:643-645, logits = lm_head(norm(h))) runs on M = batch *
+// (k + 1) rows: 160 x 151,936 x 896 at batch 32, k = 4.  Its 272 MB weight
+// dominates the bytes, but at 160 rows a kernel that streams W per 32-row
+// group (linear.hip) re-reads it five times through the caches, and one that
+// re-reads x per 16-column tile moves x's 287 KB thousands of times.  Here:
+//
+// * a persistent workgroup per CU walks its column tiles (128 output columns:
+//   4 waves x 2 W tiles of 16) and, per tile, K in 64-element steps, one flat
+//   sequence of steps across tiles, so the pipeline never drains between
+//   tiles;
+// * each step's x rows (all M) and W rows go from global memory into a slot
+//   of an LDS ring (4 to 8 slots, as many as fit) by LDS DMA
+//   (global_load_lds_dwordx4), all but one slot in flight ahead of the math:
+//   W is read from HBM exactly once, x once per tile from L2;
+// * each wave multiplies its two W tiles by all M / 16 x tiles
+//   (v_mfma_f32_16x16x32_bf16, A = W, B = x^T): a W fragment feeds MT MFMAs,
+//   an x fragment two;
+// * an output element's whole K sum stays in one wave, in k order, so the
+//   result does not depend on the grid;
+// * the logits are bf16(acc), one rounding (lm_head has no bias); the argmax
+//   form keeps, per row, the largest key (linear.hip's argmax keys: ordered
+//   bf16 bits, then the inverted column) over all of a wave's columns and
+//   stores one key per row and wave at the end.
+//
+// The ring's 16-byte segments are XOR-swizzled per row pair (segment s of row
+// r sits at s ^ ((r >> 1) & 7)): the 16 rows of an MFMA fragment read then
+// fall on distinct banks of the 256-byte bank row.
+#include "lm_head.hpp"
+
+#include <algorithm>
+
+namespace nsg {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kNT = 2;                     // 16-column W tiles per wave
+constexpr int kCols = kWaves * kNT * 16;   // output columns per workgroup tile
+constexpr int kRowBytes = kHeadStep * 2;   // one row's bytes per step
+constexpr int kLdsMax = 160 * 1024;
+constexpr int kMaxStages = 8;
+
+template <int MT>
+constexpr int stage_bytes() {
+  return (MT * 16 + kWaves * kNT * 16) * kRowBytes;
+}
+// Ring depth: as many slots as the CU's LDS holds (4 at 160 rows, 6 at 64);
+// all but one are in flight ahead of the math.
+template <int MT>
+constexpr int ring_stages() {
+  return kLdsMax / stage_bytes<MT>() < kMaxStages ? kLdsMax / stage_bytes<MT>() : kMaxStages;
+}
+
+// One LDS DMA copy of 16 bytes per lane: lane l's 16 bytes land at LDS
+// address lds + 16 l.  In asm, unseen by the compiler's wait-count pass
+// (through the builtin, that pass waits for every copy in flight before each
+// LDS read); the ring's own waits order them.  s_nop: the one wait state an
+// LDS DMA needs after an SALU write of M0.
+__device__ __forceinline__ void dma16(uint32_t lds, const void* src) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds), "v"(src)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ uint64_t key_max(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+template <int MT, bool ARG>
+__global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
+  static_assert(MT % 2 == 0 && MT >= 2 && MT <= kHeadMaxRows / 16, "whole x copies");
+  // x: MT * 16 rows x 8 segments = 2 MT copies per step, kX per wave (the
+  // last wave's surplus copies repeat the last copy: the same bytes to the
+  // same place)
+  constexpr int kXAll = 2 * MT;
+  constexpr int kX = (kXAll + kWaves - 1) / kWaves;
+  constexpr int kW = 2 * kNT;      // W copies per wave and step (its 32 rows x 8 segments)
+  constexpr int NI = kX + kW;      // vector-memory instructions per wave and step
+  constexpr int SB = stage_bytes<MT>();
+  constexpr int kStages = ring_stages<MT>();
+  static_assert(kStages >= 3 && (kStages - 2) * NI <= 63, "vmcnt counts to 63");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[kStages * SB];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nst = p.K / kHeadStep;
+  const int tiles = (p.N + kCols - 1) / kCols;
+  const int my_tiles = (tiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int total = my_tiles * nst;
+
+  // DMA sources.  Copy i of a wave fills ring slots (16-byte units) 64 i +
+  // lane of its region: row r = slot / 8, physical segment slot % 8, which
+  // holds logical segment (slot % 8) ^ ((r >> 1) & 7).  Rows past M repeat
+  // row M - 1, W rows past N repeat rows of the last four columns; their
+  // results are not kept.
+  const uint32_t ring_lds = lds_addr(ring);
+  const bf16* xsrc[kX];
+  uint32_t x_lds[kX];
+#pragma unroll
+  for (int i = 0; i < kX; ++i) {
+    const int copy = min(wave * kX + i, kXAll - 1);
+    x_lds[i] = ring_lds + copy * 1024;
+    const int slot = copy * 64 + lane;
+    const int r = slot >> 3;
+    const int seg = (slot & 7) ^ ((r >> 1) & 7);
+    xsrc[i] = p.x + (int64_t)min(r, p.M - 1) * p.ldx + seg * 8;
+  }
+  int wrow[kW], wseg[kW];
+#pragma unroll
+  for (int i = 0; i < kW; ++i) {
+    const int slot = i * 64 + lane;
+    wrow[i] = slot >> 3;
+    wseg[i] = (slot & 7) ^ ((wrow[i] >> 1) & 7);
+  }
+  const bf16* wsrc[kW];
+  auto set_w = [&](int j) {  // W rows of this wave for the workgroup's tile j
+    const int c0 = ((int)blockIdx.x + j * (int)gridDim.x) * kCols + wave * kNT * 16;
+#pragma unroll
+    for (int i = 0; i < kW; ++i) {
+      int c = c0 + wrow[i];
+      c = c < p.N ? c : p.N - 4 + (c & 3);
+      wsrc[i] = p.w + (int64_t)c * p.ldw + wseg[i] * 8;
+    }
+  };
+  const uint32_t w_lds = ring_lds + MT * 16 * kRowBytes + wave * kNT * 16 * kRowBytes;
+
+  // issue cursor: steps issued so far, and the tile / step of the next one
+  int issued = 0, i_tile = 0, i_step = 0, i_slot = 0;
+  auto issue = [&]() {
+    const uint32_t sb = (uint32_t)i_slot * SB;
+    i_slot = i_slot + 1 == kStages ? 0 : i_slot + 1;
+    const int64_t k0 = (int64_t)i_step * kHeadStep;
+#pragma unroll
+    for (int i = 0; i < kX; ++i) dma16(x_lds[i] + sb, xsrc[i] + k0);
+#pragma unroll
+    for (int i = 0; i < kW; ++i) dma16(w_lds + sb + i * 1024, wsrc[i] + k0);
+    ++issued;
+    if (++i_step == nst) {
+      i_step = 0;
+      if (++i_tile < my_tiles) set_w(i_tile);
+    }
+  };
+
+  // fragment reads: row T * 16 + lane % 16 of a region, logical segment
+  // 4 h + lane / 16 (k 32 h + 8 (lane / 16) .. + 8 of the step)
+  const int r16 = lane & 15;
+  uint32_t frag_off[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) frag_off[h] = r16 * kRowBytes + 16 * ((4 * h + (lane >> 4)) ^ (r16 >> 1));
+
+  floatx4 acc[kNT][MT];
+#pragma unroll
+  for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  uint64_t best[ARG ? MT : 1];
+#pragma unroll
+  for (int mt = 0; mt < (ARG ? MT : 1); ++mt) best[mt] = 0;
+
+  set_w(0);
+  for (int g = 0; g < kStages - 1 && g < total; ++g) issue();
+
+  int g = 0, c_slot = 0;
+  for (int j = 0; j < my_tiles; ++j) {
+    for (int s = 0; s < nst; ++s, ++g) {
+      // step g landed for this wave (issued - 1 - g later steps may still be
+      // in flight), then for every wave; the slot of step g - 1 is free
+      wait_steps<NI, kStages - 2>(issued - 1 - g);
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (issued < total) issue();
+      const uint8_t* st = ring + c_slot * SB;
+      c_slot = c_slot + 1 == kStages ? 0 : c_slot + 1;
+      const uint8_t* xs = st;
+      const uint8_t* ws = st + MT * 16 * kRowBytes + wave * kNT * 16 * kRowBytes;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        bf16x8 wf[kNT], xf[MT];
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+          wf[nt] = *reinterpret_cast<const bf16x8*>(ws + nt * 16 * kRowBytes + frag_off[h]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          xf[mt] = *reinterpret_cast<const bf16x8*>(xs + mt * 16 * kRowBytes + frag_off[h]);
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            acc[nt][mt] =
+                __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[nt], xf[mt], acc[nt][mt], 0, 0, 0);
+      }
+    }
+
+    // tile j done.  Lane l of (nt, mt) holds rows m = 16 mt + l % 16,
+    // columns n = c0 + 16 nt + 4 (l / 16) + i.
+    const int c0 = ((int)blockIdx.x + j * (int)gridDim.x) * kCols + wave * kNT * 16;
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      const int n = c0 + nt * 16 + 4 * (lane >> 4);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = mt * 16 + r16;
+        const floatx4 v = acc[nt][mt];
+        if constexpr (ARG) {
+          if (n < p.N) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              uint32_t b = float_to_bf16_bits(v[i]);
+              b = b == 0x8000u ? 0u : b;  // -0 counts as +0
+              const uint32_t ord = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+              best[mt] = key_max(best[mt], ((uint64_t)ord << 32) | (0xffffffffu - (uint32_t)(n + i)));
+            }
+          }
+        } else {
+          if (m < p.M && n < p.N) {
+            bf16* y = static_cast<bf16*>(p.out) + (int64_t)m * p.ldy + n;
+            *reinterpret_cast<uint2*>(y) = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+          }
+        }
+        acc[nt][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  }
+
+  if constexpr (ARG) {
+    // the four lanes of a row meet; one stores the row's key for this wave:
+    // keys[m * (4 * grid) + 4 * workgroup + wave]
+    uint64_t* keys = static_cast<uint64_t*>(p.out);
+    const int cols = kWaves * (int)gridDim.x;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      uint64_t k = best[mt];
+#pragma unroll
+      for (int o = 16; o < 64; o <<= 1) {
+        const uint64_t other = ((uint64_t)(uint32_t)__shfl_xor((int)(k >> 32), o, 64) << 32) |
+                               (uint32_t)__shfl_xor((int)(uint32_t)k, o, 64);
+        k = key_max(k, other);
+      }
+      const int m = mt * 16 + r16;
+      if ((lane >> 4) == 0 && m < p.M) keys[(int64_t)m * cols + kWaves * blockIdx.x + wave] = k;
+    }
+  }
+}
+
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+template <int MT>
+int32_t launch_mt(const HeadParams& p, bool argmax, hipStream_t s, int* key_cols) {
+  const int tiles = (p.N + kCols - 1) / kCols;
+  const int per_cu = kLdsMax / (ring_stages<MT>() * stage_bytes<MT>());
+  const int grid = std::min(tiles, device_cus() * std::max(per_cu, 1));
+  *key_cols = kWaves * grid;
+  if (argmax)
+    hipLaunchKernelGGL((lm_head_kernel<MT, true>), dim3(grid), dim3(kWaves * 64), 0, s, p);
+  else
+    hipLaunchKernelGGL((lm_head_kernel<MT, false>), dim3(grid), dim3(kWaves * 64), 0, s, p);
+  return launch_status("lm_head_kernel");
+}
+
+}  // namespace
+
+int32_t launch_lm_head(const HeadParams& p, bool argmax, hipStream_t s, int* key_cols) {
+  const int mt = (p.M + 15) / 16;
+  if (mt <= 2) return launch_mt<2>(p, argmax, s, key_cols);
+  if (mt <= 4) return launch_mt<4>(p, argmax, s, key_cols);
+  if (mt <= 6) return launch_mt<6>(p, argmax, s, key_cols);
+  if (mt <= 8) return launch_mt<8>(p, argmax, s, key_cols);
+  return launch_mt<10>(p, argmax, s, key_cols);
+}
+
+}  // namespace nsg

@@ -1,0 +1,30 @@
+// The wide-output linear kernel (lm_head at verify row counts), launched from
+// linear.hip's entry points.
+#pragma once
+
+#include "common.hpp"
+
+namespace nsg {
+
+// y = x W^T (no bias) for kHeadMinRows <= M <= kHeadMaxRows rows of x and a
+// wide W (vocabulary rows): logits in bf16 (out: M x N, ldy elements apart)
+// or, with keys, one argmax key per row and wave of the persistent grid
+// (out: M x key_cols uint64, the keys of linear.hip's argmax epilogue).
+struct HeadParams {
+  const bf16* x;
+  const bf16* w;
+  void* out;
+  int64_t ldx, ldw, ldy;
+  int M, N, K;
+};
+
+constexpr int kHeadMinRows = 1;
+constexpr int kHeadMaxRows = 160;
+constexpr int kHeadStep = 64;  // K must be a multiple of this (and at least 3 steps)
+
+// Launches the kernel (logits, or keys when argmax; *key_cols = the keys per
+// row written, at most 4 * ceil(N / 128)); the shape checks are the caller's:
+// 16-byte aligned rows of x and W, K % 64 == 0, K >= 192, N % 4 == 0.
+int32_t launch_lm_head(const HeadParams& p, bool argmax, hipStream_t s, int* key_cols);
+
+}  // namespace nsg

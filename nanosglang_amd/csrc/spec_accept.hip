@@ -203,7 +203,7 @@ __device__ void rollback_lanes(const AccParams& p, int b, int n, int lane, int64
     slot = got;
     if (slot == -2) {
       slot = -1;
-      atomicOr(p.flags, 2);
+      if (p.flags) atomicOr(p.flags, 2);
     }
   }
   p.rollback[(int64_t)b * p.k + lane] = slot;
@@ -1397,6 +1397,76 @@ extern "C" int32_t nsg_spec_accept_noalloc(
                      bonus_tokens, batch, k, vocab, temperature, kv_indptr, kv_indices, start_pos,
                      page_size, num_emitted, emitted, rollback_slots, ws, kNoAllocScratchBytes,
                      flags ? flags : static_cast<int*>(ws), stream);
+}
+
+// ---- greedy acceptance from the target rows' tokens ----
+// The greedy rule of greedy_finalize with each target row's argmax already
+// computed (nsg_linear_argmax in the verify forward's lm_head): one wave per
+// request, lane i <= k holding target token i and lane i < k draft token i.
+namespace nsg {
+namespace {
+__global__ __launch_bounds__(64) void greedy_tokens_kernel(AccParams p,
+                                                           const int64_t* __restrict__ ttok) {
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int k = p.k;
+  const int64_t pre = rollback_prefetch(p, b, lane);
+  int64_t x = -1, t = -1;
+  if (lane < k) x = p.dtok[(int64_t)b * k + lane];
+  if (lane <= k) t = ttok[(int64_t)b * (k + 1) + lane];
+  if (lane < k && (x < 0 || x >= p.V) && p.flags) atomicOr(p.flags, 4);  // never matches
+  const uint64_t miss = __builtin_amdgcn_ballot_w64(lane < k && x != t);
+  const int j = miss ? (int)__builtin_ctzll(miss) : k;  // first mismatch, or k
+  if (lane <= k) p.emitted[(int64_t)b * (k + 1) + lane] = lane < j ? x : (lane == j ? t : -1);
+  if (lane == 0) p.n_out[b] = j + 1;
+  rollback_lanes(p, b, j + 1, lane, pre);
+}
+}  // namespace
+}  // namespace nsg
+
+extern "C" int32_t nsg_spec_accept_greedy_tokens(const int64_t* target_tokens,
+                                                 const int64_t* draft_tokens, int32_t batch,
+                                                 int32_t k, int32_t vocab,
+                                                 const int32_t* kv_indptr,
+                                                 const int32_t* kv_indices,
+                                                 const int32_t* start_pos, int32_t page_size,
+                                                 int32_t* num_emitted, int64_t* emitted,
+                                                 int64_t* rollback_slots, int32_t* flags,
+                                                 nsg_stream_t stream) {
+  NSG_CHECK_ARG(batch >= 0 && batch <= kMaxBatch, "batch %d outside [0, %d]", batch, kMaxBatch);
+  NSG_CHECK_ARG(k >= 0 && k <= kMaxK, "k %d outside [0, %d]", k, kMaxK);
+  NSG_CHECK_ARG(vocab > 0, "vocab %d", vocab);
+  if (batch == 0) {
+    clear_error();
+    return NSG_OK;
+  }
+  NSG_CHECK_ARG(target_tokens && num_emitted && emitted, "null pointer argument");
+  NSG_CHECK_ARG(k == 0 || draft_tokens, "draft_tokens required when k > 0");
+  int log2P = 0;
+  if (rollback_slots && k > 0) {
+    NSG_CHECK_ARG(kv_indptr && kv_indices && start_pos,
+                  "rollback slots need kv_indptr, kv_indices and start_pos");
+    NSG_CHECK_ARG(page_size > 0 && (page_size & (page_size - 1)) == 0,
+                  "page_size %d must be a power of two", page_size);
+    while ((1 << log2P) < page_size) ++log2P;
+  }
+  AccParams p{};
+  p.dtok = draft_tokens;
+  p.B = batch;
+  p.k = k;
+  p.V = vocab;
+  p.greedy = 1;
+  p.kv_indptr = kv_indptr;
+  p.kv_indices = kv_indices;
+  p.start_pos = start_pos;
+  p.log2P = log2P;
+  p.n_out = num_emitted;
+  p.emitted = emitted;
+  p.rollback = k > 0 ? rollback_slots : nullptr;
+  p.flags = flags;
+  hipLaunchKernelGGL(greedy_tokens_kernel, dim3(batch), dim3(64), 0,
+                     static_cast<hipStream_t>(stream), p, target_tokens);
+  return launch_status("greedy_tokens_kernel");
 }
 
 extern "C" int32_t nsg_spec_accept_check_flags(void* workspace, int32_t* flags_h,

@@ -84,28 +84,6 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(floatx2{lo, hi}, bf16x2));
 }
 
-// s_waitcnt immediate that waits until at most n vector-memory ops of this
-// wave are outstanding (gfx9 encoding: vmcnt bits [3:0] and [15:14]; expcnt
-// and lgkmcnt left at their maxima, i.e. not waited on).
-constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
-
-// s_waitcnt until at most `later` ring steps (NI DMA instructions each) of
-// this wave are still in flight.  `later` is a runtime value in [0, L]; each
-// case has its own immediate.  vmcnt counts to 63: a larger count waits for
-// 63, which is only more conservative.
-template <int NI, int L>
-__device__ __forceinline__ void wait_steps(int later) {
-  if constexpr (L == 0) {
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-  } else {
-    if (later >= L) {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(L * NI < 63 ? L * NI : 63));
-      return;
-    }
-    wait_steps<NI, L - 1>(later);
-  }
-}
-
 // Transposing LDS reads of the V^T fragments, in asm.  Written through the
 // builtin, every such read after a global_load_lds gets a conservative
 // vmcnt(0) from the compiler (it cannot tell the read from the ring slots

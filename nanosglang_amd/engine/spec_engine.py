@@ -163,6 +163,11 @@ class _StepGraph:
         self.rollback = torch.zeros(bs, k, dtype=torch.int64, device=dev)
         self.n1 = torch.zeros(bs, dtype=torch.int32, device=dev)
         self.bonus = torch.zeros(bs, dtype=torch.int64, device=dev)
+        # greedy verify straight from the lm_head kernel: each verify row's
+        # token (the logits too, only when the engine records a trace)
+        self.ttok = torch.zeros(bs * (k + 1), dtype=torch.int64, device=dev)
+        self.tlog = (torch.zeros(bs * (k + 1), V, dtype=torch.bfloat16, device=dev)
+                     if eng.trace is not None and eng._argmax_verify(bs) else None)
         self.em1 = torch.zeros(bs, 1, dtype=torch.int64, device=dev)
         self.rb1 = torch.zeros(bs, 0, dtype=torch.int64, device=dev)
         if not eng.greedy:
@@ -288,6 +293,12 @@ class SpecEngine:
         return (self.greedy and self.model.dtype == torch.bfloat16
                 and rows <= kernels._lib().nsg_linear_max_rows())
 
+    def _argmax_verify(self, batch: int) -> bool:
+        """Greedy verify tokens straight from the lm_head kernel, accepted by
+        kernels.spec_accept_greedy_tokens: the verify logits (48.6 MB at 160
+        rows of vocabulary 151,936) are never written nor read back."""
+        return self._argmax_drafts(batch * (self.k + 1))
+
     def _bonus(self, tl: torch.Tensor, u: torch.Tensor | None, workspace=None, out=None):
         """speculative.py:174-182: the bonus after k accepted drafts is
         sample_token(target row k) with top-k / top-p; None without filters
@@ -381,6 +392,16 @@ class SpecEngine:
             g.drafts.copy_(g.vids[:, 1:])
         else:
             g.vids[:, 1:].copy_(g.drafts)
+        if self._argmax_verify(bs):
+            m.forward_packed(g.vids.view(-1), A["vpos"], pool, g.attn[k], A["vslot"],
+                             argmax_out=g.ttok, argmax_ws=self._argmax_ws, argmax_logits=g.tlog)
+            g.tl = g.tlog
+            kernels.spec_accept_greedy_tokens(g.ttok.view(bs, k + 1), g.drafts,
+                                              m.config.vocab_size, g.kvp[k], g.idx[k],
+                                              A["start"], page_size=self.P,
+                                              workspace=self._accept_ws,
+                                              out=(g.n_out, g.emitted, g.rollback))
+            return
         tl = m.forward_packed(g.vids.view(-1), A["vpos"], pool, g.attn[k], A["vslot"])
         g.tl = tl        # allocated from the graph's pool: every replay rewrites it
         bonus = self._bonus(tl.view(bs, k + 1, -1), g.u, workspace=self._sample_ws,
@@ -445,16 +466,23 @@ class SpecEngine:
         if self.trace is not None:
             k, (si, sx, _) = self.k, g.strides
             kvp = g.arena.h["kvp"][k * si:k * si + B + 1].copy()
+            if g.tl is None:
+                raise RuntimeError("trace set after the step graphs were captured")
+            ttok = g.ttok.view(g.bs, k + 1)[:B] if self._argmax_verify(g.bs) else None
             self._record(g.tl.view(g.bs, k + 1, -1)[:B], g.drafts[:B],
                          g.arena.h["start"][:B], kvp,
                          g.arena.h["idx"][k * sx:k * sx + int(kvp[-1])],
-                         g.n_out[:B], g.emitted[:B], g.rollback[:B])
+                         g.n_out[:B], g.emitted[:B], g.rollback[:B], ttok)
         return g.n_h.numpy()[:B], g.em_h.numpy()[:B]
 
-    def _record(self, tl, drafts, start, kv_indptr, kv_indices, n_out, emitted, rollback):
+    def _record(self, tl, drafts, start, kv_indptr, kv_indices, n_out, emitted, rollback,
+                target_tokens=None):
         """Append one step's verify logits, acceptance inputs and outputs to
-        ``self.trace`` (host copies)."""
+        ``self.trace`` (host copies); ``target_tokens``: the verify rows'
+        tokens of the greedy lm_head kernel, when the step accepted from
+        those."""
         self.trace.append({
+            "target_tokens": None if target_tokens is None else target_tokens.cpu().numpy(),
             "verify_logits": tl.detach().cpu(), "drafts": drafts.cpu().numpy(),
             "start": np.asarray(start, np.int64).copy(),
             "kv_indptr": np.asarray(kv_indptr, np.int32).copy(),
@@ -501,6 +529,22 @@ class SpecEngine:
             vids[:, 1:] = drafts
         vpos = self._to_dev((start_pos[:, None] + np.arange(k + 1)[None]).reshape(-1))
         sl = self._to_dev(self._slots(active, starts, [k + 1] * B))
+        if self._argmax_verify(B):
+            V = self.model.config.vocab_size
+            ttok = torch.empty(B * (k + 1), dtype=torch.int64, device=dev)
+            tl = (torch.empty(B * (k + 1), V, dtype=torch.bfloat16, device=dev)
+                  if self.trace is not None else None)
+            self.model.forward_packed(vids.view(-1), vpos, self._pool(), self.attn, sl,
+                                      argmax_out=ttok, argmax_ws=self._argmax_ws,
+                                      argmax_logits=tl)
+            n_out, emitted, rollback = kernels.spec_accept_greedy_tokens(
+                ttok.view(B, k + 1), drafts, V, self._to_dev(kvp), self._to_dev(idx),
+                self._to_dev(start_pos, torch.int32), page_size=self.P,
+                workspace=self._accept_ws)
+            if self.trace is not None:
+                self._record(tl.view(B, k + 1, -1), drafts, start_pos, kvp, idx, n_out, emitted,
+                             rollback, ttok.view(B, k + 1))
+            return n_out.cpu().numpy(), emitted.cpu().numpy()
         tl = self.model.forward_packed(vids.view(-1), vpos, self._pool(), self.attn, sl)
         u = None if self.greedy else self._uniforms(0, B * (k + 1)).view(B, k + 1)
         n_out, emitted, rollback = kernels.spec_accept(

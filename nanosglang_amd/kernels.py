@@ -469,6 +469,56 @@ def spec_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor | None,
     return n_out, emitted, rollback
 
 
+def spec_accept_greedy_tokens(target_tokens: torch.Tensor, draft_tokens: torch.Tensor | None,
+                              vocab: int, kv_indptr: torch.Tensor | None = None,
+                              kv_indices: torch.Tensor | None = None,
+                              start_pos: torch.Tensor | None = None, page_size: int = 16,
+                              workspace: AcceptWorkspace | None = None, out: tuple | None = None):
+    """Greedy acceptance from each target row's greedy token (C ABI:
+    nsg_spec_accept_greedy_tokens): :func:`spec_accept` at temperature 0 with
+    ``target_tokens`` int64 (B, k+1) = the first argmax of each target row
+    (e.g. :func:`linear_argmax` of the verify forward), so the verify logits
+    are never stored.  Same outputs and rollback slots; draft tokens outside
+    [0, vocab) set the error flag in ``workspace``'s header (read with its
+    ``check_flags``)."""
+    _require_gpu(target_tokens, "target_tokens")
+    dev = target_tokens.device
+    if target_tokens.dim() != 2 or target_tokens.dtype != torch.int64 \
+            or not target_tokens.is_contiguous():
+        raise ValueError("target_tokens must be contiguous int64 (B, k+1)")
+    B, k1 = target_tokens.shape
+    k = k1 - 1
+    if k > 0:
+        if draft_tokens is None or tuple(draft_tokens.shape) != (B, k):
+            raise ValueError("draft_tokens must be (B, k)")
+        _require_gpu(draft_tokens, "draft_tokens")
+        draft_tokens = draft_tokens.to(torch.int64).contiguous()
+    rb_ok = kv_indptr is not None and k > 0
+    if rb_ok:
+        for name, t in (("kv_indptr", kv_indptr), ("kv_indices", kv_indices),
+                        ("start_pos", start_pos)):
+            if t is None:
+                raise ValueError(f"{name} required for rollback slots")
+            _require_gpu(t, name)
+        kv_indptr = kv_indptr.to(torch.int32).contiguous()
+        kv_indices = kv_indices.to(torch.int32).contiguous()
+        start_pos = start_pos.to(torch.int32).contiguous()
+    if out is None:
+        n_out = torch.empty(B, dtype=torch.int32, device=dev)
+        emitted = torch.empty(B, k + 1, dtype=torch.int64, device=dev)
+        rollback = torch.full((B, k), -1, dtype=torch.int64, device=dev)
+    else:
+        n_out, emitted, rollback = out
+    flags = (workspace or _accept_ws(dev)).get(256)
+    rc = _lib().nsg_spec_accept_greedy_tokens(
+        target_tokens.data_ptr(), _ptr(draft_tokens) if k > 0 else None, B, k, int(vocab),
+        _ptr(kv_indptr) if rb_ok else None, _ptr(kv_indices) if rb_ok else None,
+        _ptr(start_pos) if rb_ok else None, page_size, n_out.data_ptr(), emitted.data_ptr(),
+        rollback.data_ptr() if rb_ok else None, flags.data_ptr(), _stream_ptr(dev))
+    check(rc, "nsg_spec_accept_greedy_tokens")
+    return n_out, emitted, rollback
+
+
 def sample(logits: torch.Tensor, temperature: float, top_k: int = 0, top_p: float = 1.0,
            uniforms: torch.Tensor | None = None, workspace: AcceptWorkspace | None = None,
            out: torch.Tensor | None = None) -> torch.Tensor:

@@ -192,7 +192,7 @@ class CausalLM:
                        attn_wrapper, write_indices: torch.Tensor,
                        logit_indices: torch.Tensor | None = None,
                        num_layers: int | None = None, argmax_out: torch.Tensor | None = None,
-                       argmax_ws=None) -> torch.Tensor:
+                       argmax_ws=None, argmax_logits: torch.Tensor | None = None) -> torch.Tensor:
         """Packed forward over ``T`` tokens of several requests.
 
         kv_cache: (k_cache, v_cache) pools (L, N, P, Hkv, D); attn_wrapper: a
@@ -200,7 +200,9 @@ class CausalLM:
         flat slots (T,).  Returns logits (len(logit_indices) or T, V), or,
         with ``argmax_out`` (int64, one per row), each row's greedy token
         written there (``kernels.linear_argmax``: the logits are never
-        stored)."""
+        stored); ``argmax_logits`` (T, V) bf16 then also receives the logits
+        those tokens are the argmax of (same kernel and rounding; for tests
+        and traces)."""
         c = self.config
         Hq, Hkv, D, I = (c.num_attention_heads, c.num_key_value_heads, c.head_dim,
                          c.intermediate_size)
@@ -267,5 +269,7 @@ class CausalLM:
         if logit_indices is not None:
             h = h[logit_indices]
         if argmax_out is not None:
+            if argmax_logits is not None:
+                kernels.linear(h, self.lm_head, out=argmax_logits, force=True)
             return kernels.linear_argmax(h, self.lm_head, out=argmax_out, workspace=argmax_ws)
         return kernels.linear(h, self.lm_head)

@@ -368,3 +368,57 @@ def test_one_workspace_across_shapes_and_modes_ends_zero():
 def _native_lib():
     from nanosglang_amd import _native
     return _native.load()
+
+
+@pytest.mark.parametrize("B,k,V,match", [(64, 4, 151936, 0.0), (32, 4, 5000, 0.7),
+                                         (8, 8, 3001, 1.0), (5, 0, 999, 0.0)])
+def test_greedy_from_target_tokens_equals_greedy_on_logits(B, k, V, match):
+    """nsg_spec_accept_greedy_tokens on each target row's first argmax gives
+    the outputs and rollback slots of the greedy acceptance on the logits
+    (and of the oracle), bit for bit; ``match``: the share of drafts set to
+    the target's own argmax, so that accepted prefixes of every length
+    occur."""
+    from nanosglang_amd.kernels import spec_accept_greedy_tokens
+    print(f"case: greedy from tokens B={B} k={k} V={V} match={match}", flush=True)
+    a = workloads.acceptance_batch(batch=B, k=k, vocab=V, seed=B + k)
+    am = a["target"].argmax(-1)
+    rng = np.random.default_rng(B)
+    if k:
+        take = rng.random((B, k)) < match
+        a["draft_tokens"] = np.where(take, am[:, :k], a["draft_tokens"])
+    n, em, rb, ref = _run(a, 0.0, None, seed=B)
+    _assert_exact(n, em, rb, ref)
+    start, indptr, indices = _page_table(B, k, B)
+    n2, em2, rb2 = spec_accept_greedy_tokens(
+        _dev(am, torch.int64), _dev(a["draft_tokens"], torch.int64) if k else None, V,
+        _dev(indptr, torch.int32), _dev(indices, torch.int32), _dev(start, torch.int32),
+        page_size=16)
+    torch.cuda.synchronize()
+    _assert_exact(n2.cpu().numpy(), em2.cpu().numpy(), rb2.cpu().numpy(), ref)
+
+
+def test_greedy_from_target_tokens_flags():
+    """Out-of-vocabulary drafts never match and set bit 2, rolled-back
+    positions past the pages get -1 and set bit 1, in the workspace's flag
+    word, as in the logits form."""
+    from nanosglang_amd.kernels import AcceptWorkspace, spec_accept_greedy_tokens
+    print("case: greedy from tokens flags", flush=True)
+    B, k, V = 4, 3, 1000
+    a = workloads.acceptance_batch(batch=B, k=k, vocab=V, seed=9)
+    am = a["target"].argmax(-1)
+    ws = AcceptWorkspace("cuda")
+    start, indptr, indices = _page_table(B, k, 9)
+    bad = am[:, :k].copy()
+    bad[1, 0] = V
+    bad[2, 0] = (am[2, 0] + 1) % V              # rejected: positions 1..k roll back
+    past = start.copy()
+    past[2] = (indptr[3] - indptr[2]) * 16
+    n, em, rb = spec_accept_greedy_tokens(
+        _dev(am, torch.int64), _dev(bad, torch.int64), V, _dev(indptr, torch.int32),
+        _dev(indices, torch.int32), _dev(past, torch.int32), page_size=16, workspace=ws)
+    n, em, rb = n.cpu().numpy(), em.cpu().numpy(), rb.cpu().numpy()
+    assert ws.check_flags() == 4 | 2
+    assert n[1] == 1 and em[1, 0] == am[1, 0] and (em[1, 1:] == -1).all()
+    assert n[0] == k + 1 and n[3] == k + 1 and (em[0] == am[0]).all()
+    assert n[2] == 1 and (rb[2] == -1).all()
+    assert (rb[1] >= 0).all() and (rb[0] == -1).all()

@@ -10,7 +10,9 @@ shapes, through the HIP path.
 * The end-to-end shape: the same target with a 4-layer draft, 32 requests
   with prompts U[100, 512], paged KV 8000 x 16, three speculative steps.
 
-Asserted for every step: the emitted tokens, counts and rollback slots equal
+Asserted for every step: the verify rows' greedy tokens (taken straight from
+the lm_head kernel) are the first argmax of the logits that kernel writes for
+the same rows; the emitted tokens, counts and rollback slots equal
 the greedy closed form (oracle.acceptance.spec_accept: drafts accepted while
 each equals the first argmax of its target row, then that argmax; the
 rejected positions' slots) evaluated on the verify logits the step actually
@@ -38,6 +40,10 @@ def _check_trace(trace, label):
     assert trace, label
     for s, rec in enumerate(trace):
         tl = rec["verify_logits"].float().numpy()
+        if rec["target_tokens"] is not None:
+            # greedy verify from the lm_head kernel's tokens: each is the
+            # first argmax of its verify row
+            assert np.array_equal(rec["target_tokens"], tl.argmax(-1)), (label, s)
         ref = oracle_accept(tl, None, rec["drafts"], None, 0.0, rec["kv_indptr"],
                             rec["kv_indices"], rec["start"], rec["page_size"])
         assert np.array_equal(rec["num_emitted"], ref["num_emitted"]), (label, s)

@@ -65,6 +65,35 @@ def test_linear_wide_output_matches_fp32_reference(M, K):
     _check_bias(y, x, w, b)
 
 
+@pytest.mark.parametrize("M", [33, 40, 64, 100, 128, 160])
+@pytest.mark.parametrize("N,K", [(151936, 896), (65540, 896), (65540, 4096)])
+def test_lm_head_rows_match_fp32_reference(M, N, K):
+    """lm_head above 32 rows without a bias (the kernel that shares x over
+    128 output columns, a persistent grid, an LDS ring fed by DMA): within
+    one bf16 rounding of the fp32 reference; N = 65540 leaves 4 columns in
+    the last 128-column tile."""
+    from nanosglang_amd import kernels
+    print(f"case: lm_head M={M} N={N} K={K}", flush=True)
+    x, w, _ = _data(M, N, K, seed=60 + M + K)
+    y = kernels.linear(x, w, None, force=True)
+    torch.cuda.synchronize()
+    _check_bias(y, x, w, None)
+
+
+def test_lm_head_rows_do_not_depend_on_the_row_count():
+    """Each output's K sum runs in k order in one wave: a row's logits are the
+    same bits whether 33, 100 or 160 rows run (a verify batch and its padded
+    graph batch agree)."""
+    from nanosglang_amd import kernels
+    print("case: lm_head row independence", flush=True)
+    x, w, _ = _data(160, 151936, 896, seed=77)
+    full = kernels.linear(x, w, None, force=True)
+    for M in (33, 100):
+        part = kernels.linear(x[:M], w, None, force=True)
+        torch.cuda.synchronize()
+        assert torch.equal(part, full[:M]), M
+
+
 @pytest.mark.parametrize("M", [1, 32, 70, 160])
 def test_linear_strided_rows_and_out_buffer(M):
     from nanosglang_amd import kernels
@@ -415,7 +444,8 @@ def test_fp8linear_module_matches_reference_arithmetic():
 
 
 @pytest.mark.parametrize("M", [1, 5, 8, 16, 17, 32, 33, 100, 160])
-@pytest.mark.parametrize("N,K,bias", [(151936, 896, False), (4096, 512, True), (1000, 128, False)])
+@pytest.mark.parametrize("N,K,bias", [(151936, 896, False), (65540, 896, False),
+                                      (4096, 512, True), (1000, 128, False)])
 def test_linear_argmax_equals_argmax_of_linear(M, N, K, bias):
     """nsg_linear_argmax: the greedy token of each row is the first-index
     argmax of exactly the bf16 rows the HIP linear kernel writes (same tile
@@ -432,13 +462,16 @@ def test_linear_argmax_equals_argmax_of_linear(M, N, K, bias):
     assert torch.equal(tok, y.float().argmax(dim=1))
 
 
-def test_linear_argmax_ties_take_the_lowest_column():
+@pytest.mark.parametrize("M", [6, 40, 160])
+def test_linear_argmax_ties_take_the_lowest_column(M):
     """Equal maxima (duplicated weight rows, in one workgroup's columns and in
     different workgroups', and +0 against -0) resolve to the lowest column,
-    as torch.argmax and the reference's greedy sample_token do."""
+    as torch.argmax and the reference's greedy sample_token do (6 rows: the
+    weight-streaming kernel; 40 and 160: the lm_head kernel, whose keys meet
+    across waves and workgroups)."""
     from nanosglang_amd import kernels
-    print("case: linear_argmax ties", flush=True)
-    N, K, M = 151936, 896, 6
+    print(f"case: linear_argmax ties M={M}", flush=True)
+    N, K = 151936, 896
     g = torch.Generator(device="cuda").manual_seed(3)
     x = torch.randn(M, K, generator=g, device="cuda").bfloat16()
     w = (torch.randn(N, K, generator=g, device="cuda") * K ** -0.5).bfloat16()
@@ -450,7 +483,7 @@ def test_linear_argmax_ties_take_the_lowest_column():
     w[41] = (x[2].float() * 0.5).bfloat16()
     w[40] = w[41]
     # rows 4-5: x = 0 -> every logit is +0 or -0: the first column wins
-    x[4:] = 0
+    x[4:6] = 0
     tok = kernels.linear_argmax(x, w).cpu().tolist()
     torch.cuda.synchronize()
     assert tok[0] == 9 and tok[2] == 40 and tok[4] == 0 and tok[5] == 0

@@ -21,9 +21,10 @@
 // * an output element's whole K sum stays in one wave, in k order, so the
 //   result does not depend on the grid;
 // * the logits are bf16(acc), one rounding (lm_head has no bias); the argmax
-//   form keeps, per row, the largest key (linear.hip's argmax keys: ordered
-//   bf16 bits, then the inverted column) over all of a wave's columns and
-//   stores one key per row and wave at the end.
+//   form keeps, per row and lane, the largest bf16 value and its lowest
+//   column over all the wave's tiles, and at the end stores one key per row
+//   and wave (linear.hip's argmax keys: ordered bf16 bits, then the inverted
+//   column).
 //
 // The ring's 16-byte segments are XOR-swizzled per row pair (segment s of row
 // r sits at s ^ ((r >> 1) & 7)): the 16 rows of an MFMA fragment read then
@@ -60,6 +61,15 @@ constexpr int ring_stages() {
 // LDS DMA needs after an SALU write of M0.
 __device__ __forceinline__ void dma16(uint32_t lds, const void* src) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds), "v"(src)
+               : "memory", "m0");
+}
+
+// The same with the non-temporal policy (W is streamed once: measured 54 ->
+// 49 us at 33 rows, 78 -> 74 us at 160).
+__device__ __forceinline__ void dma16_nt(uint32_t lds, const void* src) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt"
                :
                : "s"(lds), "v"(src)
                : "memory", "m0");
@@ -134,7 +144,7 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
 #pragma unroll
     for (int i = 0; i < kX; ++i) dma16(x_lds[i] + sb, xsrc[i] + k0);
 #pragma unroll
-    for (int i = 0; i < kW; ++i) dma16(w_lds + sb + i * 1024, wsrc[i] + k0);
+    for (int i = 0; i < kW; ++i) dma16_nt(w_lds + sb + i * 1024, wsrc[i] + k0);
     ++issued;
     if (++i_step == nst) {
       i_step = 0;
@@ -154,9 +164,16 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
   for (int nt = 0; nt < kNT; ++nt)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-  uint64_t best[ARG ? MT : 1];
+  // argmax: per row, this lane's largest bf16 logit and its column so far
+  // (columns come in increasing order, so a strict > keeps the lowest
+  // column of equal values; -0 equals +0)
+  float bv[ARG ? MT : 1];
+  int bc[ARG ? MT : 1];
 #pragma unroll
-  for (int mt = 0; mt < (ARG ? MT : 1); ++mt) best[mt] = 0;
+  for (int mt = 0; mt < (ARG ? MT : 1); ++mt) {
+    bv[mt] = 0.f;
+    bc[mt] = -1;
+  }
 
   set_w(0);
   for (int g = 0; g < kStages - 1 && g < total; ++g) issue();
@@ -175,22 +192,24 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
       c_slot = c_slot + 1 == kStages ? 0 : c_slot + 1;
       const uint8_t* xs = st;
       const uint8_t* ws = st + MT * 16 * kRowBytes + wave * kNT * 16 * kRowBytes;
+      bf16x8 wf[2][kNT], xf[2][MT];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        bf16x8 wf[kNT], xf[MT];
 #pragma unroll
         for (int nt = 0; nt < kNT; ++nt)
-          wf[nt] = *reinterpret_cast<const bf16x8*>(ws + nt * 16 * kRowBytes + frag_off[h]);
+          wf[h][nt] = *reinterpret_cast<const bf16x8*>(ws + nt * 16 * kRowBytes + frag_off[h]);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
-          xf[mt] = *reinterpret_cast<const bf16x8*>(xs + mt * 16 * kRowBytes + frag_off[h]);
+          xf[h][mt] = *reinterpret_cast<const bf16x8*>(xs + mt * 16 * kRowBytes + frag_off[h]);
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int nt = 0; nt < kNT; ++nt)
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
-            acc[nt][mt] =
-                __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[nt], xf[mt], acc[nt][mt], 0, 0, 0);
-      }
+            acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[h][nt], xf[h][mt],
+                                                                  acc[nt][mt], 0, 0, 0);
     }
 
     // tile j done.  Lane l of (nt, mt) holds rows m = 16 mt + l % 16,
@@ -204,14 +223,13 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
         const int m = mt * 16 + r16;
         const floatx4 v = acc[nt][mt];
         if constexpr (ARG) {
-          if (n < p.N) {
+          const bool ok = n < p.N;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              uint32_t b = float_to_bf16_bits(v[i]);
-              b = b == 0x8000u ? 0u : b;  // -0 counts as +0
-              const uint32_t ord = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
-              best[mt] = key_max(best[mt], ((uint64_t)ord << 32) | (0xffffffffu - (uint32_t)(n + i)));
-            }
+          for (int i = 0; i < 4; ++i) {
+            const float r = bf16_bits_to_float(float_to_bf16_bits(v[i]));
+            const bool take = ok && (r > bv[mt] || bc[mt] < 0);
+            bv[mt] = take ? r : bv[mt];
+            bc[mt] = take ? n + i : bc[mt];
           }
         } else {
           if (m < p.M && n < p.N) {
@@ -231,7 +249,12 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
     const int cols = kWaves * (int)gridDim.x;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      uint64_t k = best[mt];
+      // key = (order-preserving bits of the bf16 value, ~column): the max
+      // key is the largest value at its lowest column; 0 for no column
+      uint32_t b = float_to_bf16_bits(bv[mt]);
+      b = b == 0x8000u ? 0u : b;
+      const uint32_t ord = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+      uint64_t k = bc[mt] < 0 ? 0 : ((uint64_t)ord << 32) | (0xffffffffu - (uint32_t)bc[mt]);
 #pragma unroll
       for (int o = 16; o < 64; o <<= 1) {
         const uint64_t other = ((uint64_t)(uint32_t)__shfl_xor((int)(k >> 32), o, 64) << 32) |

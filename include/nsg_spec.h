@@ -366,11 +366,10 @@ int32_t nsg_silu_mul(const void* gate_up, void* out, int64_t num_tokens,
  *                        up_proj pair plus F.silu(gate) * up (causal_lm.py:481-482).
  * K must be a multiple of 64 and N of 4; x and w rows 16-byte aligned.  Larger
  * M returns NSG_ERR_UNSUPPORTED (a library GEMM serves prefill).  Wide
- * outputs (N >= 65536: lm_head) with more than 32 rows, no bias and K >= 192
- * run on a kernel that shares x across 128 output columns; there every
- * output's K sum runs in k order in one wave, so the values do not depend on
- * M or the grid (they may differ from those of the 32-row shape in the last
- * bf16 bit). */
+ * outputs (N >= 65536: lm_head) without a bias, 192 <= K < 2048 (any M) or
+ * K >= 2048 (M > 32), run on a kernel that shares x across 128 output
+ * columns; there every output's K sum runs in k order in one wave, so the
+ * values do not depend on M or the grid. */
 #define NSG_LINEAR_BIAS 0
 #define NSG_LINEAR_SILU_MUL 1
 int32_t nsg_linear_max_rows(void);

@@ -721,6 +721,7 @@ int32_t launch_cfg(LinParams& p, hipStream_t s) {
 // workgroup count against 256 CUs decides most of it, since each CU streams
 // its workgroups' W rows at a bounded rate.
 constexpr int kWideN = 65536;
+constexpr int kLongRow = 2048;   // K from which a wide output's rows count as long
 
 template <int EPI>
 int32_t launch_epi(LinParams& p, hipStream_t s) {
@@ -766,12 +767,12 @@ using namespace nsg;
 
 // Where these kernels beat hipBLASLt on MI355X (measured per shape, weights
 // streamed from HBM): up to 160 rows for the 0.5B-class q/k/v, o_proj,
-// gate/up and down_proj shapes (weights up to 17 MB) and for very wide
-// outputs (lm_head: more than 32 rows without a bias run on lm_head.hip's
-// kernel), up to 32 for weights of 16 M elements or more (8B-class layers,
-// where the library's tiles win from about 64 rows).
+// gate/up and down_proj shapes (weights up to 17 MB) and for the 0.5B-class
+// lm_head (lm_head.hip's kernel: 69 against 101 us at 160 rows), up to 32
+// for weights of 16 M elements or more (8B-class layers and lm_head, where
+// the library's tiles win from about 64 rows: 212 against 219 us at 64 rows
+// of the 128,256 x 4096 lm_head).
 constexpr int kFastRows = 160;
-constexpr int kFastRowsWide = 160;
 constexpr int kFastRowsBig = 32;
 constexpr int64_t kBigWeight = 16ll << 20;
 
@@ -779,9 +780,8 @@ extern "C" int32_t nsg_linear_max_rows(void) { return kMaxMT * 16; }
 
 extern "C" int32_t nsg_linear_preferred(int32_t M, int32_t N, int32_t K) {
   if (M < 1 || K % kChunk != 0 || N % 4 != 0) return 0;
-  const int rows = N >= kWideN ? kFastRowsWide
-                  : ((int64_t)N * K >= kBigWeight ? kFastRowsBig : kFastRows);
-  return M <= rows ? 1 : 0;
+  const bool big = N >= kWideN ? K >= kLongRow : (int64_t)N * K >= kBigWeight;
+  return M <= (big ? kFastRowsBig : kFastRows) ? 1 : 0;
 }
 
 namespace {
@@ -826,12 +826,14 @@ int32_t apply_fold(LinParams& p, const NormFold* nf, int32_t N, bool consumer_ok
   return NSG_OK;
 }
 
-// Wide outputs (lm_head) without a bias or folded norm, bf16 weights, more
-// than 32 rows: lm_head.hip's kernel (x shared by 128 output columns).
-constexpr int kHeadRouteRows = 32;
+// Wide outputs (lm_head) without a bias or folded norm, bf16 weights:
+// lm_head.hip's kernel (x shared by 128 output columns), at any row count
+// for rows shorter than 2048 (151,936 x 896: 45 against 53 - 59 us at 1 - 32
+// rows), above 32 rows for longer ones (128,256 x 4096: there this kernel's
+// eight-tile shapes stream faster up to 32 rows, 177 against 198 us).
 bool head_route(const LinParams& p) {
   return p.w && !p.bias && p.w_rows == p.N && !p.sumsq_in && !p.residual && p.N >= kWideN &&
-         p.M > kHeadRouteRows && p.M <= kHeadMaxRows && p.K % kHeadStep == 0 &&
+         (p.K < kLongRow || p.M > 32) && p.M <= kHeadMaxRows && p.K % kHeadStep == 0 &&
          p.K >= 3 * kHeadStep;
 }
 

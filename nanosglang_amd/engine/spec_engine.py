@@ -331,7 +331,9 @@ class SpecEngine:
         self._accept_ws.get(max(lib.nsg_spec_accept_workspace_bytes(self.max_batch, self.k, V),
                                 lib.nsg_spec_accept_workspace_bytes(self.max_batch, 0, V)))
         self._sample_ws.get(lib.nsg_sample_workspace_bytes(self.max_batch, V))
-        self._argmax_ws.get(lib.nsg_linear_argmax_workspace_bytes(self.max_batch, V))
+        # draft calls take max_batch rows, greedy verify calls k + 1 per request
+        self._argmax_ws.get(lib.nsg_linear_argmax_workspace_bytes(
+            self.max_batch * (self.k + 1), V))
         pool = torch.cuda.graph_pool_handle()
         for bs in graph_batch_sizes(self.max_batch):
             if bs in self._graphs:

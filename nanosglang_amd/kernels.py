@@ -339,9 +339,14 @@ class AcceptWorkspace:
     def __init__(self, device):
         self.device = torch.device(device)
         self.buf = torch.zeros(0, dtype=torch.uint8, device=self.device)
+        # buffers replaced by a larger one stay allocated: a HIP graph
+        # captured while one of them was current keeps writing to it
+        self._retired: list[torch.Tensor] = []
 
     def get(self, nbytes: int) -> torch.Tensor:
         if self.buf.numel() < nbytes:
+            if self.buf.numel():
+                self._retired.append(self.buf)
             self.buf = torch.zeros(max(nbytes, 2 * self.buf.numel()), dtype=torch.uint8,
                                    device=self.device)
         return self.buf

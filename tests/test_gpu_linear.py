@@ -65,13 +65,14 @@ def test_linear_wide_output_matches_fp32_reference(M, K):
     _check_bias(y, x, w, b)
 
 
-@pytest.mark.parametrize("M", [33, 40, 64, 100, 128, 160])
+@pytest.mark.parametrize("M", [1, 5, 16, 32, 33, 40, 64, 100, 128, 160])
 @pytest.mark.parametrize("N,K", [(151936, 896), (65540, 896), (65540, 4096)])
 def test_lm_head_rows_match_fp32_reference(M, N, K):
-    """lm_head above 32 rows without a bias (the kernel that shares x over
-    128 output columns, a persistent grid, an LDS ring fed by DMA): within
-    one bf16 rounding of the fp32 reference; N = 65540 leaves 4 columns in
-    the last 128-column tile."""
+    """lm_head without a bias (rows shorter than 2048 at any row count, longer
+    rows above 32: the kernel that shares x over 128 output columns, a
+    persistent grid, an LDS ring fed by DMA): within one bf16 rounding of the
+    fp32 reference; N = 65540 leaves 4 columns in the last 128-column
+    tile."""
     from nanosglang_amd import kernels
     print(f"case: lm_head M={M} N={N} K={K}", flush=True)
     x, w, _ = _data(M, N, K, seed=60 + M + K)
@@ -82,13 +83,13 @@ def test_lm_head_rows_match_fp32_reference(M, N, K):
 
 def test_lm_head_rows_do_not_depend_on_the_row_count():
     """Each output's K sum runs in k order in one wave: a row's logits are the
-    same bits whether 33, 100 or 160 rows run (a verify batch and its padded
-    graph batch agree)."""
+    same bits whether 1, 33 or 160 rows run (a verify batch and its padded
+    graph batch agree, and so do draft and verify rows)."""
     from nanosglang_amd import kernels
     print("case: lm_head row independence", flush=True)
     x, w, _ = _data(160, 151936, 896, seed=77)
     full = kernels.linear(x, w, None, force=True)
-    for M in (33, 100):
+    for M in (1, 7, 32, 33, 100):
         part = kernels.linear(x[:M], w, None, force=True)
         torch.cuda.synchronize()
         assert torch.equal(part, full[:M]), M
@@ -131,8 +132,10 @@ def test_linear_large_m_uses_library_gemm_with_same_semantics():
     lib = load()
     assert lib.nsg_linear_preferred(32, 1152, 896) == 1
     assert lib.nsg_linear_preferred(300, 1152, 896) == 0
-    assert lib.nsg_linear_preferred(32, 151936, 896) == 1
-    assert lib.nsg_linear_preferred(33, 151936, 896) == 0
+    assert lib.nsg_linear_preferred(160, 151936, 896) == 1     # 0.5B lm_head
+    assert lib.nsg_linear_preferred(161, 151936, 896) == 0
+    assert lib.nsg_linear_preferred(32, 128256, 4096) == 1     # 8B lm_head
+    assert lib.nsg_linear_preferred(33, 128256, 4096) == 0
     assert lib.nsg_linear_preferred(160, 896, 4864) == 1       # 0.5B down_proj
     assert lib.nsg_linear_preferred(64, 14336, 4096) == 0      # 8B-class weights
     assert lib.nsg_linear_preferred(32, 14336, 4096) == 1
@@ -462,15 +465,15 @@ def test_linear_argmax_equals_argmax_of_linear(M, N, K, bias):
     assert torch.equal(tok, y.float().argmax(dim=1))
 
 
-@pytest.mark.parametrize("M", [6, 40, 160])
-def test_linear_argmax_ties_take_the_lowest_column(M):
+@pytest.mark.parametrize("M,zero_bias", [(6, True), (6, False), (40, False), (160, False)])
+def test_linear_argmax_ties_take_the_lowest_column(M, zero_bias):
     """Equal maxima (duplicated weight rows, in one workgroup's columns and in
     different workgroups', and +0 against -0) resolve to the lowest column,
-    as torch.argmax and the reference's greedy sample_token do (6 rows: the
-    weight-streaming kernel; 40 and 160: the lm_head kernel, whose keys meet
-    across waves and workgroups)."""
+    as torch.argmax and the reference's greedy sample_token do (with a zero
+    bias: the weight-streaming kernel; without: the lm_head kernel, whose
+    keys meet across lanes, waves and workgroups)."""
     from nanosglang_amd import kernels
-    print(f"case: linear_argmax ties M={M}", flush=True)
+    print(f"case: linear_argmax ties M={M} zero_bias={zero_bias}", flush=True)
     N, K = 151936, 896
     g = torch.Generator(device="cuda").manual_seed(3)
     x = torch.randn(M, K, generator=g, device="cuda").bfloat16()
@@ -484,7 +487,8 @@ def test_linear_argmax_ties_take_the_lowest_column(M):
     w[40] = w[41]
     # rows 4-5: x = 0 -> every logit is +0 or -0: the first column wins
     x[4:6] = 0
-    tok = kernels.linear_argmax(x, w).cpu().tolist()
+    b = torch.zeros(N, dtype=torch.bfloat16, device="cuda") if zero_bias else None
+    tok = kernels.linear_argmax(x, w, b).cpu().tolist()
     torch.cuda.synchronize()
     assert tok[0] == 9 and tok[2] == 40 and tok[4] == 0 and tok[5] == 0
 

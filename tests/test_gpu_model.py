@@ -418,3 +418,26 @@ def test_fp8_resident_dequant_gives_identical_logits():
         outs.append(res)
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+def test_capture_sizes_workspaces_for_every_graph():
+    """Capturing graphs for batch sizes 1 .. 32 (greedy: draft argmax calls
+    of up to 32 rows, verify argmax calls of up to 32 * (k + 1)) allocates
+    every workspace once, before the first capture: no captured graph keeps
+    the address of a buffer that a later warm-up replaced.  Then a batch that
+    shrinks through the small graphs runs to the end."""
+    from nanosglang_amd.engine.spec_engine import SpecEngine
+    print("case: capture workspace sizing, max_batch 32, k 4", flush=True)
+    _, gpu = _tiny_models()
+    eng = SpecEngine(gpu, draft_layers=2, num_speculative=4, num_blocks=512, max_batch=32)
+    eng.capture()
+    for ws in (eng._argmax_ws, eng._accept_ws, eng._sample_ws):
+        assert not ws._retired
+    rng = np.random.default_rng(5)
+    prompts = [rng.integers(0, 1000, int(n)).tolist() for n in rng.integers(5, 40, 20)]
+    max_new = [int(m) for m in rng.integers(2, 30, 20)]
+    out = eng.generate(prompts, max_new)
+    for ws in (eng._argmax_ws, eng._accept_ws, eng._sample_ws):
+        assert not ws._retired
+    assert [len(o) for o in out] == max_new
+    assert all(0 <= t < 1000 for o in out for t in o)

@@ -171,6 +171,32 @@ def bench_acceptance(torch, dev, a, greedy, sets=3, reps=60):
     return {"us": t, "bytes": nbytes, "gbs": nbytes / t / 1e3, "sets_rotated": sets}
 
 
+def bench_lm_head(torch, dev, rows, copies=2, reps=10):
+    """Mean time of one greedy lm_head call (x @ W^T over the 151,936 x 896
+    bf16 vocabulary projection, each row's greedy token; the logits are never
+    stored) at `rows` rows: the draft step's shape at 32 rows, the verify
+    step's at 160.  `copies` weight copies (272 MB each) alternate so that
+    the caches serve no call; HIP graph of `reps` calls."""
+    from nanosglang_amd.kernels import linear_argmax
+    N, K = 151936, 896
+    g = torch.Generator(device=dev).manual_seed(7)
+    ws = [(torch.randn(N, K, generator=g, device=dev) * K ** -0.5).bfloat16()
+          for _ in range(copies)]
+    x = torch.randn(rows, K, generator=g, device=dev).bfloat16()
+    out = torch.empty(rows, dtype=torch.int64, device=dev)
+
+    def call(i):
+        linear_argmax(x, ws[i % copies], out=out)
+
+    for i in range(copies):
+        call(i)
+    t = graph_time_us(torch, call, reps)
+    nbytes = N * K * 2 + rows * K * 2 + rows * 8    # W once, x, the tokens
+    del ws
+    return {"us": t, "bytes": nbytes, "gbs": nbytes / t / 1e3,
+            "flops": 2 * rows * N * K}
+
+
 def pmc_probe(torch):
     """Dispatches whose HBM counters calibrate and measure traffic: a plain
     copy of COPY_BYTES (read COPY_BYTES, write COPY_BYTES), then the
@@ -211,6 +237,34 @@ COPY_BYTES = 256 << 20
 # the large verify shape: 8B-shape heads, k = 8, batch 64, contexts U[2048, 8192]
 LARGE_SHAPE = dict(batch=64, q_len=9, num_qo_heads=32, num_kv_heads=8, head_dim=128,
                    min_len=2048, max_len=8192, num_pages=21000)
+
+
+def pmc_probe_lm_head(torch, copies=2):
+    """A 256 MiB device copy (3x, the counter calibration), then greedy
+    lm_head calls (151,936 x 896) at 32 rows and at 160 rows, each on
+    `copies` alternating weight copies, for rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes."""
+    from nanosglang_amd.kernels import linear_argmax
+    dev = torch.device("cuda", 0)
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    N, K = 151936, 896
+    g = torch.Generator(device=dev).manual_seed(7)
+    ws = [(torch.randn(N, K, generator=g, device=dev) * K ** -0.5).bfloat16()
+          for _ in range(copies)]
+    for rows in (32, 160):
+        x = torch.randn(rows, K, generator=g, device=dev).bfloat16()
+        out = torch.empty(rows, dtype=torch.int64, device=dev)
+        for i in range(2 * copies):
+            linear_argmax(x, ws[i % copies], out=out)
+        torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "rows": [32, 160], "calls_per_shape": 2 * copies,
+                      "algorithmic_bytes": {r: N * K * 2 + r * K * 2 + r * 8 for r in (32, 160)}}),
+          flush=True)
 
 
 def pmc_probe_accept(torch, sets=3):
@@ -490,6 +544,9 @@ def main():
                     help="only a 256 MiB device copy (3x) and 3 stochastic + 3 greedy acceptance "
                          "calls at the acceptance shape, for rocprofv3 --pmc FETCH_SIZE / "
                          "WRITE_SIZE passes")
+    ap.add_argument("--pmc-probe-lm-head", action="store_true",
+                    help="only a 256 MiB device copy (3x) and 4 greedy lm_head calls at 32 and "
+                         "at 160 rows, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
     ap.add_argument("--pmc-probe-large", action="store_true",
                     help="only a 256 MiB device copy (3x) and 3 verify-attention launches at "
                          "the large shape, for rocprofv3 --pmc passes (MFMA, HBM traffic)")
@@ -509,6 +566,9 @@ def main():
         return
     if args.pmc_probe_large:
         pmc_probe_large(torch)
+        return
+    if args.pmc_probe_lm_head:
+        pmc_probe_lm_head(torch)
         return
     if args.tune_gemms and args.workload != "large-shape":
         print("--tune-gemms applies to --workload large-shape only (the default line runs "
@@ -599,6 +659,11 @@ def main():
                 log(f"acceptance {mode} {name}: {d}")
                 entries[f"acceptance_{mode}_{name}"] = d
             inputs[name] = a
+            torch.cuda.empty_cache()
+        for rows in (32, 160):
+            d = bench_lm_head(torch, dev, rows)
+            log(f"lm_head greedy {rows} rows: {d}")
+            entries[f"lm_head_greedy_{rows}_rows_v151936"] = d
             torch.cuda.empty_cache()
         big = bench_verify_attention(torch, None, dev, reps=20, pools=1, shape=LARGE_SHAPE)
         inputs["large"] = big.pop("inputs")

@@ -242,9 +242,12 @@ int32_t nsg_spec_accept(const void* target_logits, int64_t target_req_stride,
  * Same rule, outputs, rollback slots and error bits as nsg_spec_accept's
  * greedy form (speculative.py:130-141, 174-182, 186-196); the bits go to
  * *flags (a device int32, may be NULL), e.g. an acceptance workspace's
- * flag word.  No workspace. */
+ * flag word.  Draft token i of request b at draft_tokens[b * draft_stride_b
+ * + i * draft_stride_j] (k and 1 for a contiguous [B, k] array; any strides,
+ * e.g. rows of a position-major id buffer).  No workspace. */
 int32_t nsg_spec_accept_greedy_tokens(const int64_t* target_tokens,
-                                      const int64_t* draft_tokens, int32_t batch, int32_t k,
+                                      const int64_t* draft_tokens, int64_t draft_stride_b,
+                                      int64_t draft_stride_j, int32_t batch, int32_t k,
                                       int32_t vocab, const int32_t* kv_indptr,
                                       const int32_t* kv_indices, const int32_t* start_pos,
                                       int32_t page_size, int32_t* num_emitted, int64_t* emitted,

@@ -61,8 +61,8 @@ SIGNATURES = {
                            f32, i32, vp, i64, vp]),
     "nsg_attn_check_flags": (i32, [vp, C.POINTER(i32), vp]),
     "nsg_spec_accept_check_flags": (i32, [vp, C.POINTER(i32), vp]),
-    "nsg_spec_accept_greedy_tokens": (i32, [vp, vp, i32, i32, i32, vp, vp, vp, i32, vp, vp, vp,
-                                            vp, vp]),
+    "nsg_spec_accept_greedy_tokens": (i32, [vp, vp, i64, i64, i32, i32, i32, vp, vp, vp, i32,
+                                            vp, vp, vp, vp, vp]),
     "nsg_spec_accept_workspace_bytes": (i64, [i32, i32, i32]),
     "nsg_spec_accept": (i32, [vp, i64, i64, vp, i64, i64, i32, vp, vp, vp, i32, i32, i32, f32,
                               vp, vp, vp, i32, vp, vp, vp, vp, i64, vp]),

@@ -1406,13 +1406,14 @@ extern "C" int32_t nsg_spec_accept_noalloc(
 namespace nsg {
 namespace {
 __global__ __launch_bounds__(64) void greedy_tokens_kernel(AccParams p,
-                                                           const int64_t* __restrict__ ttok) {
+                                                           const int64_t* __restrict__ ttok,
+                                                           int64_t ds_b, int64_t ds_j) {
   const int b = blockIdx.x;
   const int lane = threadIdx.x;
   const int k = p.k;
   const int64_t pre = rollback_prefetch(p, b, lane);
   int64_t x = -1, t = -1;
-  if (lane < k) x = p.dtok[(int64_t)b * k + lane];
+  if (lane < k) x = p.dtok[b * ds_b + lane * ds_j];
   if (lane <= k) t = ttok[(int64_t)b * (k + 1) + lane];
   if (lane < k && (x < 0 || x >= p.V) && p.flags) atomicOr(p.flags, 4);  // never matches
   const uint64_t miss = __builtin_amdgcn_ballot_w64(lane < k && x != t);
@@ -1425,8 +1426,9 @@ __global__ __launch_bounds__(64) void greedy_tokens_kernel(AccParams p,
 }  // namespace nsg
 
 extern "C" int32_t nsg_spec_accept_greedy_tokens(const int64_t* target_tokens,
-                                                 const int64_t* draft_tokens, int32_t batch,
-                                                 int32_t k, int32_t vocab,
+                                                 const int64_t* draft_tokens,
+                                                 int64_t draft_stride_b, int64_t draft_stride_j,
+                                                 int32_t batch, int32_t k, int32_t vocab,
                                                  const int32_t* kv_indptr,
                                                  const int32_t* kv_indices,
                                                  const int32_t* start_pos, int32_t page_size,
@@ -1442,6 +1444,9 @@ extern "C" int32_t nsg_spec_accept_greedy_tokens(const int64_t* target_tokens,
   }
   NSG_CHECK_ARG(target_tokens && num_emitted && emitted, "null pointer argument");
   NSG_CHECK_ARG(k == 0 || draft_tokens, "draft_tokens required when k > 0");
+  NSG_CHECK_ARG(k == 0 || (draft_stride_b >= 0 && draft_stride_j >= 0),
+                "draft token strides %lld, %lld", (long long)draft_stride_b,
+                (long long)draft_stride_j);
   int log2P = 0;
   if (rollback_slots && k > 0) {
     NSG_CHECK_ARG(kv_indptr && kv_indices && start_pos,
@@ -1465,7 +1470,8 @@ extern "C" int32_t nsg_spec_accept_greedy_tokens(const int64_t* target_tokens,
   p.rollback = k > 0 ? rollback_slots : nullptr;
   p.flags = flags;
   hipLaunchKernelGGL(greedy_tokens_kernel, dim3(batch), dim3(64), 0,
-                     static_cast<hipStream_t>(stream), p, target_tokens);
+                     static_cast<hipStream_t>(stream), p, target_tokens, draft_stride_b,
+                     draft_stride_j);
   return launch_status("greedy_tokens_kernel");
 }
 

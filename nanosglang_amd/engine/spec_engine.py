@@ -129,7 +129,10 @@ class _StepGraph:
             nw = max(nw, (mw.value + mm.value) * kernels.NSG_ATTN_WORK_INTS)
         si, sx, sw = _round_up(bs + 1), _round_up(max_page_ids), _round_up(nw)
         self.strides = (si, sx, sw)
-        specs = [("tok0", torch.int64, bs), ("start", torch.int32, bs),
+        # "tok0": the step's token ids position-major, (k + 1) x bs: row 0
+        # the requests' last tokens (the step fill writes it), row i + 1
+        # draft i's tokens (written on the device during the step)
+        specs = [("tok0", torch.int64, (k + 1) * bs), ("start", torch.int32, bs),
                  ("pos", torch.int64, k * bs), ("slot", torch.int64, k * bs),
                  ("vpos", torch.int64, bs * (k + 1)), ("vslot", torch.int64, bs * (k + 1)),
                  ("qo", torch.int32, (k + 1) * si), ("kvp", torch.int32, (k + 1) * si),
@@ -157,7 +160,8 @@ class _StepGraph:
                 max_q_len=1 if a < k else k + 1, max_kv_len=eng.max_kv_len))
         V = c.vocab_size
         self.drafts = torch.zeros(bs, k, dtype=torch.int64, device=dev)
-        self.vids = torch.zeros(bs, k + 1, dtype=torch.int64, device=dev)
+        self.ids = D["tok0"].view(k + 1, bs)
+        self.vids = self.ids.t()             # (bs, k + 1) verify ids, request-major
         self.n_out = torch.zeros(bs, dtype=torch.int32, device=dev)
         self.emitted = torch.zeros(bs, k + 1, dtype=torch.int64, device=dev)
         self.rollback = torch.zeros(bs, k, dtype=torch.int64, device=dev)
@@ -365,15 +369,14 @@ class SpecEngine:
         m, k, A = self.model, self.k, g.arena.d
         bs = g.bs
         pool = self._pool()
-        tok = A["tok0"]
+        tok = g.ids[0]
         direct = self._argmax_drafts(bs)
         for i in range(k):
             if direct:
-                # the token lands in its verify column, which is the next
-                # draft's input (a strided view: the lookup takes any strides)
-                tok = g.vids[:, i + 1]
-                m.forward_packed(A["tok0"] if i == 0 else g.vids[:, i], g.pos[i], pool, g.attn[i],
-                                 g.slot[i], None, self.draft_layers, argmax_out=tok,
+                # the token lands in its row of the step's ids: the next
+                # draft's input and a column of the verify ids
+                m.forward_packed(g.ids[i], g.pos[i], pool, g.attn[i], g.slot[i], None,
+                                 self.draft_layers, argmax_out=g.ids[i + 1],
                                  argmax_ws=self._argmax_ws)
                 continue
             lg = m.forward_packed(tok, g.pos[i], pool, g.attn[i], g.slot[i], None,
@@ -389,22 +392,19 @@ class SpecEngine:
                                     workspace=self._accept_ws, out=(g.n1, g.em1, g.rb1))
             g.drafts[:, i].copy_(g.em1[:, 0])
             tok = g.em1[:, 0]
-        g.vids[:, 0].copy_(A["tok0"])
-        if direct:
-            g.drafts.copy_(g.vids[:, 1:])
-        else:
-            g.vids[:, 1:].copy_(g.drafts)
+        if not direct:
+            g.ids[1:].copy_(g.drafts.t())
         if self._argmax_verify(bs):
-            m.forward_packed(g.vids.view(-1), A["vpos"], pool, g.attn[k], A["vslot"],
+            m.forward_packed(g.vids, A["vpos"], pool, g.attn[k], A["vslot"],
                              argmax_out=g.ttok, argmax_ws=self._argmax_ws, argmax_logits=g.tlog)
             g.tl = g.tlog
-            kernels.spec_accept_greedy_tokens(g.ttok.view(bs, k + 1), g.drafts,
+            kernels.spec_accept_greedy_tokens(g.ttok.view(bs, k + 1), g.vids[:, 1:],
                                               m.config.vocab_size, g.kvp[k], g.idx[k],
                                               A["start"], page_size=self.P,
                                               workspace=self._accept_ws,
                                               out=(g.n_out, g.emitted, g.rollback))
             return
-        tl = m.forward_packed(g.vids.view(-1), A["vpos"], pool, g.attn[k], A["vslot"])
+        tl = m.forward_packed(g.vids, A["vpos"], pool, g.attn[k], A["vslot"])
         g.tl = tl        # allocated from the graph's pool: every replay rewrites it
         bonus = self._bonus(tl.view(bs, k + 1, -1), g.u, workspace=self._sample_ws,
                             out=g.bonus)
@@ -471,7 +471,8 @@ class SpecEngine:
             if g.tl is None:
                 raise RuntimeError("trace set after the step graphs were captured")
             ttok = g.ttok.view(g.bs, k + 1)[:B] if self._argmax_verify(g.bs) else None
-            self._record(g.tl.view(g.bs, k + 1, -1)[:B], g.drafts[:B],
+            drafts = g.vids[:B, 1:] if self._argmax_drafts(g.bs) else g.drafts[:B]
+            self._record(g.tl.view(g.bs, k + 1, -1)[:B], drafts,
                          g.arena.h["start"][:B], kvp,
                          g.arena.h["idx"][k * sx:k * sx + int(kvp[-1])],
                          g.n_out[:B], g.emitted[:B], g.rollback[:B], ttok)

@@ -483,7 +483,7 @@ def spec_accept_greedy_tokens(target_tokens: torch.Tensor, draft_tokens: torch.T
     nsg_spec_accept_greedy_tokens): :func:`spec_accept` at temperature 0 with
     ``target_tokens`` int64 (B, k+1) = the first argmax of each target row
     (e.g. :func:`linear_argmax` of the verify forward), so the verify logits
-    are never stored.  Same outputs and rollback slots; draft tokens outside
+    are never stored; ``draft_tokens`` (B, k) may have any strides.  Same outputs and rollback slots; draft tokens outside
     [0, vocab) set the error flag in ``workspace``'s header (read with its
     ``check_flags``)."""
     _require_gpu(target_tokens, "target_tokens")
@@ -493,11 +493,14 @@ def spec_accept_greedy_tokens(target_tokens: torch.Tensor, draft_tokens: torch.T
         raise ValueError("target_tokens must be contiguous int64 (B, k+1)")
     B, k1 = target_tokens.shape
     k = k1 - 1
+    ds = (0, 0)
     if k > 0:
         if draft_tokens is None or tuple(draft_tokens.shape) != (B, k):
             raise ValueError("draft_tokens must be (B, k)")
         _require_gpu(draft_tokens, "draft_tokens")
-        draft_tokens = draft_tokens.to(torch.int64).contiguous()
+        if draft_tokens.dtype != torch.int64:
+            draft_tokens = draft_tokens.to(torch.int64)
+        ds = (draft_tokens.stride(0), draft_tokens.stride(1))   # any strides
     rb_ok = kv_indptr is not None and k > 0
     if rb_ok:
         for name, t in (("kv_indptr", kv_indptr), ("kv_indices", kv_indices),
@@ -516,7 +519,8 @@ def spec_accept_greedy_tokens(target_tokens: torch.Tensor, draft_tokens: torch.T
         n_out, emitted, rollback = out
     flags = (workspace or _accept_ws(dev)).get(256)
     rc = _lib().nsg_spec_accept_greedy_tokens(
-        target_tokens.data_ptr(), _ptr(draft_tokens) if k > 0 else None, B, k, int(vocab),
+        target_tokens.data_ptr(), _ptr(draft_tokens) if k > 0 else None, ds[0], ds[1], B, k,
+        int(vocab),
         _ptr(kv_indptr) if rb_ok else None, _ptr(kv_indices) if rb_ok else None,
         _ptr(start_pos) if rb_ok else None, page_size, n_out.data_ptr(), emitted.data_ptr(),
         rollback.data_ptr() if rb_ok else None, flags.data_ptr(), _stream_ptr(dev))

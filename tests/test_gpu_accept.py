@@ -395,6 +395,15 @@ def test_greedy_from_target_tokens_equals_greedy_on_logits(B, k, V, match):
         page_size=16)
     torch.cuda.synchronize()
     _assert_exact(n2.cpu().numpy(), em2.cpu().numpy(), rb2.cpu().numpy(), ref)
+    if k:
+        # drafts as rows of a position-major (k + 1) x B id buffer: strides (1, B)
+        ids = torch.zeros(k + 1, B, dtype=torch.int64, device="cuda")
+        ids[1:] = _dev(a["draft_tokens"], torch.int64).t()
+        n3, em3, rb3 = spec_accept_greedy_tokens(
+            _dev(am, torch.int64), ids[1:].t(), V, _dev(indptr, torch.int32),
+            _dev(indices, torch.int32), _dev(start, torch.int32), page_size=16)
+        torch.cuda.synchronize()
+        _assert_exact(n3.cpu().numpy(), em3.cpu().numpy(), rb3.cpu().numpy(), ref)
 
 
 def test_greedy_from_target_tokens_flags():

@@ -101,13 +101,14 @@ void read_record(const Tensor& rec, nsg_attn_plan_t* pl, int64_t* total_q, int64
 }
 
 // Upper bound on the work (plus merge) items of a dynamic plan: every query
-// tile split into every 32-token KV step, plus one merge item.
+// tile split into every 32-token KV step, plus one merge item (tiles of the
+// smallest size a plan takes: 16 rows when the GQA group is 16 or less).
 int64_t work_bound(const int32_t* qo, const int32_t* kvp, const int32_t* last, int64_t B,
                    int64_t Hq, int64_t Hkv, int64_t P) {
   const int64_t G = std::max<int64_t>(1, Hq / std::max<int64_t>(1, Hkv));
   int64_t maxq = 1;
   for (int64_t b = 0; b < B; ++b) maxq = std::max<int64_t>(maxq, qo[b + 1] - qo[b]);
-  const int64_t T = std::max<int64_t>(1, std::min<int64_t>(64 / G, maxq));
+  const int64_t T = std::max<int64_t>(1, std::min<int64_t>((G <= 16 ? 16 : 64) / G, maxq));
   int64_t bound = 0;
   for (int64_t b = 0; b < B; ++b) {
     const int64_t ql = qo[b + 1] - qo[b], npg = kvp[b + 1] - kvp[b];

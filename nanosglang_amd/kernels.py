@@ -64,10 +64,11 @@ def _dev_i32(t, device) -> torch.Tensor:
 def attn_work_bound(qo_h: np.ndarray, kvp_h: np.ndarray, last_h: np.ndarray,
                     num_qo_heads: int, num_kv_heads: int, page_size: int) -> int:
     """Upper bound on the work (plus merge) items of a dynamic attention plan:
-    every query tile split into every 32-token KV step, plus one merge item."""
+    every query tile split into every 32-token KV step, plus one merge item
+    (tiles of the smallest size a plan takes: 16 rows when G <= 16)."""
     bound = 0
     G = max(1, num_qo_heads // max(1, num_kv_heads))
-    T = max(1, min(64 // G, int(np.diff(qo_h).max(initial=1))))
+    T = max(1, min((16 if G <= 16 else 64) // G, int(np.diff(qo_h).max(initial=1))))
     for b in range(len(qo_h) - 1):
         ql = int(qo_h[b + 1] - qo_h[b])
         npg = int(kvp_h[b + 1] - kvp_h[b])

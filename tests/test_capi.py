@@ -163,7 +163,10 @@ def test_fixed_plan_with_kv_bound_never_splits(lib):
     for kv_lens in ([5] * 32, list(rng.integers(100, 641, 32)), [4096] * 32):
         rc, pl, work, (mw, mm) = _plan_fixed(lib, [5] * 32, kv_lens, 32, 5, max_kv=4096)
         assert rc == 0, lib.nsg_last_error()
-        assert (mw, mm) == (32, 0) and (pl.num_work, pl.num_merge) == (32, 0)
+        # latency regime: query tiles of at most 16 rows (2 tokens x 7 heads):
+        # three per request, one work item each, no split, no merge
+        assert (pl.q_tile_tokens, pl.row_tiles) == (2, 1)
+        assert (mw, mm) == (96, 0) and (pl.num_work, pl.num_merge) == (96, 0)
         assert pl.max_splits == 1 and pl.kv_groups == 4
         qo = np.concatenate([[0], np.cumsum([5] * 32)]).astype(np.int32)
         kvp = np.concatenate([[0], np.cumsum([(L + 15) // 16 for L in kv_lens])]).astype(np.int32)

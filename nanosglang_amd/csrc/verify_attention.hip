@@ -30,6 +30,7 @@
 //     from the LDS tile in the same token order;
 //   - the prefetched registers go to the other LDS buffer; one barrier.
 #include <algorithm>
+#include <numeric>
 #include <type_traits>
 #include <cstdarg>
 #include <vector>
@@ -864,6 +865,12 @@ void fixed_capacity(int batch, int max_ql, int G, int num_kv_heads, int num_cus,
   *max_merge = groups;
 }
 
+int max_splits_planned(const std::vector<int>& split_counts) {
+  int mx = 1;
+  for (int c : split_counts) mx = std::max(mx, c);
+  return mx;
+}
+
 // Shared planner.  fixed_work < 0: the work list holds exactly the items the
 // plan needs.  fixed_work >= 0: it holds exactly fixed_work work items (the
 // tail padded with empty items, query tokens 0) followed by fixed_merge merge
@@ -984,9 +991,34 @@ int32_t plan_impl(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
               work_capacity);
     return NSG_ERR_WORKSPACE;
   }
+  // Work-item order.  Workgroups go round-robin over the 8 XCDs (linear id
+  // = item * KV heads + head), so items P = 8 / gcd(heads, 8) apart sit on
+  // one XCD; with several query tiles per request and no split, a request's
+  // tiles are placed P apart, and all but the first read the request's KV
+  // range from that XCD's L2 instead of another XCD's.
+  std::vector<int> order(groups.size());
+  std::iota(order.begin(), order.end(), 0);
+  const int P = 8 / std::gcd(num_kv_heads, 8);
+  if (latency && P > 1 && max_splits_planned(split_counts) == 1) {
+    std::vector<std::pair<int, int>> reqs;  // (first group, groups) per request
+    for (size_t gi = 0; gi < groups.size(); ++gi) {
+      if (gi == 0 || groups[gi].b != groups[gi - 1].b) reqs.push_back({(int)gi, 0});
+      ++reqs.back().second;
+    }
+    order.clear();
+    for (size_t c0 = 0; c0 < reqs.size(); c0 += P) {
+      const size_t c1 = std::min(reqs.size(), c0 + P);
+      int tiles = 0;
+      for (size_t r = c0; r < c1; ++r) tiles = std::max(tiles, reqs[r].second);
+      for (int t = 0; t < tiles; ++t)
+        for (size_t r = c0; r < c1; ++r)
+          if (t < reqs[r].second) order.push_back(reqs[r].first + t);
+    }
+  }
   n = 0;
   int m = 0;
-  for (size_t gi = 0; gi < groups.size(); ++gi) {
+  for (size_t oi = 0; oi < groups.size(); ++oi) {
+    const size_t gi = (size_t)order[oi];
     const Group& g = groups[gi];
     const int ns = split_counts[gi];
     max_splits = std::max(max_splits, ns);

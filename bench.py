@@ -16,13 +16,14 @@ One step = one full pass of that workload.
 workload (batch 32, 5 query tokens, 14/2 heads, D 64, page 16, KV lengths
 U[100, 640], pages scattered over an 8000-block pool): algorithmic bytes per
 launch / mean launch time, timed with HIP events around replays of a HIP
-graph of 160 launches on the launch stream, with 16 pool copies (~1 GB)
-rotated so no launch is served from the 256 MB Infinity Cache.
+graph of 160 launches on the launch stream, each launch on its own copy of
+the pool: a replay touches 160 x 6.4 MB = 1 GB of distinct K/V pages, so the
+256 MB Infinity Cache and the L2s cannot serve a launch from an earlier one.
 ``kernels`` adds the acceptance calls -- ratio tests or the greedy rule,
 residual / bonus draw and rollback slots from a page table -- at batch 64,
-k 4, vocab 151936, T 0.8 and at batch 64, k 8, vocab 128256, T 1.0 (three
-rotated buffer sets each), and the large verify shape (Llama-3-8B heads, k 8,
-batch 64, KV U[2048, 8192]).  ``cpu_baseline`` is the CPU plumbing workload
+k 4, vocab 151936, T 0.8 and at batch 64, k 8, vocab 128256, T 1.0 (rotated
+buffer sets of >= 580 MB in all), and the large verify shape (Llama-3-8B
+heads, k 8, batch 64, KV U[2048, 8192]).  ``cpu_baseline`` is the CPU plumbing workload
 (batch 1, the seed-0 0.5B-shape target with a 2-layer draft, prompt of 64
 uniform ids, k 4, greedy, 32 tokens) on the oracle's fp32 PyTorch-CPU
 restatement of the reference's loop, every affinity core, median of 5 runs
@@ -91,7 +92,7 @@ def graph_time_us(torch, fn, n, reps=5):
     return float(np.median(ts))
 
 
-def bench_verify_attention(torch, w, dev, reps=160, pools=16, shape=None):
+def bench_verify_attention(torch, w, dev, reps=160, pools=160, shape=None):
     from nanosglang_amd import workloads
     from nanosglang_amd.kernels import BatchPrefillWithPagedKVCacheWrapper
     shape = shape or {}
@@ -136,11 +137,13 @@ def acceptance_inputs(**kw):
     return a
 
 
-def bench_acceptance(torch, dev, a, greedy, sets=3, reps=60):
+def bench_acceptance(torch, dev, a, greedy, sets=None, reps=60):
     """Mean time of one full acceptance call (ratio tests or greedy rule,
     residual / bonus draw, emitted tokens, counts and rollback slots from the
     page table) on `sets` rotated logit buffers, from replays of a HIP graph
-    of `reps` calls.  Fills a["uniforms"] (host copy of the Philox uniforms
+    of `reps` calls; by default as many sets as make >= 580 MB of logits in
+    all, so that no call reads what an earlier one left in the 256 MB
+    Infinity Cache.  Fills a["uniforms"] (host copy of the Philox uniforms
     the calls used)."""
     from nanosglang_amd import workloads
     from nanosglang_amd.kernels import philox_uniform, spec_accept
@@ -152,8 +155,10 @@ def bench_acceptance(torch, dev, a, greedy, sets=3, reps=60):
     u = philox_uniform(123, 0, 0, B * k1, dev).view(B, k1)
     a["uniforms"] = u.cpu().numpy()
     pt = [torch.from_numpy(a[n]).to(dev) for n in ("kv_indptr", "kv_indices", "start")]
-    bufs = [(tl, dl)] + [(tl.clone(), dl.clone()) for _ in range(sets - 1)]
     T = 0.0 if greedy else a["temperature"]
+    if sets is None:
+        sets = max(3, -(-580_000_000 // workloads.algorithmic_bytes_acceptance(B, k, V, greedy)))
+    bufs = [(tl, dl)] + [(tl.clone(), dl.clone()) for _ in range(sets - 1)]
     out = (torch.empty(B, dtype=torch.int32, device=dev),
            torch.empty(B, k1, dtype=torch.int64, device=dev),
            torch.empty(B, k, dtype=torch.int64, device=dev))
@@ -168,7 +173,8 @@ def bench_acceptance(torch, dev, a, greedy, sets=3, reps=60):
     t = graph_time_us(torch, call, reps)
     nbytes = workloads.algorithmic_bytes_acceptance(B, k, V, greedy)
     del bufs
-    return {"us": t, "bytes": nbytes, "gbs": nbytes / t / 1e3, "sets_rotated": sets}
+    return {"us": t, "bytes": nbytes, "gbs": nbytes / t / 1e3, "sets_rotated": sets,
+            "bytes_rotated": sets * nbytes}
 
 
 def bench_lm_head(torch, dev, rows, copies=2, reps=10):

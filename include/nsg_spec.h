@@ -43,7 +43,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 16
+#define NSG_ABI_VERSION 17
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -219,7 +219,7 @@ int32_t nsg_spec_step_fill(const int32_t* page_table, int64_t page_table_stride,
  *   outside [0, vocab) (rejected, as a draft the target never proposes);
  *   bit 3, a hand-off wait that ran out its bounded spin (a workspace that was
  *   not zero, or shared with an overlapping call; outputs then undefined, and
- *   nsg_spec_accept_check_flags zeroes the whole header).
+ *   nsg_spec_accept_check_flags zeroes the whole workspace).
  * ---------------------------------------------------------------------- */
 int64_t nsg_spec_accept_workspace_bytes(int32_t batch, int32_t k, int32_t vocab);
 
@@ -255,8 +255,12 @@ int32_t nsg_spec_accept_greedy_tokens(const int64_t* target_tokens,
                                       nsg_stream_t stream);
 
 /* Copies the acceptance workspace's error flags (bits as above) to *flags_h
- * after synchronising the stream, and clears them. */
-int32_t nsg_spec_accept_check_flags(void* workspace, int32_t* flags_h, nsg_stream_t stream);
+ * after synchronising the stream, and clears them.  After bit 3 it zeroes
+ * all workspace_bytes of the workspace (hand-off slots a call gave up on may
+ * be left published anywhere in the body), so the next call starts clean.
+ * Synchronises: not for use under graph capture. */
+int32_t nsg_spec_accept_check_flags(void* workspace, int64_t workspace_bytes, int32_t* flags_h,
+                                    nsg_stream_t stream);
 
 /* nsg_spec_accept without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
@@ -271,6 +275,12 @@ int32_t nsg_spec_accept_check_flags(void* workspace, int32_t* flags_h, nsg_strea
  * its workspace (the caller zeroes it; NULL: not reported).  Every other
  * argument and all outputs are those of nsg_spec_accept, bit for bit. */
 int64_t nsg_spec_accept_noalloc_max_bytes(void);
+/* Zeroes the current device's static workspace of nsg_spec_accept_noalloc
+ * with a fill kernel on `stream` (no allocation, no memset node): the
+ * recovery after a call reported flag bit 3, whose hand-off slots may be
+ * left published.  Must not overlap a nsg_spec_accept_noalloc call on the
+ * same GPU. */
+int32_t nsg_spec_accept_noalloc_reset(nsg_stream_t stream);
 int32_t nsg_spec_accept_noalloc(const void* target_logits, int64_t target_req_stride,
                                 int64_t target_row_stride, const void* draft_logits,
                                 int64_t draft_req_stride, int64_t draft_row_stride,

@@ -13,7 +13,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libnsg_spec.so")
 
 NSG_ATTN_WORK_INTS = 8
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 i32, i64, u32, u64, f32 = C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_float
 vp = C.c_void_p
@@ -60,13 +60,14 @@ SIGNATURES = {
     "nsg_attn_run": (i32, [C.POINTER(AttnPlan), vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32,
                            f32, i32, vp, i64, vp]),
     "nsg_attn_check_flags": (i32, [vp, C.POINTER(i32), vp]),
-    "nsg_spec_accept_check_flags": (i32, [vp, C.POINTER(i32), vp]),
+    "nsg_spec_accept_check_flags": (i32, [vp, i64, C.POINTER(i32), vp]),
     "nsg_spec_accept_greedy_tokens": (i32, [vp, vp, i64, i64, i32, i32, i32, vp, vp, vp, i32,
                                             vp, vp, vp, vp, vp]),
     "nsg_spec_accept_workspace_bytes": (i64, [i32, i32, i32]),
     "nsg_spec_accept": (i32, [vp, i64, i64, vp, i64, i64, i32, vp, vp, vp, i32, i32, i32, f32,
                               vp, vp, vp, i32, vp, vp, vp, vp, i64, vp]),
     "nsg_spec_accept_noalloc_max_bytes": (i64, []),
+    "nsg_spec_accept_noalloc_reset": (i32, [vp]),
     "nsg_spec_accept_noalloc": (i32, [vp, i64, i64, vp, i64, i64, i32, vp, vp, vp, i32, i32, i32,
                                       f32, vp, vp, vp, i32, vp, vp, vp, vp, vp]),
     "nsg_sample_workspace_bytes": (i64, [i32, i32]),

@@ -77,8 +77,8 @@ def build_torch_ops(verbose: bool = True) -> str:
            "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
            *[f"-I{d}" for d in cpp_extension.include_paths()], f"-I{rocm}/include",
            TORCH_OPS_SRC, "-o", tmp, f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch",
-           "-ltorch_cpu", "-ltorch_hip", f"-L{PKG}", "-lnsg_spec", "-Wl,-rpath,$ORIGIN",
-           f"-Wl,-rpath,{torch_lib}"]
+           "-ltorch_cpu", "-ltorch_hip", f"-L{rocm}/lib", "-lamdhip64", f"-L{PKG}",
+           "-lnsg_spec", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"torch operator library failed to build:\n{r.stderr}")

@@ -1372,6 +1372,25 @@ int32_t scratch_address(void** out) {
 
 extern "C" int64_t nsg_spec_accept_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
 
+namespace {
+// Zeroes n 16-byte words from p (a plain fill kernel rather than a memset
+// node, so that a reset enqueued on a capturing stream replays correctly).
+__global__ __launch_bounds__(256) void clear_words_kernel(u32x4* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    p[i] = u32x4{0u, 0u, 0u, 0u};
+}
+}  // namespace
+
+extern "C" int32_t nsg_spec_accept_noalloc_reset(nsg_stream_t stream) {
+  void* ws = nullptr;
+  const int32_t rc = scratch_address(&ws);
+  if (rc) return rc;
+  const int64_t words = kNoAllocScratchBytes / 16;
+  hipLaunchKernelGGL(clear_words_kernel, dim3(512), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<u32x4*>(ws), words);
+  return launch_status("clear_words_kernel");
+}
+
 extern "C" int32_t nsg_spec_accept_noalloc(
     const void* target_logits, int64_t target_req_stride, int64_t target_row_stride,
     const void* draft_logits, int64_t draft_req_stride, int64_t draft_row_stride,
@@ -1475,17 +1494,19 @@ extern "C" int32_t nsg_spec_accept_greedy_tokens(const int64_t* target_tokens,
   return launch_status("greedy_tokens_kernel");
 }
 
-extern "C" int32_t nsg_spec_accept_check_flags(void* workspace, int32_t* flags_h,
-                                               nsg_stream_t stream) {
+extern "C" int32_t nsg_spec_accept_check_flags(void* workspace, int64_t workspace_bytes,
+                                               int32_t* flags_h, nsg_stream_t stream) {
   NSG_CHECK_ARG(workspace && flags_h, "null argument");
+  NSG_CHECK_ARG(workspace_bytes >= (int64_t)sizeof(int32_t), "workspace_bytes %lld",
+                (long long)workspace_bytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
   NSG_CHECK_HIP(hipMemcpyAsync(flags_h, workspace, sizeof(int32_t), hipMemcpyDeviceToHost, s));
   NSG_CHECK_HIP(hipStreamSynchronize(s));
-  NSG_CHECK_HIP(hipMemsetAsync(workspace, 0, sizeof(int32_t), s));
-  if (*flags_h & 8) {   // a hand-off gave up: the counters may be left non-zero
-    NSG_CHECK_HIP(hipMemsetAsync(workspace, 0, kWorkspaceHeaderBytes, s));
-    NSG_CHECK_HIP(hipStreamSynchronize(s));
-  }
+  // a hand-off gave up (bit 3): published slots may be left behind anywhere
+  // in the body, so the whole workspace is cleared, not only the flag word
+  const int64_t n = (*flags_h & 8) ? workspace_bytes : (int64_t)sizeof(int32_t);
+  NSG_CHECK_HIP(hipMemsetAsync(workspace, 0, n, s));
+  NSG_CHECK_HIP(hipStreamSynchronize(s));
   clear_error();
   return NSG_OK;
 }

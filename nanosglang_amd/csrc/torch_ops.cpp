@@ -15,6 +15,7 @@
 //   nsg::verify_attention_plan  the host planner: plan record + work list
 //   nsg::verify_attention_run   one layer from a plan; allocates nothing
 //   nsg::spec_accept            acceptance / residual / bonus / rollback slots
+//   nsg::spec_accept_check_flags  its device error flags for the current stream
 //   nsg::sample                 temperature / top-k / top-p, one token per row
 //   nsg::kv_write, nsg::rope_kv_write
 //                               K / V rows (after RoPE) into flat KV slots
@@ -34,6 +35,8 @@
 #include <tuple>
 #include <utility>
 #include <vector>
+
+#include <hip/hip_runtime_api.h>
 
 #include "../../include/nsg_spec.h"
 
@@ -199,18 +202,41 @@ void verify_attention_run(const Tensor& plan, const Tensor& work, const Tensor& 
 // (one of each per stream: calls on one stream run in order, so they may
 // share it; each kind keeps its own, the acceptance one being zero between
 // calls).  All are zero-filled when created.
+//
+// A HIP graph captured while a workspace was current keeps its address, so
+// a workspace replaced by a larger one stays allocated (in `retired`) for
+// the life of the process, and none is created or grown while its stream is
+// being captured (the caller makes one eager call of its largest shape on
+// that stream first): an allocation there would come from the graph's
+// private pool.
+
+struct Workspace {
+  Tensor cur;
+  std::vector<Tensor> retired;
+};
 
 std::mutex g_ws_mu;
-std::map<std::tuple<int, void*, int>, Tensor> g_ws;
+std::map<std::tuple<int, void*, int>, Workspace> g_ws;
+
+const char* const kWsNames[] = {"attention", "acceptance", "sampling"};
 
 Tensor workspace(const at::Device& dev, void* stream, int kind, int64_t bytes) {
   std::lock_guard<std::mutex> lock(g_ws_mu);
-  Tensor& t = g_ws[{dev.index(), stream, kind}];
-  if (!t.defined() || t.numel() < bytes) {
-    const int64_t n = t.defined() ? std::max(bytes, 2 * t.numel()) : bytes;
-    t = at::zeros({n}, at::TensorOptions().dtype(at::kByte).device(dev));
+  Workspace& w = g_ws[{dev.index(), stream, kind}];
+  if (!w.cur.defined() || w.cur.numel() < bytes) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cs);
+    TORCH_CHECK(e == hipSuccess, "hipStreamIsCapturing failed: ", hipGetErrorString(e));
+    TORCH_CHECK(cs == hipStreamCaptureStatusNone, "the ", kWsNames[kind],
+                " workspace of this stream needs ", bytes, " bytes (has ",
+                w.cur.defined() ? w.cur.numel() : 0,
+                ") while the stream is being captured; make one eager call of the largest "
+                "shape on this stream before capturing");
+    const int64_t n = w.cur.defined() ? std::max(bytes, 2 * w.cur.numel()) : bytes;
+    if (w.cur.defined()) w.retired.push_back(w.cur);
+    w.cur = at::zeros({n}, at::TensorOptions().dtype(at::kByte).device(dev));
   }
-  return t;
+  return w.cur;
 }
 
 enum { kAttnWs = 0, kAcceptWs = 1, kSampleWs = 2 };
@@ -326,6 +352,31 @@ std::tuple<Tensor, Tensor, Tensor> spec_accept(
                       ws.data_ptr(), ws.numel(), s),
       "nsg_spec_accept");
   return {n_out, emitted, rollback};
+}
+
+// The error flags of nsg::spec_accept's workspace for the current stream of
+// `device` (bits of nsg_spec_accept: 1 a rolled-back position past its pages,
+// 2 a draft token outside the vocabulary, 3 a hand-off wait gave up), read
+// and cleared; after bit 3 the whole workspace is zeroed again.  Synchronises
+// the stream.  0 when the stream has no acceptance workspace yet.
+int64_t spec_accept_check_flags(at::Device device) {
+  TORCH_CHECK(device.is_cuda(), "spec_accept_check_flags: a GPU device is required");
+  const at::Device dev(device.type(), device.has_index() ? device.index()
+                                                          : c10::hip::current_device());
+  const DeviceGuard guard(dev);
+  void* s = static_cast<void*>(
+      c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(dev.index()).stream());
+  Tensor ws;
+  {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    auto it = g_ws.find({dev.index(), s, kAcceptWs});
+    if (it == g_ws.end() || !it->second.cur.defined()) return 0;
+    ws = it->second.cur;
+  }
+  int32_t flags = 0;
+  check_status(nsg_spec_accept_check_flags(ws.data_ptr(), ws.numel(), &flags, s),
+               "nsg_spec_accept_check_flags");
+  return flags;
 }
 
 Tensor sample(const Tensor& logits, double temperature, int64_t top_k, double top_p,
@@ -448,6 +499,7 @@ TORCH_LIBRARY(nsg, m) {
       "Tensor? uniforms, float temperature, Tensor? kv_indptr=None, Tensor? kv_indices=None, "
       "Tensor? start_pos=None, int page_size=16, Tensor? bonus_tokens=None) "
       "-> (Tensor, Tensor, Tensor)");
+  m.def("spec_accept_check_flags(Device device) -> int", &spec_accept_check_flags);
   m.def(
       "sample(Tensor logits, float temperature, int top_k=0, float top_p=1.0, "
       "Tensor? uniforms=None) -> Tensor");

@@ -475,17 +475,22 @@ class SpecEngine:
             self._record(g.tl.view(g.bs, k + 1, -1)[:B], drafts,
                          g.arena.h["start"][:B], kvp,
                          g.arena.h["idx"][k * sx:k * sx + int(kvp[-1])],
-                         g.n_out[:B], g.emitted[:B], g.rollback[:B], ttok)
+                         g.n_out[:B], g.emitted[:B], g.rollback[:B], ttok,
+                         None if g.dlog is None else g.dlog[:B],
+                         None if g.u is None else g.u[:B])
         return g.n_h.numpy()[:B], g.em_h.numpy()[:B]
 
     def _record(self, tl, drafts, start, kv_indptr, kv_indices, n_out, emitted, rollback,
-                target_tokens=None):
+                target_tokens=None, draft_logits=None, uniforms=None):
         """Append one step's verify logits, acceptance inputs and outputs to
         ``self.trace`` (host copies); ``target_tokens``: the verify rows'
         tokens of the greedy lm_head kernel, when the step accepted from
-        those."""
+        those; ``draft_logits`` / ``uniforms``: the stochastic acceptance's
+        other inputs."""
         self.trace.append({
             "target_tokens": None if target_tokens is None else target_tokens.cpu().numpy(),
+            "draft_logits": None if draft_logits is None else draft_logits.detach().cpu(),
+            "uniforms": None if uniforms is None else uniforms.cpu().numpy(),
             "verify_logits": tl.detach().cpu(), "drafts": drafts.cpu().numpy(),
             "start": np.asarray(start, np.int64).copy(),
             "kv_indptr": np.asarray(kv_indptr, np.int32).copy(),
@@ -556,7 +561,7 @@ class SpecEngine:
             page_size=self.P, bonus_tokens=self._bonus(tl.view(B, k + 1, -1), u))
         if self.trace is not None:
             self._record(tl.view(B, k + 1, -1), drafts, start_pos, kvp, idx, n_out, emitted,
-                         rollback)
+                         rollback, None, dlog, u)
         return n_out.cpu().numpy(), emitted.cpu().numpy()
 
     # ---- main entry ----
@@ -618,6 +623,29 @@ class SpecEngine:
             r.synced = min(r.synced, len(r.table.block_indices))
         return n_h
 
+    # device error bits of the attention and acceptance kernels (their
+    # workspaces' flag words), by kernel
+    _ATTN_FLAGS = {1: "a KV page id outside the pool (attention)"}
+    _ACCEPT_FLAGS = {2: "a rolled-back position past its request's pages (acceptance)",
+                     4: "a draft token outside the vocabulary (acceptance)",
+                     8: "an acceptance hand-off wait gave up; its outputs are undefined "
+                        "(the workspace was cleared)"}
+
+    def check_device_flags(self) -> None:
+        """Reads and clears the error flags the attention and acceptance
+        kernels raise on the device, and raises RuntimeError naming every
+        condition found, as the reference raises RuntimeError on bad KV state
+        (paged_kv_cache.py:88-89,116-119).  Synchronises the stream."""
+        found = []
+        a = self.attn.check_flags()
+        found += [msg for bit, msg in self._ATTN_FLAGS.items() if a & bit]
+        c = self._accept_ws.check_flags()
+        found += [msg for bit, msg in self._ACCEPT_FLAGS.items() if c & bit]
+        if a & ~1 or c & ~14:
+            found.append(f"unknown flag bits (attention {a:#x}, acceptance {c:#x})")
+        if found:
+            raise RuntimeError("device error flags: " + "; ".join(found))
+
     def _check_batch(self, n: int) -> None:
         if self.use_graphs and n > self.max_batch:
             raise ValueError(f"{n} requests > max_batch {self.max_batch} of the graphs")
@@ -625,14 +653,18 @@ class SpecEngine:
             self.capture()
 
     @torch.inference_mode()
-    def prefill(self, prompts: list[list[int]]):
+    def prefill(self, prompts: list[list[int]], synthetic_context: bool = False):
         """Admit and prefill ``prompts`` (additive API, with
         :meth:`speculative_step_batch`).  Returns (first tokens, block
         tables): request b's KV cache holds positions < len(prompts[b]) in
-        block_tables[b]; its first token sits at position len(prompts[b])."""
+        block_tables[b]; its first token sits at position len(prompts[b]).
+        ``synthetic_context``: as in :meth:`generate`, the prompt positions'
+        K/V are the pool's seeded noise and the first token is the prompt's
+        last id."""
         self._check_batch(len(prompts))
         reqs = [_Req(i, list(p), 1) for i, p in enumerate(prompts)]
-        self._admit(reqs)
+        self._admit(reqs, synthetic_context)
+        self.check_device_flags()
         return [r.out[0] for r in reqs], [r.table for r in reqs]
 
     @torch.inference_mode()
@@ -665,6 +697,7 @@ class SpecEngine:
             for i, r in enumerate(reqs):
                 r.row = i
         self._step(reqs)
+        self.check_device_flags()
         return [r.out[1:] for r in reqs]
 
     @torch.inference_mode()
@@ -704,7 +737,7 @@ class SpecEngine:
                 else:
                     still.append(r)
             active = still
-        torch.cuda.synchronize(self.device)
+        self.check_device_flags()           # synchronises the stream
         t_total = time.perf_counter() - t0
         n_tok = sum(len(r.out) for r in reqs)
         self.stats = {

@@ -361,12 +361,9 @@ class AcceptWorkspace:
         if self.buf.numel() == 0:
             return 0
         f = C.c_int32(0)
-        check(_lib().nsg_spec_accept_check_flags(self.buf.data_ptr(), C.byref(f),
-                                                 _stream_ptr(self.device)),
+        check(_lib().nsg_spec_accept_check_flags(self.buf.data_ptr(), self.buf.numel(),
+                                                 C.byref(f), _stream_ptr(self.device)),
               "nsg_spec_accept_check_flags")
-        if f.value & 8:
-            self.buf.zero_()
-            torch.cuda.synchronize(self.device)
         return f.value
 
 
@@ -720,16 +717,28 @@ def embed_rows(ids: torch.Tensor, table: torch.Tensor, out: torch.Tensor | None 
     return out
 
 
-def _fold_args(x, sumsq_in, norm_eps, residual, sumsq_out):
-    """C-ABI arguments of the folded RMSNorm (see nsg_linear_fold)."""
+MAX_SUMSQ_PARTS = 64     # partial sums per row a folded-norm consumer reads (nsg_linear_fold)
+
+
+def _fold_args(x, sumsq_in, norm_eps, residual, sumsq_out, n_out=None):
+    """C-ABI arguments of the folded RMSNorm (see nsg_linear_fold).  The C
+    ABI takes no sizes for ``residual`` / ``sumsq_out``: their shapes are
+    checked here, against M = x rows and the N = ``n_out`` columns written."""
+    M = x.shape[0]
     if sumsq_in is not None and (sumsq_in.dtype != torch.float32 or not sumsq_in.is_contiguous()
-                                 or sumsq_in.shape[1] != x.shape[0]):
-        raise ValueError("sumsq_in must be contiguous float32 (parts, M)")
-    if residual is not None and (residual.dtype != torch.bfloat16 or residual.stride(1) != 1):
-        raise ValueError("residual must be bf16 rows with unit inner stride")
+                                 or sumsq_in.dim() != 2 or sumsq_in.shape[1] != M
+                                 or not 1 <= sumsq_in.shape[0] <= MAX_SUMSQ_PARTS):
+        raise ValueError(f"sumsq_in must be contiguous float32 (parts <= {MAX_SUMSQ_PARTS}, "
+                         f"M = {M})")
+    if residual is not None and (residual.dtype != torch.bfloat16 or residual.dim() != 2
+                                 or residual.stride(1) != 1 or residual.shape[0] < M
+                                 or (n_out is not None and residual.shape[1] != n_out)):
+        raise ValueError(f"residual must be bf16 (>= {M}, {n_out}) rows with unit inner stride")
     if sumsq_out is not None and (sumsq_out.dtype != torch.float32
-                                  or not sumsq_out.is_contiguous()):
-        raise ValueError("sumsq_out must be contiguous float32")
+                                  or not sumsq_out.is_contiguous()
+                                  or (n_out is not None
+                                      and tuple(sumsq_out.shape) != (n_out // 16, M))):
+        raise ValueError(f"sumsq_out must be contiguous float32 ({n_out} // 16, {M})")
     return (_ptr(sumsq_in), 0 if sumsq_in is None else sumsq_in.shape[0], x.shape[1],
             float(norm_eps), _ptr(residual), 0 if residual is None else residual.stride(0),
             _ptr(sumsq_out))
@@ -831,7 +840,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
         check(lib.nsg_linear_fold(x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
                                   _ptr(bias), out.data_ptr(), out.stride(0), M, N, K,
                                   LINEAR_SILU_MUL if swiglu else LINEAR_BIAS,
-                                  *_fold_args(x, sumsq_in, norm_eps, residual, sumsq_out),
+                                  *_fold_args(x, sumsq_in, norm_eps, residual, sumsq_out, N),
                                   _stream_ptr(x.device)), "nsg_linear_fold")
         return out
     fits = (M <= lib.nsg_linear_max_rows() and K % 64 == 0 and N % 4 == 0 and x.stride(1) == 1

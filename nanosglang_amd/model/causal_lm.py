@@ -131,6 +131,7 @@ class CausalLM:
         self.lm_head = self.embed  # tie_word_embeddings
         self.rope_cos, self.rope_sin = rope_tables(c, self.device)
         self._fold = self._fold_norm_weights()
+        self.last_forward_folded = False
 
     def _fold_norm_weights(self) -> bool:
         """RMSNorm folded into the linears after it (bf16 weights, hidden a
@@ -211,6 +212,7 @@ class CausalLM:
         eps = c.rms_norm_eps
         T = input_ids.numel()
         folded = self._fold and T <= kernels._lib().nsg_linear_max_rows()
+        self.last_forward_folded = folded     # which norm path the call took
         ssa = None
         if self.embed.dtype == torch.bfloat16 and c.hidden_size % 16 == 0:
             # causal_lm.py:613 -- ids may be any (T,) or (B, J) view; with the

@@ -414,6 +414,65 @@ def test_fp8_linear_bit_exact_vs_bf16_kernel_on_dequantized_weights(M):
     assert torch.equal(q8, qb) and torch.equal(kc, kc2) and torch.equal(vc, vc2)
 
 
+@pytest.mark.parametrize("M", [1, 32, 64, 160])
+def test_fp8_linear_8b_shapes(M):
+    """FP8 weights at the large shape's decoder linears (hidden 4096, 32 / 8
+    heads of 128, FFN 14336): q/k/v 6144 x 4096 with RoPE + KV write, o_proj
+    4096 x 4096, gate_up 28672 x 4096 with SwiGLU, down 4096 x 14336.  Each
+    is bit-exact against the bf16 kernel on the dequantised weights (the
+    weight-streaming kernel's 8B-class tile shapes, bf16 and FP8 alike) and
+    within bf16 rounding of an fp32 product."""
+    from nanosglang_amd import kernels
+    from nanosglang_amd.model.causal_lm import ModelConfig, rope_tables
+    print(f"case: fp8 linear, 8B shapes, M={M}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(100 + M)
+    H, I, Hq, Hkv, D = 4096, 14336, 32, 8, 128
+    x = torch.randn(M, H, generator=g, device="cuda").bfloat16()
+    # q/k/v: bias path (no bias, as Llama) and RoPE + KV write
+    w8, s = _fp8_weights([Hq * D, Hkv * D, Hkv * D], H, seed=M + 7)
+    wd = kernels.dequant_fp8(w8, s)
+    y8 = kernels.linear(x, w8, w_scale=s, force=True)
+    assert torch.equal(y8, kernels.linear(x, wd, force=True))
+    _check_bias(y8, x, wd, None)
+    cfg = ModelConfig(model_type="llama", vocab_size=1000, hidden_size=H, intermediate_size=I,
+                      num_hidden_layers=1, num_attention_heads=Hq, num_key_value_heads=Hkv,
+                      max_position_embeddings=8192, rope_theta=5e5, attention_bias=False)
+    cos, sin = (t.cuda() for t in rope_tables(cfg, "cpu"))
+    pos = (torch.arange(M, device="cuda") * 37 + 2048) % 8192
+    slots = torch.arange(M, device="cuda") * 3
+    caches = [torch.zeros(3 * M, 1, Hkv, D, dtype=torch.bfloat16, device="cuda")
+              for _ in range(4)]
+    q8 = kernels.linear_rope_kv(x, w8, None, Hq, Hkv, D, pos, cos, sin, slots, caches[0],
+                                caches[1], w_scale=s, force=True)
+    qb = kernels.linear_rope_kv(x, wd, None, Hq, Hkv, D, pos, cos, sin, slots, caches[2],
+                                caches[3], force=True)
+    torch.cuda.synchronize()
+    assert torch.equal(q8, qb)
+    assert torch.equal(caches[0], caches[2]) and torch.equal(caches[1], caches[3])
+    # o_proj
+    w8, s = _fp8_weights([H], H, seed=M + 8)
+    wd = kernels.dequant_fp8(w8, s)
+    y8 = kernels.linear(x, w8, w_scale=s, force=True)
+    assert torch.equal(y8, kernels.linear(x, wd, force=True))
+    _check_bias(y8, x, wd, None)
+    # gate_up with SwiGLU (separate gate / up scales)
+    w8, s = _fp8_weights([I, I], H, seed=M + 9)
+    wd = kernels.dequant_fp8(w8, s)
+    y8 = kernels.linear(x, w8, swiglu=True, w_scale=s, force=True)
+    assert torch.equal(y8, kernels.linear(x, wd, swiglu=True, force=True))
+    gu = x.float() @ wd.float().T
+    ref = torch.nn.functional.silu(gu[:, :I]) * gu[:, I:]
+    assert ((y8.float() - ref).abs() <= 2.0 ** -6 * ref.abs() + 2e-3).all()
+    del w8, wd, gu
+    # down
+    xd = torch.randn(M, I, generator=g, device="cuda").bfloat16()
+    w8, s = _fp8_weights([H], I, seed=M + 10)
+    wd = kernels.dequant_fp8(w8, s)
+    y8 = kernels.linear(xd, w8, w_scale=s, force=True)
+    assert torch.equal(y8, kernels.linear(xd, wd, force=True))
+    _check_bias(y8, xd, wd, None)
+
+
 def test_fp8_linear_library_path_for_prefill_rows():
     from nanosglang_amd import kernels
     print("case: fp8 linear M=300 (library path)", flush=True)

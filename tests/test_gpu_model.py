@@ -106,19 +106,22 @@ def _tiny_models(scale=8.0, dtype=torch.float32):
     return CPUCausalLM(ocfg, wc), CausalLM(ModelConfig(**TINY), weights=w)
 
 
+@pytest.mark.parametrize("lens", [(40, 7, 129), (40, 7, 29)])
 @pytest.mark.parametrize("scale,dtype,tol", [(1.0, torch.float32, 2e-2),
                                              (3.0, torch.bfloat16, 5e-2)])
-def test_packed_forward_matches_cpu_oracle(scale, dtype, tol):
+def test_packed_forward_matches_cpu_oracle(scale, dtype, tol, lens):
     """bf16 GPU logits vs the oracle: at init scale against fp32 (relative
     error 2e-2), with 3x weights against the oracle in bf16 (5e-2; the oracle's
     own bf16-vs-fp32 gap there is 2.3e-2).  Argmax agreement >= 0.9: with 1000
     random logits even the oracle's bf16 and fp32 runs agree on only ~0.96-0.98
-    of positions."""
+    of positions.  176 packed rows take the separate RMSNorm kernels; 76 rows
+    (<= 160, every decode / verify / draft forward) take the norms folded into
+    the linears (bf16(w_ln * W), one rounding), asserted to have run."""
     from nanosglang_amd.engine.paged_kv_cache import BlockManager, PagedKVCache
     from nanosglang_amd.kernels import BatchPrefillWithPagedKVCacheWrapper
     cpu, gpu = _tiny_models(scale, dtype)
     rng = np.random.default_rng(0)
-    prompts = [rng.integers(0, 1000, n).tolist() for n in (40, 7, 129)]
+    prompts = [rng.integers(0, 1000, n).tolist() for n in lens]
     bm = BlockManager(64, 16, 4, 2, 64, torch.bfloat16, "cuda")
     kv = PagedKVCache(bm)
     tables = [kv.allocate_for_request(len(p)) for p in prompts]
@@ -134,6 +137,7 @@ def test_packed_forward_matches_cpu_oracle(scale, dtype, tol):
     slots = torch.tensor(np.concatenate([kv.slots(t, 0, n) for t, n in zip(tables, lens)]),
                          device="cuda")
     got = gpu.forward_packed(ids, pos, (bm.k_cache, bm.v_cache), w, slots).float().cpu()
+    assert gpu.last_forward_folded == (sum(lens) <= 160)
     off = 0
     for p in prompts:
         S = len(p)
@@ -147,6 +151,60 @@ def test_packed_forward_matches_cpu_oracle(scale, dtype, tol):
         assert rel < tol
         assert agree >= 0.9
         off += S
+
+
+@pytest.mark.parametrize("scale,dtype,tol", [(1.0, torch.float32, 2e-2),
+                                             (3.0, torch.bfloat16, 5e-2)])
+def test_decode_rows_match_cpu_oracle(scale, dtype, tol):
+    """A decode-shaped forward -- one new token per request on top of its
+    cached prompt, the rows the folded norms serve in every draft step --
+    against the oracle's last row of the whole sequence, at the bars of the
+    packed test; two steps, so the second reads KV the first step wrote."""
+    from nanosglang_amd.engine.paged_kv_cache import BlockManager, PagedKVCache
+    from nanosglang_amd.kernels import BatchPrefillWithPagedKVCacheWrapper
+    cpu, gpu = _tiny_models(scale, dtype)
+    rng = np.random.default_rng(5)
+    seqs = [rng.integers(0, 1000, n).tolist() for n in (40, 7, 29, 16)]
+    B = len(seqs)
+    bm = BlockManager(64, 16, 4, 2, 64, torch.bfloat16, "cuda")
+    kv = PagedKVCache(bm)
+    tables = [kv.allocate_for_request(len(p)) for p in seqs]
+    ws = torch.empty(32 << 20, dtype=torch.uint8, device="cuda")
+
+    def run(rows_per_req, starts):
+        lens = [s + n for s, n in zip(starts, rows_per_req)]
+        for t, L in zip(tables, lens):
+            kv.reserve(t, L)
+        qo = np.concatenate([[0], np.cumsum(rows_per_req)]).astype(np.int32)
+        npg = [(L + 15) // 16 for L in lens]
+        kvp = np.concatenate([[0], np.cumsum(npg)]).astype(np.int32)
+        idx = np.concatenate([t.block_indices[:n] for t, n in zip(tables, npg)]).astype(np.int32)
+        last = np.asarray([L - (n - 1) * 16 for L, n in zip(lens, npg)], np.int32)
+        w = BatchPrefillWithPagedKVCacheWrapper(ws)
+        w.plan(qo, kvp, idx, last, 4, 2, 64, 16, causal=True)
+        ids = torch.tensor(np.concatenate([p[s:s + n] for p, s, n in
+                                           zip(seqs, starts, rows_per_req)]), device="cuda")
+        pos = torch.tensor(np.concatenate([np.arange(s, s + n) for s, n in
+                                           zip(starts, rows_per_req)]), device="cuda")
+        slots = torch.tensor(np.concatenate([kv.slots(t, s, n) for t, s, n in
+                                             zip(tables, starts, rows_per_req)]), device="cuda")
+        return gpu.forward_packed(ids, pos, (bm.k_cache, bm.v_cache), w, slots).float().cpu()
+
+    run([len(p) for p in seqs], [0] * B)                 # prefill (packed rows)
+    for step in range(2):
+        starts = [len(p) for p in seqs]
+        for p in seqs:
+            p.append(int(rng.integers(0, 1000)))
+        got = run([1] * B, starts)
+        assert gpu.last_forward_folded
+        for b, p in enumerate(seqs):
+            S = len(p)
+            cache = [(a.to(dtype), c.to(dtype)) for a, c in cpu.new_cache(1, S)]
+            ref = cpu.forward(torch.tensor([p]), torch.arange(S)[None], cache, 0,
+                              causal_mask(S, S, dtype))[0, -1].float()
+            rel = ((got[b] - ref).norm() / ref.norm()).item()
+            print(f"  step {step} request {b} (S={S}): rel err {rel:.3e}", flush=True)
+            assert rel < tol
 
 
 @pytest.mark.parametrize("graphs", [True, False])
@@ -441,3 +499,29 @@ def test_capture_sizes_workspaces_for_every_graph():
         assert not ws._retired
     assert [len(o) for o in out] == max_new
     assert all(0 <= t < 1000 for o in out for t in o)
+
+
+@pytest.mark.parametrize("graphs", [True, False])
+def test_engine_raises_on_device_error_flags(graphs):
+    """A block table that names a page outside the KV pool: the attention
+    kernel reads the pool's first page instead and raises its device flag,
+    and the engine turns the flag into a RuntimeError naming it (the
+    reference raises RuntimeError on bad KV state, paged_kv_cache.py:88-89,
+    116-119).  The flags are cleared by the read: with the table repaired
+    the next step runs clean."""
+    from nanosglang_amd.engine.spec_engine import SpecEngine
+    print(f"case: engine device-flag check, graphs={graphs}", flush=True)
+    _, gpu = _tiny_models()
+    rng = np.random.default_rng(9)
+    prompts = [rng.integers(0, 1000, n).tolist() for n in (40, 33)]
+    eng = SpecEngine(gpu, draft_layers=2, num_speculative=4, num_blocks=64, use_graphs=graphs,
+                     max_batch=4)
+    first, tables = eng.prefill(prompts)
+    start = [len(p) for p in prompts]
+    good = tables[0].block_indices[0]
+    tables[0].block_indices[0] = 64 + 5               # the pool has pages 0..63
+    with pytest.raises(RuntimeError, match="page id outside the pool"):
+        eng.speculative_step_batch(first, start, tables)
+    tables[0].block_indices[0] = good
+    res = eng.speculative_step_batch(first, start, tables)
+    assert all(1 <= len(r) <= 5 for r in res)

@@ -138,3 +138,75 @@ def test_kv_write_operators_equal_the_wrappers():
     assert torch.equal(caches[0], caches[2]) and torch.equal(caches[1], caches[3])
     flat = caches[0].view(-1, Hkv, D)
     assert torch.equal(flat[slots], k)
+
+
+def _accept_args(B, k, V, seed, T=0.8):
+    a = workloads.acceptance_batch(batch=B, k=k, vocab=V, seed=seed)
+    u = torch.rand(B, k + 1, generator=torch.Generator().manual_seed(seed)).cuda()
+    return (_dev(a["target"]), _dev(a["draft"]), _dev(a["draft_tokens"], torch.int64), u, T)
+
+
+def test_spec_accept_operator_graph_keeps_its_workspace_after_growth():
+    """A graph captured around nsg::spec_accept keeps using the per-stream
+    workspace it was captured with: after a larger eager call on the same
+    stream grows that workspace, every replay still equals a call on a fresh
+    workspace (the replaced buffer stays allocated), and so does the larger
+    call."""
+    print("case: nsg::spec_accept captured, then its workspace grown", flush=True)
+    small, big = _accept_args(8, 4, 5000, 31), _accept_args(64, 4, 151936, 32)
+    ref_small = kernels.spec_accept(*small, workspace=kernels.AcceptWorkspace("cuda"))
+    ref_big = kernels.spec_accept(*big, workspace=kernels.AcceptWorkspace("cuda"))
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        torch.ops.nsg.spec_accept(*small)            # creates the stream's workspace
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            out = torch.ops.nsg.spec_accept(*small)
+        for rep in range(3):
+            got_big = torch.ops.nsg.spec_accept(*big)  # the first one grows the workspace
+            g.replay()
+            s.synchronize()
+            for x, y in zip(out, ref_small):
+                assert torch.equal(x, y), rep
+            for x, y in zip(got_big, ref_big):
+                assert torch.equal(x, y), rep
+        assert torch.ops.nsg.spec_accept_check_flags(torch.device("cuda", 0)) == 0
+    del g
+    torch.cuda.synchronize()
+
+
+def test_spec_accept_operator_refuses_to_grow_its_workspace_under_capture():
+    """A first nsg::spec_accept call on a stream that is being captured would
+    allocate its workspace from the graph's private pool: it raises instead,
+    before any kernel is enqueued."""
+    print("case: nsg::spec_accept workspace growth under capture", flush=True)
+    args = _accept_args(8, 4, 5000, 33)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with pytest.raises(RuntimeError, match="being captured"):
+            with torch.cuda.graph(g, stream=s):
+                torch.ops.nsg.spec_accept(*args)
+    del g
+    torch.cuda.synchronize()
+
+
+def test_spec_accept_check_flags_operator_reports_device_errors():
+    """nsg::spec_accept_check_flags returns and clears the error bits of the
+    current stream's acceptance workspace: a draft token outside the
+    vocabulary sets bit 2 (that request is rejected at position 0)."""
+    print("case: nsg::spec_accept_check_flags", flush=True)
+    dev = torch.device("cuda", 0)
+    tl, dl, dt, u, T = _accept_args(8, 4, 5000, 34)
+    torch.ops.nsg.spec_accept(tl, dl, dt, u, T)
+    assert torch.ops.nsg.spec_accept_check_flags(dev) == 0
+    bad = dt.clone()
+    bad[3, 0] = 5000
+    n, em, _ = torch.ops.nsg.spec_accept(tl, dl, bad, u, T)
+    assert torch.ops.nsg.spec_accept_check_flags(dev) == 4
+    assert torch.ops.nsg.spec_accept_check_flags(dev) == 0
+    assert int(n[3]) == 1 and 0 <= int(em[3, 0]) < 5000

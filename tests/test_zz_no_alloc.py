@@ -3,7 +3,8 @@ called through the C ABI: its outputs equal nsg_spec_accept's bit for bit,
 greedy and stochastic, on two calls in a row -- the second with a smaller
 input, so the static scratch holds the first call's contents when it runs --
 and the device error flags reach the caller's word; an input whose workspace
-exceeds the static scratch is refused without a launch."""
+exceeds the static scratch is refused without a launch; the scratch reset
+leaves it working."""
 import ctypes as C
 
 import numpy as np
@@ -96,3 +97,21 @@ def test_noalloc_reports_flags_and_refuses_oversized_inputs():
                                      None, torch.cuda.current_stream().cuda_stream)
     assert rc == 3                                        # NSG_ERR_WORKSPACE, nothing launched
     assert b"static scratch" in lib.nsg_last_error()
+
+
+def test_noalloc_reset_leaves_a_working_scratch():
+    """nsg_spec_accept_noalloc_reset (the recovery after flag bit 3) zeroes
+    the static scratch with a fill kernel: calls after it still equal
+    nsg_spec_accept, stochastic then greedy."""
+    lib = _native.load()
+    print("case: nsg_spec_accept_noalloc_reset", flush=True)
+    stream = torch.cuda.current_stream().cuda_stream
+    for temperature in (0.8, 0.0):
+        _native.check(lib.nsg_spec_accept_noalloc_reset(stream), "nsg_spec_accept_noalloc_reset")
+        inp = _inputs(16, 4, 20000, 35)
+        ws = torch.zeros(lib.nsg_spec_accept_workspace_bytes(16, 4, 20000), dtype=torch.uint8,
+                         device="cuda")
+        ref = _call(lib, inp, temperature, False, ws=ws)
+        got = _call(lib, inp, temperature, True)
+        for r, g in zip(ref, got):
+            np.testing.assert_array_equal(g, r)

@@ -32,11 +32,23 @@ HIPCC_FLAGS = [
 # Per-file additions.  spec_accept.hip: logits are never NaN (a NaN logit
 # makes the reference's softmax NaN too), so max/min need no NaN
 # canonicalisation -- it doubled the cost of the per-logit max in the
-# acceptance pass.  linear.hip, lm_head.hip: their asm copies into LDS set
+# acceptance pass.  verify_attention.hip likewise: its scores come from
+# finite Q and K (masked ones are a finite sentinel), and the canonicalising
+# maxes were 100 of the kernel's 3,240 instructions.  linear.hip, lm_head.hip: their asm copies into LDS set
 # m0 and say so in their clobber lists, which the compiler warns about for
 # every kernel instance (the files' kernels use m0 for nothing else).
-FILE_FLAGS = {"spec_accept.hip": ["-fno-honor-nans"], "linear.hip": ["-Wno-inline-asm"],
-              "lm_head.hip": ["-Wno-inline-asm"]}
+# The files with MFMA kernels keep the accumulators in ordinary VGPRs
+# (-amdgpu-mfma-vgpr-form): left to its heuristics the compiler put them in
+# AGPRs and copied them back and forth around every softmax / epilogue step
+# (about 490 v_accvgpr moves in the verify-shape attention kernel, 4,200 in
+# linear.hip); measured 8.74 -> 8.40 us per cache-cold verify-shape
+# attention launch, 80 -> 77 us for the 160-row lm_head, 12,000 -> 12,160
+# tok/s end to end, outputs bit-identical.
+MFMA_VGPR = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+FILE_FLAGS = {"spec_accept.hip": ["-fno-honor-nans"],
+              "linear.hip": ["-Wno-inline-asm", *MFMA_VGPR],
+              "lm_head.hip": ["-Wno-inline-asm", *MFMA_VGPR],
+              "verify_attention.hip": ["-fno-honor-nans", *MFMA_VGPR]}
 
 
 def _hipcc() -> str:

@@ -468,16 +468,26 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
       if (it < n_it) issue(it, it);
   }
 
-  for (int it0 = 0; it0 < per; it0 += kNBuf) {
+  // Groups of one wave have no barrier inside the loop and run only their
+  // own steps; the waves of a larger group all run `per` iterations so that
+  // their barriers stay matched.
+  const int n_loop = RT == 1 ? n_it : per;
+  for (int it0 = 0; it0 < n_loop; it0 += kNBuf) {
 #pragma unroll
     for (int slot = 0; slot < kNBuf; ++slot) {  // unrolled: ring slot is a constant
       const int it = it0 + slot;
-      if (it >= per) break;
-      const bool real = it < n_it;
+      if (it >= n_loop) break;
+      const bool real = RT == 1 || it < n_it;
       if (real) {
-        // steps issued so far: min(n_it, max(PF, it + kNBuf - 1)); wait
-        // until at most those after `it` are in flight
-        wait_steps<NI, PF - 1>(min(n_it, max(PF, it + kNBuf - 1)) - 1 - it);
+        // Steps issued so far: min(n_it, max(PF, it + kNBuf - 1)); wait until
+        // at most those after `it` are in flight.  With several groups (PF =
+        // kNBuf) that is min(steps left, kNBuf - 2) past the first iteration,
+        // which the common case settles with one compare.
+        const int left = n_it - 1 - it;
+        if (KS > 1 && (slot > 0 || it0 > 0))
+          wait_steps<NI, kNBuf - 2>(min(left, kNBuf - 2));
+        else
+          wait_steps<NI, PF - 1>(min(n_it, max(PF, it + kNBuf - 1)) - 1 - it);
       }
       if constexpr (RT > 1) {
         // step `it` landed for every wave of the group and slot (it - 1) is

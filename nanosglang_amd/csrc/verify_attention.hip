@@ -662,66 +662,105 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
   if (bad_page) atomicOr(p.flags, 1);
   // ---- the 4 lane groups sharing query row r16 hold partial sums ----
   float l = sum_xor16_32(l_run);
-  // d tiles this wave finishes: all of them with one KV group; with several,
-  // group g finishes the tiles dt = g (mod KS) of its rows, so every wave
-  // shares the combine and the output stores
-  auto own = [&](int dt) { return KS == 1 || dt % KS == grp; };
-  if constexpr (KS > 1) {
-    // ---- combine the KV groups through LDS (the rings are idle: every
-    //      group's last real step waited for all of its copies) ----
-    constexpr int SROW = D + 4;  // O[D], m, l, 2 pad
-    float* sc = reinterpret_cast<float*>(&ring[0][0][0][0]);
-    static_assert((size_t)KS * ROWS * SROW * 4 <= (size_t)kRingBytes,
-                  "combine scratch fits the rings");
-    __syncthreads();
-    float* mine = sc + ((size_t)grp * ROWS + row) * SROW;
+  if constexpr (KS == 1) {
+    if (!row_ok) return;
+    if (nsplit == 1) {
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      bf16* orow = p.out + ((size_t)(qs + tau) * p.Hq + h * G + gam) * D + 4 * g4;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-      if (!own(dt)) *reinterpret_cast<floatx4*>(mine + dt * 16 + 4 * g4) = oacc[dt];
-    if (g4 == 0) {
-      mine[D] = m_run;
-      mine[D + 1] = l;
-    }
-    __syncthreads();
-    float M = kMaskVal;
-#pragma unroll
-    for (int g = 0; g < KS; ++g) M = fmaxf(M, sc[((size_t)g * ROWS + row) * SROW + D]);
-    const float wself = __builtin_amdgcn_exp2f(m_run - M);
-    l *= wself;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-      if (own(dt)) oacc[dt] *= wself;
-#pragma unroll
-    for (int g = 0; g < KS; ++g) {
-      if (g == grp) continue;
-      const float* o = sc + ((size_t)g * ROWS + row) * SROW;
-      const float wgt = __builtin_amdgcn_exp2f(o[D] - M);
-      l += wgt * o[D + 1];
+      for (int dt = 0; dt < DT; ++dt) {
+        const floatx4 o = oacc[dt];
+        *reinterpret_cast<u32x2*>(orow + dt * 16) =
+            u32x2{cvt_pk_bf16(o[0] * inv, o[1] * inv), cvt_pk_bf16(o[2] * inv, o[3] * inv)};
+      }
+    } else {
+      float* prow = p.partials + ((size_t)wi * p.Hkv + h) * ROWS * PSTRIDE + (size_t)row * PSTRIDE;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
-        if (own(dt)) oacc[dt] += wgt * *reinterpret_cast<const floatx4*>(o + dt * 16 + 4 * g4);
-    }
-    m_run = M;
-  }
-  if (!row_ok) return;
-  if (nsplit == 1) {
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    bf16* orow = p.out + ((size_t)(qs + tau) * p.Hq + h * G + gam) * D + 4 * g4;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      if (!own(dt)) continue;
-      const floatx4 o = oacc[dt];
-      *reinterpret_cast<u32x2*>(orow + dt * 16) =
-          u32x2{cvt_pk_bf16(o[0] * inv, o[1] * inv), cvt_pk_bf16(o[2] * inv, o[3] * inv)};
+        *reinterpret_cast<floatx4*>(prow + dt * 16 + 4 * g4) = oacc[dt];
+      if (g4 == 0) {
+        prow[D] = m_run;
+        prow[D + 1] = l;
+      }
     }
   } else {
-    float* prow = p.partials + ((size_t)wi * p.Hkv + h) * ROWS * PSTRIDE + (size_t)row * PSTRIDE;
+    // ---- combine the KV groups through LDS.  Every group writes its
+    //      partial (O, m, l); group g then finishes the d tiles g, g + KS, ...
+    //      of its rows from all KS partials, so every wave shares the
+    //      combine and the output stores.  No branch depends on the group:
+    //      its tiles are addressed, not selected. ----
+    constexpr int SROW = D + 4;   // O[D], m, l, 2 pad
+    constexpr int OWN = DT / KS;  // d tiles each group finishes
+    static_assert(DT % KS == 0, "d tiles split evenly over the KV groups");
+    // Single-wave groups write into their own ring, idle once the wave's
+    // last step is read (all of its copies landed before that step), so one
+    // barrier suffices; the waves of a larger group share a ring and wait for
+    // each other first.
+    float* sc = reinterpret_cast<float*>(&ring[0][0][0][0]);
+    auto part = [&](int g) {
+      return RT == 1 ? reinterpret_cast<float*>(&ring[g][0][0][0]) + (size_t)row * SROW
+                     : sc + ((size_t)g * ROWS + row) * SROW;
+    };
+    static_assert(RT == 1 ? (size_t)ROWS * SROW * 4 <= (size_t)kNBuf * 2 * TILE * 2
+                          : (size_t)KS * ROWS * SROW * 4 <= (size_t)kRingBytes,
+                  "combine partials fit the rings");
+    if constexpr (RT > 1) __syncthreads();
+    {
+      float* mine = part(grp);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-      if (own(dt)) *reinterpret_cast<floatx4*>(prow + dt * 16 + 4 * g4) = oacc[dt];
-    if (g4 == 0 && grp == 0) {
-      prow[D] = m_run;
-      prow[D + 1] = l;
+      for (int dt = 0; dt < DT; ++dt)
+        *reinterpret_cast<floatx4*>(mine + dt * 16 + 4 * g4) = oacc[dt];
+      // (the four lane groups of a row hold the same m and l)
+      *reinterpret_cast<floatx2*>(mine + D) = floatx2{m_run, l};
+    }
+    __syncthreads();
+    // every group's (m, l) and this group's d tiles of every partial, read
+    // in one batch
+    float mg[KS], lg[KS];
+    floatx4 og[KS][OWN];
+#pragma unroll
+    for (int g = 0; g < KS; ++g) {
+      const float* o = part(g);
+      const floatx2 ml = *reinterpret_cast<const floatx2*>(o + D);
+      mg[g] = ml[0];
+      lg[g] = ml[1];
+#pragma unroll
+      for (int j = 0; j < OWN; ++j)
+        og[g][j] = *reinterpret_cast<const floatx4*>(o + (grp + KS * j) * 16 + 4 * g4);
+    }
+    float M = mg[0];
+#pragma unroll
+    for (int g = 1; g < KS; ++g) M = fmaxf(M, mg[g]);
+    float lsum = 0.f;
+    floatx4 acc[OWN];
+#pragma unroll
+    for (int j = 0; j < OWN; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < KS; ++g) {
+      const float w = __builtin_amdgcn_exp2f(mg[g] - M);
+      lsum += w * lg[g];
+#pragma unroll
+      for (int j = 0; j < OWN; ++j) acc[j] += w * og[g][j];
+    }
+    if (!row_ok) return;
+    if (nsplit == 1) {
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      bf16* orow = p.out + ((size_t)(qs + tau) * p.Hq + h * G + gam) * D + 4 * g4;
+#pragma unroll
+      for (int j = 0; j < OWN; ++j) {
+        const floatx4 o = acc[j];
+        *reinterpret_cast<u32x2*>(orow + (grp + KS * j) * 16) =
+            u32x2{cvt_pk_bf16(o[0] * inv, o[1] * inv), cvt_pk_bf16(o[2] * inv, o[3] * inv)};
+      }
+    } else {
+      float* prow = p.partials + ((size_t)wi * p.Hkv + h) * ROWS * PSTRIDE + (size_t)row * PSTRIDE;
+#pragma unroll
+      for (int j = 0; j < OWN; ++j)
+        *reinterpret_cast<floatx4*>(prow + (grp + KS * j) * 16 + 4 * g4) = acc[j];
+      if (g4 == 0 && grp == 0) {
+        prow[D] = M;
+        prow[D + 1] = lsum;
+      }
     }
   }
 }

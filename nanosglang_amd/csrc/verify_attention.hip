@@ -323,6 +323,7 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
   int d_off[NI];
   int d_lds[NI];
   bool d_v[NI];
+  bool d_hi[NI];  // the copy's rows are tokens 16..31 of the step
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int j = (wave + RT * i) % NINST;      // padding repeats a real copy
@@ -335,6 +336,7 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
     d_off[i] = lc * 8;
     d_lds[i] = which * TILE + jj * TPI * D;
     d_v[i] = which != 0;
+    d_hi[i] = jj * TPI >= 16;  // (16 is a multiple of TPI: a copy never straddles)
   }
   // Pages of at least 16 tokens: a step (32 tokens from a multiple of 32)
   // spans at most two pages, and each copy's offset inside its page is fixed,
@@ -393,12 +395,26 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
     const uint32_t rowb = (uint32_t)(t0 & (P - 1)) * (uint32_t)(tok_stride * 2);  // < one page
     const uint64_t offa = oka ? (uint64_t)(uint32_t)pga * page_bytes : 0;
     const uint64_t offb = okb ? (uint64_t)(uint32_t)pgb * page_bytes : 0;
+    if (t0 + kTokIt - 1 <= last_tok) {
+      // a full step (every step but an item's last): the address is a
+      // wave-uniform page base plus the lane's fixed 32-bit offset, so each
+      // copy is one instruction with a scalar base
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const char* base =
+            reinterpret_cast<const char*>(d_v[i] ? p.vc : p.kc) + (d_hi[i] ? offb : offa) + rowb;
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(base + lo_row[i]),
+                                         static_cast<void*>(&ring[grp][slot][0][0] + d_lds[i]),
+                                         16, 0, kDmaPolicy);
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const char* base = reinterpret_cast<const char*>(d_v[i] ? p.vc : p.kc);
       const bool in = t0 + d_t[i] <= last_tok;
       const char* src =
-          base + ((in && d_t[i] >= 16) ? offb : offa) + ((in ? lo_row[i] : lo_end[i]) + rowb);
+          base + ((in && d_hi[i]) ? offb : offa) + ((in ? lo_row[i] : lo_end[i]) + rowb);
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
                                        static_cast<void*>(&ring[grp][slot][0][0] + d_lds[i]), 16,
                                        0, kDmaPolicy);

@@ -43,7 +43,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 17
+#define NSG_ABI_VERSION 18
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -178,6 +178,26 @@ int32_t nsg_spec_step_fill(const int32_t* page_table, int64_t page_table_stride,
                            int32_t dummy_page, int32_t num_qo_heads, int32_t num_kv_heads,
                            int32_t head_dim, int32_t num_cus, int32_t max_kv_len,
                            const nsg_spec_step_bufs_t* bufs, nsg_attn_plan_t* plans);
+
+/* nsg_spec_step_fill for the step after one whose results just arrived, for
+ * an engine that queued that next step before those results (see the host
+ * gate below): request j of the finished step (rows[j], num_pages[j],
+ * start_pos[j]) emitted n_emitted[j] tokens emitted[j * (k + 1) + 0 ..
+ * n_emitted[j] - 1] and had to_go[j] tokens left to produce before it.  The
+ * requests with to_go[j] > n_emitted[j] continue, in order, at start_pos[j] +
+ * n_emitted[j] with their last emitted token; *next_batch receives their
+ * count.  No separate reference line: it is the reference's per-request
+ * bookkeeping (speculative.py:184-196, positions and last token) folded into
+ * the next step's fill. */
+int32_t nsg_spec_step_fill_next(const int32_t* page_table, int64_t page_table_stride,
+                                const int32_t* rows, const int32_t* num_pages,
+                                const int64_t* start_pos, const int64_t* to_go,
+                                const int32_t* n_emitted, const int64_t* emitted, int32_t batch,
+                                int32_t padded_batch, int32_t k, int32_t page_size,
+                                int32_t dummy_page, int32_t num_qo_heads, int32_t num_kv_heads,
+                                int32_t head_dim, int32_t num_cus, int32_t max_kv_len,
+                                const nsg_spec_step_bufs_t* bufs, nsg_attn_plan_t* plans,
+                                int32_t* next_batch);
 
 /* ------------------------------------------------------------------------
  * Fused acceptance: ratio test, residual resample, bonus token and rollback
@@ -519,6 +539,35 @@ int32_t nsg_embed_rows(const int64_t* ids, int64_t id_stride_b, int64_t id_strid
  * ---------------------------------------------------------------------- */
 int32_t nsg_philox_uniform(uint64_t seed, uint32_t stream_id, uint64_t offset, int64_t n,
                            float* out, nsg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Host gate.  No single reference line: the reference's step loop is
+ * synchronous (read a step's results, build the next inputs, launch; its
+ * engine around nano_sglang/decode/speculative.py:50-184).  These let an
+ * engine queue step s + 1 while step s runs and release it once the host has
+ * written step s + 1's inputs.
+ *
+ * nsg_host_gate_alloc: a 64-byte coherent pinned host word pair, zeroed;
+ *   *flag is a host pointer the GPU can also read.  nsg_host_gate_free frees it.
+ * nsg_host_gate_wait: enqueues one small kernel that waits until *flag != 0
+ *   (system-scope reads), copies nbytes (a multiple of 16, both pointers
+ *   16-byte aligned; 0 = no copy) from the pinned host buffer src_host to
+ *   the device buffer dst, then writes *flag = 0.  After timeout_us (at most
+ *   60 s) it stops waiting, sets bit 0 of the device word *err, copies and
+ *   returns: the work queued after it then runs on whatever inputs are there.
+ * The host raises the flag with a plain store of 1 after writing the inputs
+ * (and not again before the gate has run).
+ * ---------------------------------------------------------------------- */
+/* nsg_export_step: n_host[i] = n_emitted[i] (i < rows) and emitted_host[i] =
+ * emitted[i] (i < rows * cols), by one kernel (graph-capturable) writing
+ * straight into pinned host memory: a step's emitted counts and tokens for
+ * the host, without copy commands after the step. */
+int32_t nsg_export_step(const int32_t* n_emitted, const int64_t* emitted, int32_t rows,
+                        int32_t cols, int32_t* n_host, int64_t* emitted_host, nsg_stream_t stream);
+int32_t nsg_host_gate_alloc(int32_t** flag);
+int32_t nsg_host_gate_free(int32_t* flag);
+int32_t nsg_host_gate_wait(int32_t* flag, int32_t* err, int64_t timeout_us,
+                           const void* src_host, void* dst, int64_t nbytes, nsg_stream_t stream);
 
 #ifdef __cplusplus
 }

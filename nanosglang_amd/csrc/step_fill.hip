@@ -17,6 +17,7 @@
 //   padding rows: every page the dummy page, start 0, token 0 (engine.py:378-391).
 #include <climits>
 #include <cstring>
+#include <vector>
 
 #include "common.hpp"
 
@@ -24,6 +25,13 @@ namespace nsg {
 namespace {
 
 constexpr int kMaxDrafts = 32;
+
+int32_t fill_impl(const int32_t* page_table, int64_t page_table_stride, const int32_t* rows,
+                  const int32_t* num_pages, const int64_t* start_pos, const int64_t* last_token,
+                  int32_t batch, int32_t padded_batch, int32_t k, int32_t page_size,
+                  int32_t dummy_page, int32_t num_qo_heads, int32_t num_kv_heads,
+                  int32_t head_dim, int32_t num_cus, int32_t max_kv_len,
+                  const nsg_spec_step_bufs_t* bufs, nsg_attn_plan_t* plans);
 
 }  // namespace
 }  // namespace nsg
@@ -38,6 +46,58 @@ extern "C" int32_t nsg_spec_step_fill(const int32_t* page_table, int64_t page_ta
                                       int32_t num_qo_heads, int32_t num_kv_heads,
                                       int32_t head_dim, int32_t num_cus, int32_t max_kv_len,
                                       const nsg_spec_step_bufs_t* bufs, nsg_attn_plan_t* plans) {
+  return fill_impl(page_table, page_table_stride, rows, num_pages, start_pos, last_token, batch,
+                   padded_batch, k, page_size, dummy_page, num_qo_heads, num_kv_heads, head_dim,
+                   num_cus, max_kv_len, bufs, plans);
+}
+
+extern "C" int32_t nsg_spec_step_fill_next(
+    const int32_t* page_table, int64_t page_table_stride, const int32_t* rows,
+    const int32_t* num_pages, const int64_t* start_pos, const int64_t* to_go,
+    const int32_t* n_emitted, const int64_t* emitted, int32_t batch, int32_t padded_batch,
+    int32_t k, int32_t page_size, int32_t dummy_page, int32_t num_qo_heads,
+    int32_t num_kv_heads, int32_t head_dim, int32_t num_cus, int32_t max_kv_len,
+    const nsg_spec_step_bufs_t* bufs, nsg_attn_plan_t* plans, int32_t* next_batch) {
+  NSG_CHECK_ARG(next_batch != nullptr, "null next_batch");
+  NSG_CHECK_ARG(batch >= 0 && batch <= padded_batch, "batch %d outside [0, padded_batch %d]",
+                batch, padded_batch);
+  NSG_CHECK_ARG(k >= 0 && k <= kMaxDrafts, "k %d outside [0, %d]", k, kMaxDrafts);
+  NSG_CHECK_ARG(batch == 0 || (rows && num_pages && start_pos && to_go && n_emitted && emitted),
+                "null request array");
+  std::vector<int32_t> r2, np2;
+  std::vector<int64_t> s2, t2;
+  r2.reserve(batch);
+  np2.reserve(batch);
+  s2.reserve(batch);
+  t2.reserve(batch);
+  for (int j = 0; j < batch; ++j) {
+    const int n = n_emitted[j];
+    NSG_CHECK_ARG(n >= 1 && n <= k + 1, "request %d emitted %d tokens, outside [1, k + 1]", j,
+                  n);
+    if (to_go[j] <= n) continue;  // done after this step
+    r2.push_back(rows[j]);
+    np2.push_back(num_pages[j]);
+    s2.push_back(start_pos[j] + n);
+    t2.push_back(emitted[(int64_t)j * (k + 1) + n - 1]);
+  }
+  const int32_t nb = (int32_t)r2.size();
+  const int32_t rc = fill_impl(page_table, page_table_stride, r2.data(), np2.data(), s2.data(),
+                               t2.data(), nb, padded_batch, k, page_size, dummy_page,
+                               num_qo_heads, num_kv_heads, head_dim, num_cus, max_kv_len, bufs,
+                               plans);
+  if (rc == NSG_OK) *next_batch = nb;
+  return rc;
+}
+
+namespace nsg {
+namespace {
+
+int32_t fill_impl(const int32_t* page_table, int64_t page_table_stride, const int32_t* rows,
+                  const int32_t* num_pages, const int64_t* start_pos, const int64_t* last_token,
+                  int32_t batch, int32_t padded_batch, int32_t k, int32_t page_size,
+                  int32_t dummy_page, int32_t num_qo_heads, int32_t num_kv_heads,
+                  int32_t head_dim, int32_t num_cus, int32_t max_kv_len,
+                  const nsg_spec_step_bufs_t* bufs, nsg_attn_plan_t* plans) {
   NSG_CHECK_ARG(bufs && plans, "null bufs or plans");
   NSG_CHECK_ARG(batch >= 0 && batch <= padded_batch, "batch %d outside [0, padded_batch %d]",
                 batch, padded_batch);
@@ -141,3 +201,6 @@ extern "C" int32_t nsg_spec_step_fill(const int32_t* page_table, int64_t page_ta
   clear_error();
   return NSG_OK;
 }
+
+}  // namespace
+}  // namespace nsg

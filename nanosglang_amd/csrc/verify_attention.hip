@@ -986,6 +986,7 @@ int32_t plan_impl(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
   }
   struct Group { int b, qb, qn, kv_end, lim0; };
   std::vector<Group> groups;
+  groups.reserve((size_t)batch * std::max(1, max_ql));
   long long total_it = 0;
   // query tiles of T tokens, each with its KV range (bottom-right causal)
   auto make_groups = [&](int T) -> int32_t {
@@ -1010,20 +1011,27 @@ int32_t plan_impl(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
     }
     return NSG_OK;
   };
-  int T = q_tile_tokens(G, max_ql, false);
-  if (int32_t rc = make_groups(T)) return rc;
   // KV groups: several per workgroup when even minimum-length items cannot
   // fill the GPU (the latency regime), one otherwise; a graph-captured plan
   // takes the latency regime exactly when it has a KV-length bound (see
-  // fixed_capacity).  A split is at least kMinSplitSteps steps per group: its
-  // partial rows cost about as much traffic as one step of K and V.
+  // fixed_capacity), known before the tiles are made.  A split is at least
+  // kMinSplitSteps steps per group: its partial rows cost about as much
+  // traffic as one step of K and V.
   const long long t1 = target_items(1, num_cus, num_kv_heads);
-  const bool latency = page_size >= kMinGroupPage &&
-                       (fixed_work >= 0 ? fixed_kv_len > 0
-                                        : (total_it + t1 - 1) / t1 <= kMinSplitSteps);
-  if (latency && q_tile_tokens(G, max_ql, true) != T) {
-    T = q_tile_tokens(G, max_ql, true);
+  bool latency;
+  int T;
+  if (fixed_work >= 0) {
+    latency = page_size >= kMinGroupPage && fixed_kv_len > 0;
+    T = q_tile_tokens(G, max_ql, latency);
     if (int32_t rc = make_groups(T)) return rc;
+  } else {
+    T = q_tile_tokens(G, max_ql, false);
+    if (int32_t rc = make_groups(T)) return rc;
+    latency = page_size >= kMinGroupPage && (total_it + t1 - 1) / t1 <= kMinSplitSteps;
+    if (latency && q_tile_tokens(G, max_ql, true) != T) {
+      T = q_tile_tokens(G, max_ql, true);
+      if (int32_t rc = make_groups(T)) return rc;
+    }
   }
   const int RT = (T * G + 15) / 16;
   const int KS = latency ? kv_groups_max(head_dim) : 1;
@@ -1066,6 +1074,7 @@ int32_t plan_impl(const int32_t* qo_indptr_h, const int32_t* kv_indptr_h,
   const int P = 8 / std::gcd(num_kv_heads, 8);
   if (latency && P > 1 && max_splits_planned(split_counts) == 1) {
     std::vector<std::pair<int, int>> reqs;  // (first group, groups) per request
+    reqs.reserve((size_t)batch);
     for (size_t gi = 0; gi < groups.size(); ++gi) {
       if (gi == 0 || groups[gi].b != groups[gi - 1].b) reqs.push_back({(int)gi, 0});
       ++reqs.back().second;

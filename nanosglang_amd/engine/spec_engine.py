@@ -45,6 +45,7 @@ draft tokens, ratio tests and resamples use Philox uniforms from
 from __future__ import annotations
 
 import time
+import weakref
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -65,6 +66,12 @@ class _Req:
     start: int = 0          # position of out[-1]; KV holds positions < start
     row: int = -1           # row of the engine's page-table mirror (graph mode)
     synced: int = 0         # pages of `table` mirrored into that row
+
+
+def _free_gate(flag: int) -> None:
+    lib = _native._lib
+    if lib is not None:
+        lib.nsg_host_gate_free(flag)
 
 
 def graph_batch_sizes(max_bs: int) -> list[int]:
@@ -190,7 +197,7 @@ class SpecEngine:
                  block_size: int = 16, temperature: float = 0.0, seed: int = 0,
                  workspace_bytes: int = 256 << 20, use_graphs: bool = True,
                  max_batch: int = 32, top_k: int = 0, top_p: float = 1.0,
-                 kv_split: bool = False):
+                 kv_split: bool = False, pipeline: bool = True):
         c = model.config
         self.model = model
         self.k = num_speculative
@@ -234,6 +241,12 @@ class SpecEngine:
         # so that a caller can check the acceptance on exactly the logits the
         # step produced; None (default) records nothing.
         self.trace: list | None = None
+        # pipeline: in graph mode, generate() queues step s + 1 (behind a host
+        # gate) while step s runs, so that the graph launch and input upload
+        # overlap the GPU's work (see _decode_pipelined)
+        self.pipeline = pipeline
+        self._gate_flag = None          # coherent pinned host word (nsg_host_gate_alloc)
+        self._gate_err = torch.zeros(1, dtype=torch.int32, device=self.device)
 
     # ---- helpers ----
     def _uniforms(self, stream: int, n: int) -> torch.Tensor:
@@ -403,6 +416,7 @@ class SpecEngine:
                                               A["start"], page_size=self.P,
                                               workspace=self._accept_ws,
                                               out=(g.n_out, g.emitted, g.rollback))
+            self._export(g)
             return
         tl = m.forward_packed(g.vids, A["vpos"], pool, g.attn[k], A["vslot"])
         g.tl = tl        # allocated from the graph's pool: every replay rewrites it
@@ -412,22 +426,58 @@ class SpecEngine:
                             g.kvp[k], g.idx[k], A["start"], page_size=self.P,
                             workspace=self._accept_ws, out=(g.n_out, g.emitted, g.rollback),
                             bonus_tokens=bonus)
+        self._export(g)
+
+    def _export(self, g: _StepGraph) -> None:
+        """The step's emitted counts and tokens into the graph's pinned host
+        buffers (g.n_h, g.em_h), by a kernel captured at the end of the step."""
+        kernels.check(kernels._lib().nsg_export_step(
+            g.n_out.data_ptr(), g.emitted.data_ptr(), g.bs, self.k + 1, g.n_h.data_ptr(),
+            g.em_h.data_ptr(), kernels._stream_ptr(self.device)), "nsg_export_step")
 
     def _fill_step(self, g: _StepGraph, active: list) -> None:
         """Host side of one step, one native call (``nsg_spec_step_fill``):
         tokens, positions, KV slots, the k + 1 page tables and attention plans,
         written into the graph's pinned staging buffer.  Request rows come
         from the engine's page-table mirror (``_sync_table``)."""
-        c = self.model.config
         B = len(active)
+        self._fill_arrays(g, np.fromiter((r.row for r in active), np.int32, B),
+                          np.fromiter((r.synced for r in active), np.int32, B),
+                          np.fromiter((r.start for r in active), np.int64, B),
+                          np.fromiter((r.out[-1] for r in active), np.int64, B))
+
+    def _fill_next_args(self, nxt: _StepGraph, g: _StepGraph, cur: list) -> tuple:
+        """Arguments of nsg_spec_step_fill_next: the inputs of step s + 1
+        (graph nxt) from the results of step s (graph g's pinned n_out /
+        emitted copies) for the requests `cur` of step s.  The arrays are
+        kept alive in the returned tuple."""
+        c, B = self.model.config, len(cur)
+        arrs = (np.fromiter((r.row for r in cur), np.int32, B),
+                np.fromiter((r.synced for r in cur), np.int32, B),
+                np.fromiter((r.start for r in cur), np.int64, B),
+                np.fromiter((r.max_new - len(r.out) for r in cur), np.int64, B))
+        nb = kernels.C.c_int32(0)
+        args = (self._tab.ctypes.data, self._tab.shape[1], *(a.ctypes.data for a in arrs),
+                g.n_h.data_ptr(), g.em_h.data_ptr(), B, nxt.bs, self.k, self.P,
+                self._dummy_block, c.num_attention_heads, c.num_key_value_heads, c.head_dim,
+                kernels.MI355X_CUS, self.max_kv_len, kernels.C.byref(nxt.bufs), nxt.plans,
+                kernels.C.byref(nb))
+        return args, arrs, nb
+
+    def _run_fill_next(self, fill_next: tuple) -> int:
+        args, _, nb = fill_next
+        kernels.check(kernels._lib().nsg_spec_step_fill_next(*args), "nsg_spec_step_fill_next")
+        return nb.value
+
+    def _fill_arrays(self, g: _StepGraph, rows, npg, starts, last) -> None:
+        """_fill_step on per-request arrays: page-table mirror rows (int32),
+        mirrored page counts (int32), start positions and last tokens (int64),
+        all C-contiguous."""
+        c = self.model.config
+        B = len(rows)
         if B:
-            tab = self._tab
-            rows = np.fromiter((r.row for r in active), np.int32, B)
-            npg = np.fromiter((r.synced for r in active), np.int32, B)
-            starts = np.fromiter((r.start for r in active), np.int64, B)
-            last = np.fromiter((r.out[-1] for r in active), np.int64, B)
-            ptrs = (tab.ctypes.data, tab.shape[1], rows.ctypes.data, npg.ctypes.data,
-                    starts.ctypes.data, last.ctypes.data)
+            ptrs = (self._tab.ctypes.data, self._tab.shape[1], rows.ctypes.data,
+                    npg.ctypes.data, starts.ctypes.data, last.ctypes.data)
         else:
             ptrs = (None, 0, None, None, None, None)
         kernels.check(kernels._lib().nsg_spec_step_fill(
@@ -445,26 +495,60 @@ class SpecEngine:
             self._tab[r.row, r.synced:n] = bt[r.synced:]
         r.synced = n
 
-    def _step_graph(self, active: list):
-        B = len(active)
-        bs = min(b for b in self._graphs if b >= B)
-        g = self._graphs[bs]
-        self._fill_step(g, active)
-        g.arena.upload()
+    # the host gate gives up after this long (a host that never raises the
+    # flag, e.g. after an exception, costs this much and sets the gate's error word)
+    GATE_TIMEOUT_US = 2_000_000
+
+    def _graph_for(self, n: int) -> _StepGraph:
+        return self._graphs[min(b for b in self._graphs if b >= n)]
+
+    def _gate(self) -> int:
+        """The host gate's flag word (allocated once per engine)."""
+        if self._gate_flag is None:
+            p = kernels.C.c_void_p()
+            kernels.check(kernels._lib().nsg_host_gate_alloc(kernels.C.byref(p)),
+                          "nsg_host_gate_alloc")
+            self._gate_flag = p.value
+            weakref.finalize(self, _free_gate, p.value)
+        return self._gate_flag
+
+    def _raise_gate(self) -> None:
+        kernels.C.c_int32.from_address(self._gate_flag).value = 1
+
+    def _launch(self, g: _StepGraph, gated: bool) -> torch.cuda.Event:
+        """Queues one speculative step of graph g on the current stream: the
+        host gate (gated: the step waits until _raise_gate), the upload of
+        its staging buffer, the Philox uniforms (sampling), the replay and
+        the export of its results to pinned memory (inside the graph).
+        Returns an event recorded after the replay."""
+        bs, k = g.bs, self.k
+        lib = kernels._lib()
+        sp = kernels._stream_ptr(self.device)
+        if gated:    # the gate also uploads the staging buffer once released
+            A = g.arena
+            kernels.check(lib.nsg_host_gate_wait(self._gate(), self._gate_err.data_ptr(),
+                                                 self.GATE_TIMEOUT_US, A.host.data_ptr(),
+                                                 A.dev.data_ptr(), A.nbytes, sp),
+                          "nsg_host_gate_wait")
+        else:
+            g.arena.upload()
         if not self.greedy:
-            k = self.k
             o0, o1 = self._rng_offset
-            lib = kernels._lib()
-            sp = kernels._stream_ptr(self.device)
             kernels.check(lib.nsg_philox_uniform(self.seed, 0, o0, bs * (k + 1), g.u.data_ptr(),
                                                  sp), "nsg_philox_uniform")
             kernels.check(lib.nsg_philox_uniform(self.seed, 1, o1, bs * k, g.ud.data_ptr(), sp),
                           "nsg_philox_uniform")
             self._rng_offset = [o0 + bs * (k + 1), o1 + bs * k]
-        g.graph.replay()
-        g.n_h.copy_(g.n_out, non_blocking=True)
-        g.em_h.copy_(g.emitted, non_blocking=True)
-        torch.cuda.current_stream(self.device).synchronize()
+        g.graph.replay()       # ends with the export of its results to g.n_h / g.em_h
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        return ev
+
+    def _step_graph(self, active: list, rows: int = 0):
+        B = len(active)
+        g = self._graph_for(max(B, rows))
+        self._fill_step(g, active)
+        self._launch(g, gated=False).synchronize()
         if self.trace is not None:
             k, (si, sx, _) = self.k, g.strides
             kvp = g.arena.h["kvp"][k * si:k * si + B + 1].copy()
@@ -600,19 +684,20 @@ class SpecEngine:
             r.out.append(f)
             r.start = len(r.prompt)
 
-    def _step(self, active: list):
+    def _step(self, active: list, rows: int = 0):
         """One speculative step for the active requests: reserve the verify
         window's pages (scheduler.py:221-232 applied to k + 1 positions),
         draft, verify and accept (graph or eager), append the emitted tokens,
         advance the positions and roll back pages past them.  Returns the
-        per-request emitted counts."""
+        per-request emitted counts.  Graph mode runs the graph for at least
+        ``rows`` rows (generate passes the previous step's batch)."""
         k = self.k
         for r in active:
             self.kv.reserve(r.table, r.start + k + 1)
             if self.use_graphs:
                 self._sync_table(r)
         if self.use_graphs:
-            n_h, em_h = self._step_graph(active)
+            n_h, em_h = self._step_graph(active, rows)
         else:
             n_h, em_h = self._step_eager(active)
         for j, r in enumerate(active):
@@ -622,6 +707,86 @@ class SpecEngine:
             self.kv.truncate(r.table, r.start)        # rollback of rejected pages
             r.synced = min(r.synced, len(r.table.block_indices))
         return n_h
+
+    def _decode_pipelined(self, active: list, count) -> None:
+        """The speculative steps of generate() in graph mode, pipelined: while
+        step s runs on the GPU, step s + 1 is already queued behind the host
+        gate (nsg_host_gate_wait), with pages reserved for its verify window
+        whatever step s accepts.  Once step s's results are read, the host
+        appends them, writes step s + 1's inputs (requests that finished at s
+        become padding rows) and raises the gate; page rollback and frees
+        follow while step s + 1 runs.  In both loops step s + 1 runs the
+        graph sized for step s's batch (requests that finish at s are padding
+        rows for one step), so its graph does not depend on step s's outcome;
+        step s + 1 is queued early when some request surely outlives step s
+        (more than k + 1 tokens to go).  Every step therefore runs the graph,
+        inputs and Philox offsets of the unpipelined loop, and the tokens are
+        identical.  ``count(B, n)`` receives each step's batch size and
+        emitted counts."""
+        k = self.k
+        for r in active:
+            self.kv.reserve(r.table, r.start + k + 1)
+            self._sync_table(r)
+        g = self._graph_for(len(active))
+        self._fill_step(g, active)
+        ev = self._launch(g, gated=False)
+        cur = active
+        cap = self._max_pages() * self.P     # positions the page-table mirror holds
+        pending = False                  # a gated step is queued and not yet released
+        try:
+            while cur:
+                nxt = None
+                if (any(r.max_new - len(r.out) > k + 1 for r in cur) and
+                        all(r.start + 2 * (k + 1) <= cap for r in cur)):
+                    for r in cur:        # step s + 1's window, whatever step s accepts
+                        self.kv.reserve(r.table, r.start + 2 * (k + 1))
+                        self._sync_table(r)
+                    nxt = self._graph_for(len(cur))
+                    pending = True
+                    ev_next = self._launch(nxt, gated=True)
+                    # step s + 1's fill, but for step s's results (n_out,
+                    # emitted), prepared while step s runs
+                    fill_next = self._fill_next_args(nxt, g, cur)
+                ev.synchronize()
+                if nxt is not None:    # release step s + 1 first, bookkeeping after
+                    self._run_fill_next(fill_next)
+                    self._raise_gate()
+                    pending = False
+                B = len(cur)
+                n_h = g.n_h.numpy()[:B].copy()
+                em_h = g.em_h.numpy()[:B].copy()
+                count(B, n_h)
+                still = []
+                for j, r in enumerate(cur):
+                    n = int(n_h[j])
+                    r.out.extend(em_h[j, :n].tolist())
+                    r.start += n
+                    if len(r.out) < r.max_new:
+                        still.append(r)
+                # rollback and frees, off the GPU's path: keep step s + 1's
+                # window when it is already queued
+                keep = k + 1 if nxt is not None else 0
+                for r in cur:
+                    if len(r.out) >= r.max_new:
+                        del r.out[r.max_new:]
+                        self.kv.free_request(r.table)
+                    else:
+                        self.kv.truncate(r.table, r.start + keep)
+                        r.synced = min(r.synced, len(r.table.block_indices))
+                if nxt is not None:
+                    g, ev = nxt, ev_next
+                elif still:
+                    for r in still:
+                        self.kv.reserve(r.table, r.start + k + 1)
+                        self._sync_table(r)
+                    g = self._graph_for(len(cur))
+                    self._fill_step(g, still)
+                    ev = self._launch(g, gated=False)
+                cur = still
+        finally:
+            if pending:                  # an exception left a queued step held: release it
+                self._raise_gate()
+                torch.cuda.current_stream(self.device).synchronize()
 
     # device error bits of the attention and acceptance kernels (their
     # workspaces' flag words), by kernel
@@ -641,6 +806,9 @@ class SpecEngine:
         found += [msg for bit, msg in self._ATTN_FLAGS.items() if a & bit]
         c = self._accept_ws.check_flags()
         found += [msg for bit, msg in self._ACCEPT_FLAGS.items() if c & bit]
+        if int(self._gate_err.item()):
+            self._gate_err.zero_()
+            found.append("the host gate timed out (a pipelined step ran on stale inputs)")
         if a & ~1 or c & ~14:
             found.append(f"unknown flag bits (attention {a:#x}, acceptance {c:#x})")
         if found:
@@ -716,19 +884,28 @@ class SpecEngine:
         self._admit(reqs, synthetic_context)
         lens = [len(r.prompt) for r in reqs]
         t_prefill = time.perf_counter() - t0
-        steps = proposed = accepted = req_steps = 0
         active = [r for r in reqs if len(r.out) < r.max_new]
         for r in reqs:
             if r not in active:
                 self.kv.free_request(r.table)
         # 3. speculative steps
+        tally = [0, 0, 0, 0]                # steps, request-steps, proposed, accepted
+
+        def count(B, n_h):
+            tally[0] += 1
+            tally[1] += B
+            tally[2] += B * k
+            tally[3] += int(n_h.sum()) - B
+
+        if active and self.use_graphs and self.pipeline and self.trace is None:
+            self._decode_pipelined(active, count)
+            active = []
+        prev = 0
         while active:
             B = len(active)
-            n_h = self._step(active)
-            steps += 1
-            req_steps += B
-            proposed += B * k
-            accepted += int(n_h.sum()) - B
+            n_h = self._step(active, prev)
+            prev = B
+            count(B, n_h)
             still = []
             for r in active:
                 if len(r.out) >= r.max_new:
@@ -737,6 +914,7 @@ class SpecEngine:
                 else:
                     still.append(r)
             active = still
+        steps, req_steps, proposed, accepted = tally
         self.check_device_flags()           # synchronises the stream
         t_total = time.perf_counter() - t0
         n_tok = sum(len(r.out) for r in reqs)

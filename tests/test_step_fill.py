@@ -172,3 +172,44 @@ def test_step_fill_mirrors_into_a_persistent_page_table():
     e._sync_table(r)
     assert list(e._tab[1, :2]) == [5, 7] and r.synced == 2
     assert (e._tab[0] == -1).all()
+
+
+@pytest.mark.parametrize("B,bs,k,P", [(6, 8, 4, 16), (32, 32, 4, 16), (5, 8, 2, 4)])
+def test_step_fill_next_equals_fill_on_the_continuing_requests(lib, B, bs, k, P):
+    """nsg_spec_step_fill_next (the pipelined engine's fill from the previous
+    step's results) writes exactly what nsg_spec_step_fill writes for the
+    requests that continue: to_go > emitted count, at start + n with their
+    last emitted token, in order; the others drop out."""
+    tab, rows, npg, starts, _, _, dummy = _case(11 + B, B, bs, 2 * k + 1, P)   # pages for two windows
+    rng = np.random.default_rng(B)
+    n = rng.integers(1, k + 2, B).astype(np.int32)
+    emitted = rng.integers(0, 150000, (B, k + 1)).astype(np.int64)
+    to_go = rng.integers(1, 3 * (k + 1), B).astype(np.int64)
+    to_go[0], to_go[-1] = n[0], n[-1] + 1            # one request ends, one just continues
+    live = to_go > n
+    max_kv_len = 1022 * P
+    ref = _Staging(lib, bs, k, max_kv_len, 4096)
+    assert _fill(lib, ref, tab, rows[live], npg[live], starts[live] + n[live],
+                 emitted[live, n[live] - 1], bs, k, P, dummy, max_kv_len) == 0
+    got = _Staging(lib, bs, k, max_kv_len, 4096)
+    nb = C.c_int32(-1)
+    arrs = [np.ascontiguousarray(a) for a in (rows, npg, starts, to_go, n, emitted)]
+    rc = lib.nsg_spec_step_fill_next(tab.ctypes.data, tab.shape[1],
+                                     *[a.ctypes.data for a in arrs], B, bs, k, P, dummy, Hq,
+                                     Hkv, D, CUS, max_kv_len, C.byref(got.bufs), got.plans,
+                                     C.byref(nb))
+    assert rc == 0
+    assert nb.value == int(live.sum())
+    for name in ("tok0", "start", "pos", "slot", "vpos", "vslot", "qo", "kvp", "last", "idx",
+                 "work"):
+        np.testing.assert_array_equal(getattr(got, name), getattr(ref, name), err_msg=name)
+    for a in range(k + 1):
+        assert bytes(got.plans[a]) == bytes(ref.plans[a])
+    # an emitted count outside [1, k + 1] is refused
+    bad = n.copy()
+    bad[1] = k + 2
+    arrs[4] = bad
+    assert lib.nsg_spec_step_fill_next(tab.ctypes.data, tab.shape[1],
+                                       *[a.ctypes.data for a in arrs], B, bs, k, P, dummy, Hq,
+                                       Hkv, D, CUS, max_kv_len, C.byref(got.bufs), got.plans,
+                                       C.byref(nb)) == 1

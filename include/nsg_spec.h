@@ -561,9 +561,13 @@ int32_t nsg_philox_uniform(uint64_t seed, uint32_t stream_id, uint64_t offset, i
 /* nsg_export_step: n_host[i] = n_emitted[i] (i < rows) and emitted_host[i] =
  * emitted[i] (i < rows * cols), by one kernel (graph-capturable) writing
  * straight into pinned host memory: a step's emitted counts and tokens for
- * the host, without copy commands after the step. */
+ * the host, without copy commands after the step.  Then, when done_host is
+ * not NULL (a word from nsg_host_gate_alloc), *done_host = 1 once those
+ * stores are visible to the host: the host may poll it instead of waiting
+ * on an event, and clears it before the next use. */
 int32_t nsg_export_step(const int32_t* n_emitted, const int64_t* emitted, int32_t rows,
-                        int32_t cols, int32_t* n_host, int64_t* emitted_host, nsg_stream_t stream);
+                        int32_t cols, int32_t* n_host, int64_t* emitted_host, int32_t* done_host,
+                        nsg_stream_t stream);
 int32_t nsg_host_gate_alloc(int32_t** flag);
 int32_t nsg_host_gate_free(int32_t* flag);
 int32_t nsg_host_gate_wait(int32_t* flag, int32_t* err, int64_t timeout_us,

@@ -88,7 +88,7 @@ SIGNATURES = {
     "nsg_embed_rows": (i32, [vp, i64, i64, i32, i32, vp, i64, i32, i32, vp, i64, vp, vp]),
     "nsg_silu_mul": (i32, [vp, vp, i64, i32, vp]),
     "nsg_philox_uniform": (i32, [u64, u32, u64, i64, vp, vp]),
-    "nsg_export_step": (i32, [vp, vp, i32, i32, vp, vp, vp]),
+    "nsg_export_step": (i32, [vp, vp, i32, i32, vp, vp, vp, vp]),
     "nsg_host_gate_alloc": (i32, [C.POINTER(C.c_void_p)]),
     "nsg_host_gate_free": (i32, [vp]),
     "nsg_host_gate_wait": (i32, [vp, vp, i64, vp, vp, i64, vp]),

@@ -62,12 +62,18 @@ __global__ __launch_bounds__(kGateThreads) void host_gate_kernel(int32_t* flag, 
 }
 
 // The step's results to pinned host memory, by a kernel at the end of the
-// step's graph (two copy commands after it cost about 4 us each).
+// step's graph (two copy commands after it cost about 4 us each), then the
+// done word: the host polls it instead of waiting on an event.
 __global__ __launch_bounds__(256) void export_kernel(const int32_t* n, const int64_t* em,
                                                      int32_t rows, int32_t cols, int32_t* n_host,
-                                                     int64_t* em_host) {
+                                                     int64_t* em_host, int32_t* done) {
   for (int i = threadIdx.x; i < rows; i += 256) n_host[i] = n[i];
   for (int i = threadIdx.x; i < rows * cols; i += 256) em_host[i] = em[i];
+  if (done) {
+    __threadfence_system();  // this thread's result stores before the done word
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(done, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
 }
 
 }  // namespace
@@ -77,17 +83,14 @@ using namespace nsg;
 
 extern "C" int32_t nsg_export_step(const int32_t* n_emitted, const int64_t* emitted,
                                    int32_t rows, int32_t cols, int32_t* n_host,
-                                   int64_t* emitted_host, nsg_stream_t stream) {
+                                   int64_t* emitted_host, int32_t* done_host,
+                                   nsg_stream_t stream) {
   NSG_CHECK_ARG(rows >= 0 && cols >= 0 && (int64_t)rows * cols <= (1 << 24),
                 "rows %d, cols %d", rows, cols);
   NSG_CHECK_ARG(rows == 0 || (n_emitted && emitted && n_host && emitted_host),
                 "null pointer");
-  if (rows == 0) {
-    clear_error();
-    return NSG_OK;
-  }
   hipLaunchKernelGGL(export_kernel, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     n_emitted, emitted, rows, cols, n_host, emitted_host);
+                     n_emitted, emitted, rows, cols, n_host, emitted_host, done_host);
   return launch_status("export_kernel");
 }
 

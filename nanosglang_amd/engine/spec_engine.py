@@ -189,6 +189,13 @@ class _StepGraph:
             self.u = self.ud = self.dlog = None
         self.n_h = torch.zeros(bs, dtype=torch.int32, pin_memory=True)
         self.em_h = torch.zeros(bs, k + 1, dtype=torch.int64, pin_memory=True)
+        # coherent pinned word the step's export kernel sets once n_h / em_h
+        # hold the step's results (the host polls it, then clears it)
+        p = kernels.C.c_void_p()
+        kernels.check(lib.nsg_host_gate_alloc(kernels.C.byref(p)), "nsg_host_gate_alloc")
+        self.done_ptr = p.value
+        self.done = kernels.C.c_int32.from_address(p.value)
+        weakref.finalize(self, _free_gate, p.value)
         self.graph = None
 
 
@@ -433,7 +440,7 @@ class SpecEngine:
         buffers (g.n_h, g.em_h), by a kernel captured at the end of the step."""
         kernels.check(kernels._lib().nsg_export_step(
             g.n_out.data_ptr(), g.emitted.data_ptr(), g.bs, self.k + 1, g.n_h.data_ptr(),
-            g.em_h.data_ptr(), kernels._stream_ptr(self.device)), "nsg_export_step")
+            g.em_h.data_ptr(), g.done_ptr, kernels._stream_ptr(self.device)), "nsg_export_step")
 
     def _fill_step(self, g: _StepGraph, active: list) -> None:
         """Host side of one step, one native call (``nsg_spec_step_fill``):
@@ -515,15 +522,34 @@ class SpecEngine:
     def _raise_gate(self) -> None:
         kernels.C.c_int32.from_address(self._gate_flag).value = 1
 
-    def _launch(self, g: _StepGraph, gated: bool) -> torch.cuda.Event:
+    # a step that has not finished after this long is reported as hung
+    STEP_TIMEOUT_S = 60.0
+
+    def _wait_done(self, g: _StepGraph) -> None:
+        """Waits (polling the pinned done word the step's export kernel sets)
+        until the step queued on graph g has finished; its results are then
+        in g.n_h / g.em_h."""
+        done = g.done
+        if done.value:
+            return
+        t0 = time.perf_counter()
+        while not done.value:
+            if time.perf_counter() - t0 > self.STEP_TIMEOUT_S:
+                raise RuntimeError(f"speculative step (graph of {g.bs} rows) did not finish "
+                                   f"within {self.STEP_TIMEOUT_S} s")
+
+    def _launch(self, g: _StepGraph, gated: bool) -> None:
         """Queues one speculative step of graph g on the current stream: the
         host gate (gated: the step waits until _raise_gate), the upload of
-        its staging buffer, the Philox uniforms (sampling), the replay and
-        the export of its results to pinned memory (inside the graph).
-        Returns an event recorded after the replay."""
+        its staging buffer, the Philox uniforms (sampling), the replay, whose
+        last kernel exports the results to pinned memory and sets g's done
+        word (cleared here for an ungated step; the gated step's owner clears
+        it before raising the gate)."""
         bs, k = g.bs, self.k
         lib = kernels._lib()
         sp = kernels._stream_ptr(self.device)
+        if not gated:
+            g.done.value = 0
         if gated:    # the gate also uploads the staging buffer once released
             A = g.arena
             kernels.check(lib.nsg_host_gate_wait(self._gate(), self._gate_err.data_ptr(),
@@ -540,15 +566,13 @@ class SpecEngine:
                           "nsg_philox_uniform")
             self._rng_offset = [o0 + bs * (k + 1), o1 + bs * k]
         g.graph.replay()       # ends with the export of its results to g.n_h / g.em_h
-        ev = torch.cuda.Event()
-        ev.record(torch.cuda.current_stream(self.device))
-        return ev
 
     def _step_graph(self, active: list, rows: int = 0):
         B = len(active)
         g = self._graph_for(max(B, rows))
         self._fill_step(g, active)
-        self._launch(g, gated=False).synchronize()
+        self._launch(g, gated=False)
+        self._wait_done(g)
         if self.trace is not None:
             k, (si, sx, _) = self.k, g.strides
             kvp = g.arena.h["kvp"][k * si:k * si + B + 1].copy()
@@ -729,7 +753,7 @@ class SpecEngine:
             self._sync_table(r)
         g = self._graph_for(len(active))
         self._fill_step(g, active)
-        ev = self._launch(g, gated=False)
+        self._launch(g, gated=False)
         cur = active
         cap = self._max_pages() * self.P     # positions the page-table mirror holds
         pending = False                  # a gated step is queued and not yet released
@@ -743,13 +767,14 @@ class SpecEngine:
                         self._sync_table(r)
                     nxt = self._graph_for(len(cur))
                     pending = True
-                    ev_next = self._launch(nxt, gated=True)
+                    self._launch(nxt, gated=True)
                     # step s + 1's fill, but for step s's results (n_out,
                     # emitted), prepared while step s runs
                     fill_next = self._fill_next_args(nxt, g, cur)
-                ev.synchronize()
+                self._wait_done(g)
                 if nxt is not None:    # release step s + 1 first, bookkeeping after
                     self._run_fill_next(fill_next)
+                    nxt.done.value = 0
                     self._raise_gate()
                     pending = False
                 B = len(cur)
@@ -774,14 +799,14 @@ class SpecEngine:
                         self.kv.truncate(r.table, r.start + keep)
                         r.synced = min(r.synced, len(r.table.block_indices))
                 if nxt is not None:
-                    g, ev = nxt, ev_next
+                    g = nxt
                 elif still:
                     for r in still:
                         self.kv.reserve(r.table, r.start + k + 1)
                         self._sync_table(r)
                     g = self._graph_for(len(cur))
                     self._fill_step(g, still)
-                    ev = self._launch(g, gated=False)
+                    self._launch(g, gated=False)
                 cur = still
         finally:
             if pending:                  # an exception left a queued step held: release it

@@ -43,7 +43,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 18
+#define NSG_ABI_VERSION 19
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -518,6 +518,33 @@ int32_t nsg_linear_argmax(const void* x, int64_t ldx, const void* w, int64_t ldw
                           const void* bias, int32_t M, int32_t N, int32_t K, void* workspace,
                           int64_t workspace_bytes, int64_t* tokens, int64_t token_stride,
                           nsg_stream_t stream);
+
+/* The lm_head after the final RMSNorm (causal_lm.py:643-645, logits =
+ * lm_head(norm(h))) with that norm folded in, as nsg_linear_fold folds a
+ * layer's norms: W' = bf16(w_norm[k] * W[n, k]) (w_norm folded into W's
+ * columns), x the un-normalised rows (the last layer's residual stream), and
+ * row m of x W'^T scaled by rsqrt(S_m / norm_dim + eps) before its single
+ * bf16 rounding, S_m the sum of sumsq_in[c * M + m] over c < sumsq_parts in
+ * order c = 0, 1, ... (the partials the last layer's down_proj epilogue
+ * writes).  One launch fewer than nsg_rmsnorm + the lm_head; rounding differs
+ * from the reference's norm as nsg_linear_fold's does.  1 <= M <= 160,
+ * N % 4 == 0, K % 64 == 0, K >= 192, bf16 weights, x / w rows and sumsq_in
+ * 16-byte aligned; nsg_lm_head_fold_supported(M, N, K, sumsq_parts) tells
+ * whether a shape fits (M * sumsq_parts a multiple of 4, the partials within
+ * one LDS ring slot: sumsq_parts <= 56 at 160 rows), else the calls return
+ * NSG_ERR_UNSUPPORTED.
+ * nsg_lm_head_fold: the logits, y (M x N, ldy elements apart, 8-byte aligned
+ * rows); nsg_lm_head_fold_argmax: the greedy token of each row, as
+ * nsg_linear_argmax (same workspace size and key rule), of those logits. */
+int32_t nsg_lm_head_fold_supported(int32_t M, int32_t N, int32_t K, int32_t sumsq_parts);
+int32_t nsg_lm_head_fold(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y,
+                         int64_t ldy, int32_t M, int32_t N, int32_t K, const float* sumsq_in,
+                         int32_t sumsq_parts, int32_t norm_dim, float eps, nsg_stream_t stream);
+int32_t nsg_lm_head_fold_argmax(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                int32_t M, int32_t N, int32_t K, const float* sumsq_in,
+                                int32_t sumsq_parts, int32_t norm_dim, float eps,
+                                void* workspace, int64_t workspace_bytes, int64_t* tokens,
+                                int64_t token_stride, nsg_stream_t stream);
 
 /* Embedding rows: out[r] = table[ids[b * id_stride_b + j * id_stride_j]] for
  * r = b * per_batch + j (embed_tokens(input_ids), causal_lm.py:613, on an index view

@@ -13,7 +13,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libnsg_spec.so")
 
 NSG_ATTN_WORK_INTS = 8
-ABI_VERSION = 18
+ABI_VERSION = 19
 
 i32, i64, u32, u64, f32 = C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_float
 vp = C.c_void_p
@@ -85,6 +85,10 @@ SIGNATURES = {
     "nsg_row_sumsq": (i32, [vp, i64, i32, i32, vp, vp]),
     "nsg_linear_argmax_workspace_bytes": (i64, [i32, i32]),
     "nsg_linear_argmax": (i32, [vp, i64, vp, i64, vp, i32, i32, i32, vp, i64, vp, i64, vp]),
+    "nsg_lm_head_fold_supported": (i32, [i32, i32, i32, i32]),
+    "nsg_lm_head_fold": (i32, [vp, i64, vp, i64, vp, i64, i32, i32, i32, vp, i32, i32, f32, vp]),
+    "nsg_lm_head_fold_argmax": (i32, [vp, i64, vp, i64, i32, i32, i32, vp, i32, i32, f32, vp,
+                                      i64, vp, i64, vp]),
     "nsg_embed_rows": (i32, [vp, i64, i64, i32, i32, vp, i64, i32, i32, vp, i64, vp, vp]),
     "nsg_silu_mul": (i32, [vp, vp, i64, i32, vp]),
     "nsg_philox_uniform": (i32, [u64, u32, u64, i64, vp, vp]),

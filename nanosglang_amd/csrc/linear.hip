@@ -1089,6 +1089,81 @@ extern "C" int32_t nsg_linear_argmax(const void* x, int64_t ldx, const void* w, 
   return launch_status("argmax_keys_kernel");
 }
 
+// ---- lm_head with the final RMSNorm folded in (bf16 weights) ----
+namespace {
+
+int32_t head_fold_params(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t M,
+                         int32_t N, int32_t K, const float* sumsq_in, int32_t sumsq_parts,
+                         int32_t norm_dim, float eps, HeadParams* hp) {
+  NSG_CHECK_ARG(x && w && sumsq_in, "null x, weight or sums of squares");
+  NSG_CHECK_ARG(M >= 1 && M <= kHeadMaxRows, "M %d outside [1, %d]", M, kHeadMaxRows);
+  NSG_CHECK_ARG(N >= 4 && N % 4 == 0, "N %d must be a positive multiple of 4", N);
+  NSG_CHECK_ARG(K >= 3 * kHeadStep && K % kHeadStep == 0, "K %d must be a multiple of %d, >= %d",
+                K, kHeadStep, 3 * kHeadStep);
+  NSG_CHECK_ARG(ldx >= K && ldw >= K && ldx % 8 == 0 && ldw % 8 == 0 && (uintptr_t)x % 16 == 0 &&
+                    (uintptr_t)w % 16 == 0 && (uintptr_t)sumsq_in % 16 == 0,
+                "x and w rows and sumsq_in must be 16-byte aligned");
+  NSG_CHECK_ARG(sumsq_parts >= 1 && norm_dim > 0 && eps >= 0.f,
+                "folded norm: %d partials, dim %d, eps %g", sumsq_parts, norm_dim, (double)eps);
+  if (!lm_head_fold_fits(M, sumsq_parts)) {
+    set_error("the folded norm does not fit at M %d with %d partials per row", M, sumsq_parts);
+    return NSG_ERR_UNSUPPORTED;
+  }
+  *hp = HeadParams{static_cast<const bf16*>(x), static_cast<const bf16*>(w), nullptr, ldx, ldw,
+                   0, M, N, K, sumsq_in, sumsq_parts, norm_dim, eps};
+  return NSG_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t nsg_lm_head_fold_supported(int32_t M, int32_t N, int32_t K,
+                                              int32_t sumsq_parts) {
+  return M >= 1 && M <= kHeadMaxRows && N >= 4 && N % 4 == 0 && K >= 3 * kHeadStep &&
+                 K % kHeadStep == 0 && lm_head_fold_fits(M, sumsq_parts)
+             ? 1
+             : 0;
+}
+
+extern "C" int32_t nsg_lm_head_fold(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                    void* y, int64_t ldy, int32_t M, int32_t N, int32_t K,
+                                    const float* sumsq_in, int32_t sumsq_parts, int32_t norm_dim,
+                                    float eps, nsg_stream_t stream) {
+  HeadParams hp{};
+  if (int32_t rc = head_fold_params(x, ldx, w, ldw, M, N, K, sumsq_in, sumsq_parts, norm_dim,
+                                    eps, &hp))
+    return rc;
+  NSG_CHECK_ARG(y && ldy >= N && ldy % 4 == 0 && (uintptr_t)y % 8 == 0,
+                "y rows must be 8-byte aligned, ldy %lld >= N %d", (long long)ldy, N);
+  hp.out = y;
+  hp.ldy = ldy;
+  int key_cols = 0;
+  return launch_lm_head(hp, false, static_cast<hipStream_t>(stream), &key_cols);
+}
+
+extern "C" int32_t nsg_lm_head_fold_argmax(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                           int32_t M, int32_t N, int32_t K,
+                                           const float* sumsq_in, int32_t sumsq_parts,
+                                           int32_t norm_dim, float eps, void* workspace,
+                                           int64_t workspace_bytes, int64_t* tokens,
+                                           int64_t token_stride, nsg_stream_t stream) {
+  HeadParams hp{};
+  if (int32_t rc = head_fold_params(x, ldx, w, ldw, M, N, K, sumsq_in, sumsq_parts, norm_dim,
+                                    eps, &hp))
+    return rc;
+  NSG_CHECK_ARG(workspace && tokens && token_stride >= 1 && (uintptr_t)workspace % 8 == 0,
+                "null workspace or tokens, token stride < 1, or workspace not 8-byte aligned");
+  NSG_CHECK_ARG(workspace_bytes >= nsg_linear_argmax_workspace_bytes(M, N),
+                "workspace %lld bytes < %lld", (long long)workspace_bytes,
+                (long long)nsg_linear_argmax_workspace_bytes(M, N));
+  hp.out = workspace;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int key_cols = 0;
+  if (int32_t rc = launch_lm_head(hp, true, s, &key_cols)) return rc;
+  hipLaunchKernelGGL(argmax_keys_kernel, dim3(M), dim3(256), 0, s,
+                     static_cast<const uint64_t*>(workspace), key_cols, tokens, token_stride);
+  return launch_status("argmax_keys_kernel");
+}
+
 // ---- FP8 weights for a library GEMM (many rows, prefill) ----
 // The dequantisation of FP8Linear.forward (w8.to(bf16) * scale,
 // quantization.py:49-52) in one pass: 16 weight bytes per thread in, 32

@@ -29,6 +29,14 @@
 // The ring's 16-byte segments are XOR-swizzled per row pair (segment s of row
 // r sits at s ^ ((r >> 1) & 7)): the 16 rows of an MFMA fragment read then
 // fall on distinct banks of the 256-byte bank row.
+//
+// Folded final RMSNorm (FOLD): the rows' partial sums of squares reach the
+// ring's last slot by LDS DMA before the ring's first steps are issued (that
+// slot is first filled by the main loop, after its first barrier); once they
+// have landed, thread t adds row t's partials in order and leaves the row
+// scale in the slot's last KB, from which every lane takes the scales of its
+// rows into registers.  The copies are older than the ring's, so waiting for
+// them leaves the ring's first steps in flight.
 #include "lm_head.hpp"
 
 #include <algorithm>
@@ -77,7 +85,7 @@ __device__ __forceinline__ void dma16_nt(uint32_t lds, const void* src) {
 
 __device__ __forceinline__ uint64_t key_max(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
-template <int MT, bool ARG>
+template <int MT, bool ARG, bool FOLD>
 __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
   static_assert(MT % 2 == 0 && MT >= 2 && MT <= kHeadMaxRows / 16, "whole x copies");
   // x: MT * 16 rows x 8 segments = 2 MT copies per step, kX per wave (the
@@ -175,8 +183,39 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
     bc[mt] = -1;
   }
 
+  if constexpr (FOLD) {  // the partial sums into the last slot, 1 KB per copy
+    const int n16 = p.M * p.parts / 4;
+    const int n_copies = (n16 + 63) / 64;
+    const uint32_t part_lds = ring_lds + (kStages - 1) * SB;
+    for (int i = wave; i < n_copies; i += kWaves)
+      dma16(part_lds + i * 1024, p.sumsq + (int64_t)min(i * 64 + lane, n16 - 1) * 4);
+  }
   set_w(0);
   for (int g = 0; g < kStages - 1 && g < total; ++g) issue();
+
+  float rs[FOLD ? MT : 1];  // the row scales of this lane's rows 16 mt + lane % 16
+  if constexpr (FOLD) {
+    wait_steps<NI, kStages - 1>(issued);  // this wave's partial copies have landed
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // ... and every wave's
+    asm volatile("" ::: "memory");
+    const float* part = reinterpret_cast<const float*>(ring + (kStages - 1) * SB);
+    float* scale = reinterpret_cast<float*>(ring + kStages * SB - 1024);
+    const int t = threadIdx.x;
+    if (t < MT * 16) {
+      float sq = 0.f;
+      if (t < p.M)
+        for (int c = 0; c < p.parts; ++c) sq += part[c * p.M + t];
+      scale[t] = t < p.M ? 1.f / sqrtf(sq / (float)p.norm_dim + p.eps) : 0.f;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) rs[mt] = scale[mt * 16 + r16];
+    // read before the main loop's first copies refill the slot
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
 
   int g = 0, c_slot = 0;
   for (int j = 0; j < my_tiles; ++j) {
@@ -226,7 +265,7 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
           const bool ok = n < p.N;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float r = bf16_bits_to_float(float_to_bf16_bits(v[i]));
+            const float r = bf16_bits_to_float(float_to_bf16_bits(FOLD ? v[i] * rs[mt] : v[i]));
             const bool take = ok && (r > bv[mt] || bc[mt] < 0);
             bv[mt] = take ? r : bv[mt];
             bc[mt] = take ? n + i : bc[mt];
@@ -234,7 +273,14 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
         } else {
           if (m < p.M && n < p.N) {
             bf16* y = static_cast<bf16*>(p.out) + (int64_t)m * p.ldy + n;
-            *reinterpret_cast<uint2*>(y) = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            if constexpr (FOLD) {
+              const float sc = rs[mt];
+              *reinterpret_cast<uint2*>(y) = uint2{pack_bf16x2(v[0] * sc, v[1] * sc),
+                                                   pack_bf16x2(v[2] * sc, v[3] * sc)};
+            } else {
+              *reinterpret_cast<uint2*>(y) =
+                  uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            }
           }
         }
         acc[nt][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -286,14 +332,39 @@ int32_t launch_mt(const HeadParams& p, bool argmax, hipStream_t s, int* key_cols
   const int per_cu = kLdsMax / (ring_stages<MT>() * stage_bytes<MT>());
   const int grid = std::min(tiles, device_cus() * std::max(per_cu, 1));
   *key_cols = kWaves * grid;
-  if (argmax)
-    hipLaunchKernelGGL((lm_head_kernel<MT, true>), dim3(grid), dim3(kWaves * 64), 0, s, p);
-  else
-    hipLaunchKernelGGL((lm_head_kernel<MT, false>), dim3(grid), dim3(kWaves * 64), 0, s, p);
+  const dim3 g(grid), b(kWaves * 64);
+  if (p.sumsq) {
+    if (argmax)
+      hipLaunchKernelGGL((lm_head_kernel<MT, true, true>), g, b, 0, s, p);
+    else
+      hipLaunchKernelGGL((lm_head_kernel<MT, false, true>), g, b, 0, s, p);
+  } else {
+    if (argmax)
+      hipLaunchKernelGGL((lm_head_kernel<MT, true, false>), g, b, 0, s, p);
+    else
+      hipLaunchKernelGGL((lm_head_kernel<MT, false, false>), g, b, 0, s, p);
+  }
   return launch_status("lm_head_kernel");
 }
 
+template <int MT>
+bool fold_fits_mt(int M, int parts) {
+  const int64_t n16 = (int64_t)M * parts / 4;
+  return ((n16 + 63) / 64) * 1024 <= stage_bytes<MT>() - 1024;
+}
+
 }  // namespace
+
+bool lm_head_fold_fits(int M, int parts) {
+  if (M < kHeadMinRows || M > kHeadMaxRows || parts < 1 || ((int64_t)M * parts) % 4 != 0)
+    return false;
+  const int mt = (M + 15) / 16;
+  if (mt <= 2) return fold_fits_mt<2>(M, parts);
+  if (mt <= 4) return fold_fits_mt<4>(M, parts);
+  if (mt <= 6) return fold_fits_mt<6>(M, parts);
+  if (mt <= 8) return fold_fits_mt<8>(M, parts);
+  return fold_fits_mt<10>(M, parts);
+}
 
 int32_t launch_lm_head(const HeadParams& p, bool argmax, hipStream_t s, int* key_cols) {
   const int mt = (p.M + 15) / 16;

@@ -10,12 +10,23 @@ namespace nsg {
 // wide W (vocabulary rows): logits in bf16 (out: M x N, ldy elements apart)
 // or, with keys, one argmax key per row and wave of the persistent grid
 // (out: M x key_cols uint64, the keys of linear.hip's argmax epilogue).
+//
+// With sumsq set, the final RMSNorm is folded in (its weight already folded
+// into W's columns): x holds the un-normalised rows, and row m's fp32 result
+// is multiplied by rsqrt(S_m / norm_dim + eps) before its bf16 rounding,
+// where S_m is the sum of sumsq[c * M + m] over c < parts, added in order
+// c = 0, 1, ... (the partial sums of squares, one per 16 columns, that the
+// last decoder layer's down_proj epilogue writes).
 struct HeadParams {
   const bf16* x;
   const bf16* w;
   void* out;
   int64_t ldx, ldw, ldy;
   int M, N, K;
+  const float* sumsq;
+  int parts;
+  int norm_dim;
+  float eps;
 };
 
 constexpr int kHeadMinRows = 1;
@@ -26,5 +37,11 @@ constexpr int kHeadStep = 64;  // K must be a multiple of this (and at least 3 s
 // row written, at most 4 * ceil(N / 128)); the shape checks are the caller's:
 // 16-byte aligned rows of x and W, K % 64 == 0, K >= 192, N % 4 == 0.
 int32_t launch_lm_head(const HeadParams& p, bool argmax, hipStream_t s, int* key_cols);
+
+// Whether the folded norm fits the kernel at M rows with `parts` partial sums
+// per row: the partials are staged through one ring slot (M * parts a
+// multiple of 4, whole 1 KB copies, the slot's last KB left for the row
+// scales).
+bool lm_head_fold_fits(int M, int parts);
 
 }  // namespace nsg

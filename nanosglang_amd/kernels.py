@@ -688,6 +688,59 @@ def linear_argmax(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | No
     return out
 
 
+def lm_head_fold_supported(M: int, N: int, K: int, parts: int) -> bool:
+    """Whether :func:`lm_head_fold` takes M rows of K against N vocabulary
+    rows with ``parts`` partial sums of squares per row."""
+    return bool(_lib().nsg_lm_head_fold_supported(M, N, K, parts))
+
+
+def lm_head_fold(x: torch.Tensor, weight: torch.Tensor, sumsq_in: torch.Tensor, eps: float,
+                 out: torch.Tensor | None = None, argmax_out: torch.Tensor | None = None,
+                 workspace: AcceptWorkspace | None = None) -> torch.Tensor:
+    """The lm_head after the final RMSNorm with that norm folded in (C ABI:
+    nsg_lm_head_fold / nsg_lm_head_fold_argmax): ``x`` (M, K) holds the
+    un-normalised rows, ``weight`` (N, K) the norm weight folded into its
+    columns, ``sumsq_in`` (K / 16, M) float32 the rows' partial sums of
+    squares (the last layer's down_proj writes them); row m of x @ weight.T
+    is scaled by rsqrt(mean(x_m^2) + eps) before its bf16 rounding.  Returns
+    the (M, N) bf16 logits, or with ``argmax_out`` (int64 (M,), any positive
+    stride) each row's greedy token (the lowest column of its largest
+    logit), written there and returned."""
+    _require_gpu(x, "x")
+    M, K = x.shape
+    N = weight.shape[0]
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or x.stride(1) != 1 \
+            or weight.stride(1) != 1 or weight.shape[1] != K:
+        raise ValueError("x (M, K) and weight (N, K) must be bf16 rows with unit inner stride")
+    if sumsq_in.dtype != torch.float32 or sumsq_in.dim() != 2 or sumsq_in.shape[1] != M \
+            or not sumsq_in.is_contiguous():
+        raise ValueError("sumsq_in must be contiguous float32 (parts, M)")
+    parts = sumsq_in.shape[0]
+    lib = _lib()
+    stream = _stream_ptr(x.device)
+    if argmax_out is None:
+        if out is None:
+            out = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
+        if out.dtype != torch.bfloat16 or out.shape != (M, N) or out.stride(1) != 1:
+            raise ValueError("out must be bf16 (M, N) rows with unit inner stride")
+        check(lib.nsg_lm_head_fold(x.data_ptr(), x.stride(0), weight.data_ptr(),
+                                   weight.stride(0), out.data_ptr(), out.stride(0), M, N, K,
+                                   sumsq_in.data_ptr(), parts, K, float(eps), stream),
+              "nsg_lm_head_fold")
+        return out
+    if argmax_out.dtype != torch.int64 or argmax_out.dim() != 1 or argmax_out.numel() != M \
+            or argmax_out.stride(0) < 1:
+        raise ValueError("argmax_out must be int64 (M,) with a positive stride")
+    ws = (workspace or _accept_ws(x.device, "argmax")).get(
+        lib.nsg_linear_argmax_workspace_bytes(M, N))
+    check(lib.nsg_lm_head_fold_argmax(x.data_ptr(), x.stride(0), weight.data_ptr(),
+                                      weight.stride(0), M, N, K, sumsq_in.data_ptr(), parts, K,
+                                      float(eps), ws.data_ptr(), ws.numel(),
+                                      argmax_out.data_ptr(), argmax_out.stride(0), stream),
+          "nsg_lm_head_fold_argmax")
+    return argmax_out
+
+
 def embed_rows(ids: torch.Tensor, table: torch.Tensor, out: torch.Tensor | None = None,
                sumsq_out: torch.Tensor | None = None) -> torch.Tensor:
     """table[ids] for int64 ids of shape (T,) or (B, J), any strides, as

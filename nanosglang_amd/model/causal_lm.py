@@ -27,7 +27,9 @@ MI355X-side choices:
   o_proj and down_proj kernels add their result to the residual stream and
   write the rows' partial sums of squares, and the q/k/v and gate/up kernels
   scale each row by rsqrt(mean(x^2) + eps) before their epilogues -- two
-  launches fewer per layer;
+  launches fewer per layer; the final norm folds into the lm_head the same
+  way (``kernels.lm_head_fold``) when every row's logits or tokens are
+  wanted;
 * a draft made of the first ``n`` layers plus the shared embedding, final
   norm and lm_head is ``forward_packed(..., num_layers=n)`` on the same
   weights.
@@ -129,6 +131,7 @@ class CausalLM:
                     "ln1": d(L["ln1"]), "ln2": d(L["ln2"])})
             self.norm = d(weights["norm"])
         self.lm_head = self.embed  # tie_word_embeddings
+        self.lm_head_g = None
         self.rope_cos, self.rope_sin = rope_tables(c, self.device)
         self._fold = self._fold_norm_weights()
         self.last_forward_folded = False
@@ -137,14 +140,24 @@ class CausalLM:
         """RMSNorm folded into the linears after it (bf16 weights, hidden a
         multiple of 16 and at most 1024): each layer gets copies of its q/k/v
         and gate/up weights with its norm weight folded into their columns,
-        ``qkv_g`` / ``gate_up_g`` = bf16(w_ln[k] * W[n, k]); the forward then
-        runs the folded path (``forward_packed``).  Returns whether it did."""
+        ``qkv_g`` / ``gate_up_g`` = bf16(w_ln[k] * W[n, k]), and the lm_head
+        the final norm's weight (``lm_head_g``); the forward then runs the
+        folded path (``forward_packed``).  Returns whether it did."""
         H = self.config.hidden_size
         if self.dtype != torch.bfloat16 or H % 16 or H > 1024:
             return False
         for L in self.layers:
             L["qkv_g"] = (L["qkv"].float() * L["ln1"].float()[None, :]).to(torch.bfloat16)
             L["gate_up_g"] = (L["gate_up"].float() * L["ln2"].float()[None, :]).to(torch.bfloat16)
+        # the final norm folded into the lm_head the same way (the tied
+        # embedding itself when the norm weight is all ones)
+        if bool((self.norm == 1).all()):
+            self.lm_head_g = self.lm_head
+        else:
+            self.lm_head_g = torch.empty_like(self.lm_head)
+            for r0 in range(0, self.lm_head.shape[0], 16384):
+                rows = self.lm_head[r0:r0 + 16384].float() * self.norm.float()[None, :]
+                self.lm_head_g[r0:r0 + 16384] = rows.to(torch.bfloat16)
         self._ones = torch.ones(H, device=self.device, dtype=torch.bfloat16)
         return True
 
@@ -166,6 +179,7 @@ class CausalLM:
         # FP8 weights keep the norms as kernels of their own (a per-row FP8
         # scale cannot absorb a per-column norm weight)
         self._fold = False
+        self.lm_head_g = None
         for L in self.layers:
             L.pop("qkv_g", None)
             L.pop("gate_up_g", None)
@@ -242,6 +256,17 @@ class CausalLM:
                 g = kernels.linear(residual, L["gate_up_g"], swiglu=True, sumsq_in=ssb,
                                    norm_eps=eps)
                 kernels.linear(g, L["down"], residual=residual, sumsq_out=ssa)
+            if logit_indices is None and kernels.lm_head_fold_supported(
+                    T, c.vocab_size, c.hidden_size, ssa.shape[0]):
+                # the final norm folded into the lm_head (causal_lm.py:643-645):
+                # the residual rows and their partial sums go straight in
+                if argmax_out is not None:
+                    if argmax_logits is not None:
+                        kernels.lm_head_fold(residual, self.lm_head_g, ssa, eps,
+                                             out=argmax_logits)
+                    return kernels.lm_head_fold(residual, self.lm_head_g, ssa, eps,
+                                                argmax_out=argmax_out, workspace=argmax_ws)
+                return kernels.lm_head_fold(residual, self.lm_head_g, ssa, eps)
             h = kernels.rmsnorm(residual, self.norm, eps)
         else:
             # separate norm kernels; with folded weights (many rows: prefill)

@@ -213,3 +213,27 @@ def test_sample_workspace_and_argument_checks(lib):
     rc = lib.nsg_sample(None, 10, 2, 1, 10, 1.0, 0, 1.0, None, 1, None, None, 0, None)
     assert rc == 1 and "logits_dtype" in lib.nsg_last_error().decode()
     assert lib.nsg_sample(None, 10, 0, 0, 10, 1.0, 5, 0.5, None, 1, None, None, 0, None) == 0
+
+
+def test_lm_head_fold_shape_rule_and_argument_checks(lib):
+    """nsg_lm_head_fold_supported is host logic: the partial sums of every
+    row must fit one ring slot of the lm_head kernel (M * parts a multiple of
+    4, whole 1 KB copies, one KB kept for the row scales)."""
+    ok = lib.nsg_lm_head_fold_supported
+    assert ok(160, 151936, 896, 56) == 1          # the 0.5B verify call
+    assert ok(32, 151936, 896, 56) == 1           # a draft call
+    assert ok(1, 1000, 896, 56) == 1
+    assert ok(160, 151936, 1024, 64) == 0         # 40 KB of partials > the slot
+    assert ok(128, 151936, 1024, 64) == 0         # 32 KB: no KB left for the scales
+    assert ok(96, 151936, 1024, 64) == 1
+    assert ok(161, 151936, 896, 56) == 0          # more rows than the kernel takes
+    assert ok(7, 1000, 896, 57) == 0              # 7 * 57 not a multiple of 4
+    assert ok(32, 1002, 896, 56) == 0             # N % 4
+    assert ok(32, 1000, 800, 50) == 0             # K % 64
+    # argument errors before any GPU work
+    rc = lib.nsg_lm_head_fold(None, 896, None, 896, None, 1000, 32, 1000, 896, None, 56, 896,
+                              1e-6, None)
+    assert rc == 1 and "null" in lib.nsg_last_error().decode()
+    rc = lib.nsg_lm_head_fold_argmax(16, 896, 16, 896, 161, 1000, 896, 16, 56, 896, 1e-6, None,
+                                     0, None, 1, None)
+    assert rc == 1 and "M 161" in lib.nsg_last_error().decode()

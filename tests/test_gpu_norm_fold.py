@@ -8,6 +8,9 @@ PyTorch fp32 references of the same ops:
 * consumer (gate/up with SwiGLU, q/k/v with RoPE + KV write): x holds the
   un-normalised rows, W the norm weight folded into its columns, and each
   row of x W^T is scaled by rsqrt(mean(x^2) + eps) before the epilogue;
+* the lm_head with the final norm folded in (logits and greedy tokens):
+  bit-exact against the plain lm_head on rows whose scale is a power of two,
+  within bf16 rounding of the fp32 value otherwise;
 * bitwise-identical results across calls and graph replays (the partial
   sums are added in one fixed order, no atomics).
 """
@@ -138,6 +141,112 @@ def test_consumer_rope_exact_rows(M, Hq, Hkv, D, K):
     q2 = kernels.linear_rope_kv(h, w, b, Hq, Hkv, D, pos, cos, sin, slots, kc2, vc2, force=True)
     torch.cuda.synchronize()
     assert torch.equal(q, q2) and torch.equal(kc, kc2) and torch.equal(vc, vc2)
+
+
+@pytest.mark.parametrize("M", [1, 17, 32, 100, 160])
+@pytest.mark.parametrize("N", [1000, 151936])
+def test_lm_head_fold_exact_rows(M, N):
+    """Folded lm_head against the plain lm_head on the normalised rows, bit
+    for bit, logits and greedy tokens (see _power_of_two_rows; the integer
+    weights make many equal logits, so the tokens also check the tie rule:
+    the lowest column wins)."""
+    from nanosglang_amd import kernels
+    K = 896
+    print(f"case: lm_head fold exact M={M} N={N}", flush=True)
+    x, h = _power_of_two_rows(M, K, seed=M + N)
+    g = torch.Generator(device="cuda").manual_seed(M + 3)
+    w = torch.randint(-1, 2, (N, K), generator=g, device="cuda").bfloat16()
+    ss = kernels.row_sumsq(x)
+    assert kernels.lm_head_fold_supported(M, N, K, ss.shape[0])
+    y = kernels.lm_head_fold(x, w, ss, 0.0)
+    y2 = kernels.linear(h, w, force=True)
+    tok = torch.full((M, 3), -1, dtype=torch.int64, device="cuda")
+    kernels.lm_head_fold(x, w, ss, 0.0, argmax_out=tok[:, 1])
+    tok2 = kernels.linear_argmax(h, w)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    assert torch.equal(tok[:, 1], tok2)
+    assert (tok[:, 0] == -1).all() and (tok[:, 2] == -1).all()
+    first = (y2.float() == y2.float().max(1, keepdim=True).values).int().argmax(1)
+    assert torch.equal(tok2, first)
+
+
+@pytest.mark.parametrize("M", [1, 33, 160])
+def test_lm_head_fold_scales_rows(M):
+    """Random rows and a random norm weight: the logits within bf16 rounding
+    of the fp32 value r_m * (x_m . bf16(w_norm * W_n)), and each greedy token
+    the first column of its row's largest returned logit."""
+    from nanosglang_amd import kernels
+    K, N = 896, 151936
+    print(f"case: lm_head fold M={M}", flush=True)
+    x = _rand((M, K), seed=M + 41, scale=3.0)
+    gamma = (torch.rand(K, generator=torch.Generator(device="cuda").manual_seed(6),
+                        device="cuda") + 0.5).bfloat16()
+    w = _rand((N, K), seed=42, scale=K ** -0.5)
+    wg = (w.float() * gamma.float()[None, :]).bfloat16()
+    ss = kernels.row_sumsq(x)
+    y = kernels.lm_head_fold(x, wg, ss, EPS)
+    tok = kernels.lm_head_fold(x, wg, ss, EPS,
+                               argmax_out=torch.empty(M, dtype=torch.int64, device="cuda"))
+    torch.cuda.synchronize()
+    r = torch.rsqrt((x.float() ** 2).mean(-1, keepdim=True) + EPS)
+    ref = r * (x.float() @ wg.float().T)
+    err = (y.float() - ref).abs()
+    print(f"  max err {err.max().item():.3e}", flush=True)
+    assert (err <= 2.0 ** -7 * ref.abs() + 1e-3).all()
+    yf = y.float()
+    first = (yf == yf.max(1, keepdim=True).values).int().argmax(1)
+    assert torch.equal(tok, first)
+
+
+def test_lm_head_fold_rejects_what_does_not_fit():
+    """Shapes outside the folded kernel: an error, no launch."""
+    from nanosglang_amd import kernels
+    print("case: lm_head fold unsupported shapes", flush=True)
+    assert not kernels.lm_head_fold_supported(160, 1000, 1024, 64)   # partials > one ring slot
+    assert not kernels.lm_head_fold_supported(161, 1000, 896, 56)    # more than 160 rows
+    x = _rand((160, 1024), seed=7)
+    w = _rand((1000, 1024), seed=8)
+    with pytest.raises(RuntimeError):
+        kernels.lm_head_fold(x, w, kernels.row_sumsq(x), EPS)
+
+
+def test_lm_head_fold_is_deterministic_and_graph_safe():
+    """The folded lm_head (logits and tokens) after a producer: the same bits
+    across eager calls and graph replays with eager work in between."""
+    from nanosglang_amd import kernels
+    print("case: lm_head fold graph replay", flush=True)
+    M, H, N = 160, 896, 151936
+    x = _rand((M, H), seed=51)
+    wo = _rand((H, H), seed=52, scale=H ** -0.5)
+    wl = _rand((N, H), seed=53, scale=H ** -0.5)
+    res0 = _rand((M, H), seed=54, scale=2.0)
+    res, ss = res0.clone(), torch.empty(H // 16, M, device="cuda")
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    tok = torch.empty(M, dtype=torch.int64, device="cuda")
+
+    def step():
+        kernels.linear(x, wo, residual=res, sumsq_out=ss)
+        kernels.lm_head_fold(res, wl, ss, EPS, out=out)
+        kernels.lm_head_fold(res, wl, ss, EPS, argmax_out=tok)
+
+    step()
+    ref, ref_tok = out.clone(), tok.clone()
+    graph = torch.cuda.CUDAGraph()
+    res.copy_(res0)
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(3):
+        res.copy_(res0)
+        out.zero_()
+        tok.fill_(-1)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref) and torch.equal(tok, ref_tok)
+        res.copy_(res0)
+        step()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref) and torch.equal(tok, ref_tok)
 
 
 def test_folded_linears_are_deterministic_and_graph_safe():

@@ -43,7 +43,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 19
+#define NSG_ABI_VERSION 20
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -273,6 +273,20 @@ int32_t nsg_spec_accept_greedy_tokens(const int64_t* target_tokens,
                                       int32_t page_size, int32_t* num_emitted, int64_t* emitted,
                                       int64_t* rollback_slots, int32_t* flags,
                                       nsg_stream_t stream);
+
+/* nsg_spec_accept_greedy_tokens with target token i of request b the greedy
+ * token of keys row b * (k + 1) + i (key_cols keys per row, from
+ * nsg_lm_head_fold_keys over the verify rows), reduced in the same launch;
+ * target_tokens_out (may be NULL) receives those tokens. */
+int32_t nsg_spec_accept_greedy_keys(const void* target_keys, int32_t key_cols,
+                                    int64_t* target_tokens_out, const int64_t* draft_tokens,
+                                    int64_t draft_stride_b, int64_t draft_stride_j,
+                                    int32_t batch, int32_t k, int32_t vocab,
+                                    const int32_t* kv_indptr, const int32_t* kv_indices,
+                                    const int32_t* start_pos, int32_t page_size,
+                                    int32_t* num_emitted, int64_t* emitted,
+                                    int64_t* rollback_slots, int32_t* flags,
+                                    nsg_stream_t stream);
 
 /* Copies the acceptance workspace's error flags (bits as above) to *flags_h
  * after synchronising the stream, and clears them.  After bit 3 it zeroes
@@ -545,6 +559,17 @@ int32_t nsg_lm_head_fold_argmax(const void* x, int64_t ldx, const void* w, int64
                                 int32_t sumsq_parts, int32_t norm_dim, float eps,
                                 void* workspace, int64_t workspace_bytes, int64_t* tokens,
                                 int64_t token_stride, nsg_stream_t stream);
+/* nsg_lm_head_fold_argmax without the second launch: only the argmax keys
+ * (M rows of *key_cols uint64 keys, written to keys, keys_bytes >=
+ * nsg_linear_argmax_workspace_bytes(M, N)), for a consumer that reduces them
+ * itself (nsg_embed_rows_keys, nsg_spec_accept_greedy_keys): the row's token
+ * is the column of its largest key (0xffffffff - the key's low 32 bits),
+ * the token nsg_lm_head_fold_argmax writes.  *key_cols (at most
+ * 4 * ceil(N / 128)) depends only on M, N and the device. */
+int32_t nsg_lm_head_fold_keys(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t M,
+                              int32_t N, int32_t K, const float* sumsq_in, int32_t sumsq_parts,
+                              int32_t norm_dim, float eps, void* keys, int64_t keys_bytes,
+                              int32_t* key_cols, nsg_stream_t stream);
 
 /* Embedding rows: out[r] = table[ids[b * id_stride_b + j * id_stride_j]] for
  * r = b * per_batch + j (embed_tokens(input_ids), causal_lm.py:613, on an index view
@@ -556,6 +581,17 @@ int32_t nsg_embed_rows(const int64_t* ids, int64_t id_stride_b, int64_t id_strid
                        int32_t batch, int32_t per_batch, const void* table, int64_t ld_table,
                        int32_t vocab, int32_t hidden, void* out, int64_t ld_out,
                        float* sumsq_out, nsg_stream_t stream);
+/* nsg_embed_rows where column key_j of the ids is the greedy token of the
+ * previous lm_head call (its argmax keys, nsg_lm_head_fold_keys: keys row b,
+ * key_cols keys): for every b, ids[b * id_stride_b + key_j * id_stride_j] =
+ * that token is written, then its row looked up with the others.  The draft
+ * model's next input (speculative.py:95-100, 104-109) without a launch of
+ * its own. */
+int32_t nsg_embed_rows_keys(int64_t* ids, int64_t id_stride_b, int64_t id_stride_j,
+                            int32_t batch, int32_t per_batch, int32_t key_j, const void* keys,
+                            int32_t key_cols, const void* table, int64_t ld_table, int32_t vocab,
+                            int32_t hidden, void* out, int64_t ld_out, float* sumsq_out,
+                            nsg_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Philox4x32-10 uniforms: out[i] = u(seed, stream_id, offset + i) with

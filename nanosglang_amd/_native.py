@@ -13,7 +13,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libnsg_spec.so")
 
 NSG_ATTN_WORK_INTS = 8
-ABI_VERSION = 19
+ABI_VERSION = 20
 
 i32, i64, u32, u64, f32 = C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_float
 vp = C.c_void_p
@@ -63,6 +63,8 @@ SIGNATURES = {
     "nsg_spec_accept_check_flags": (i32, [vp, i64, C.POINTER(i32), vp]),
     "nsg_spec_accept_greedy_tokens": (i32, [vp, vp, i64, i64, i32, i32, i32, vp, vp, vp, i32,
                                             vp, vp, vp, vp, vp]),
+    "nsg_spec_accept_greedy_keys": (i32, [vp, i32, vp, vp, i64, i64, i32, i32, i32, vp, vp, vp,
+                                          i32, vp, vp, vp, vp, vp]),
     "nsg_spec_accept_workspace_bytes": (i64, [i32, i32, i32]),
     "nsg_spec_accept": (i32, [vp, i64, i64, vp, i64, i64, i32, vp, vp, vp, i32, i32, i32, f32,
                               vp, vp, vp, i32, vp, vp, vp, vp, i64, vp]),
@@ -90,6 +92,10 @@ SIGNATURES = {
     "nsg_lm_head_fold_argmax": (i32, [vp, i64, vp, i64, i32, i32, i32, vp, i32, i32, f32, vp,
                                       i64, vp, i64, vp]),
     "nsg_embed_rows": (i32, [vp, i64, i64, i32, i32, vp, i64, i32, i32, vp, i64, vp, vp]),
+    "nsg_lm_head_fold_keys": (i32, [vp, i64, vp, i64, i32, i32, i32, vp, i32, i32, f32, vp, i64,
+                                    vp, vp]),
+    "nsg_embed_rows_keys": (i32, [vp, i64, i64, i32, i32, i32, vp, i32, vp, i64, i32, i32, vp,
+                                  i64, vp, vp]),
     "nsg_silu_mul": (i32, [vp, vp, i64, i32, vp]),
     "nsg_philox_uniform": (i32, [u64, u32, u64, i64, vp, vp]),
     "nsg_export_step": (i32, [vp, vp, i32, i32, vp, vp, vp, vp]),

@@ -126,6 +126,37 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Greedy argmax keys of the lm_head kernels: per row, one key per workgroup
+// (or wave) = (order-preserving bits of its largest bf16 logit) << 32 |
+// (0xffffffff - its lowest column), 0 for no column; the row's token is the
+// column of the largest key.  One wave reduces a row of n keys: up to 16
+// loads per lane in flight at once (addresses clamped, values past n
+// dropped), then an xor butterfly; every lane returns the row's largest key.
+__device__ __forceinline__ uint64_t wave_max_key(const uint64_t* row, int n, int lane) {
+  constexpr int kU = 16;
+  uint64_t k = 0;
+  for (int c0 = 0; c0 < n; c0 += 64 * kU) {
+    uint64_t v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) v[u] = row[min(c0 + u * 64 + lane, n - 1)];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const uint64_t x = c0 + u * 64 + lane < n ? v[u] : 0;
+      k = x > k ? x : k;
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t other = ((uint64_t)(uint32_t)__shfl_xor((int)(k >> 32), o, 64) << 32) |
+                           (uint32_t)__shfl_xor((int)(uint32_t)k, o, 64);
+    k = other > k ? other : k;
+  }
+  return k;
+}
+__device__ __forceinline__ int64_t key_token(uint64_t k) {
+  return (int64_t)(0xffffffffu - (uint32_t)k);
+}
+
 // s_waitcnt immediate that waits until at most n vector-memory ops of this
 // wave are outstanding (gfx9 encoding: vmcnt bits [3:0] and [15:14]; expcnt
 // and lgkmcnt left at their maxima, i.e. not waited on).

@@ -166,15 +166,26 @@ __global__ __launch_bounds__(kNormThreads) void row_sumsq_kernel(const uint16_t*
 // outside [0, vocab) read the nearest valid row), one wave per row, and, when
 // sumsq is given, the row's per-16-column sums of squares
 // sumsq[(c / 16) rows + r] (the layout row_sumsq_kernel writes).
+// With keys: the ids of column key_j (rows r = b * J + key_j) are first the
+// greedy tokens of keys row b (key_cols keys, the lm_head's argmax keys),
+// written to ids and then looked up; the other rows read their ids.
 __global__ __launch_bounds__(kNormThreads) void embed_rows_kernel(
-    const int64_t* __restrict__ ids, int64_t sb, int64_t sj, int J, int rows,
+    int64_t* __restrict__ ids, int64_t sb, int64_t sj, int J, int rows,
     const uint16_t* __restrict__ table, int64_t ldt, int vocab, int H,
-    uint16_t* __restrict__ out, int64_t ldo, float* __restrict__ sumsq) {
+    uint16_t* __restrict__ out, int64_t ldo, float* __restrict__ sumsq,
+    const uint64_t* __restrict__ keys, int key_cols, int key_j) {
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * (kNormThreads / 64) + (threadIdx.x >> 6);
   if (r >= rows) return;  // wave-uniform
   const int b = r / J, j = r - b * J;
-  const int64_t id = min(max(ids[b * sb + j * sj], (int64_t)0), (int64_t)vocab - 1);
+  int64_t raw;
+  if (keys && j == key_j) {  // wave-uniform
+    raw = key_token(wave_max_key(keys + (int64_t)b * key_cols, key_cols, lane));
+    if (lane == 0) ids[b * sb + j * sj] = raw;
+  } else {
+    raw = ids[b * sb + j * sj];
+  }
+  const int64_t id = min(max(raw, (int64_t)0), (int64_t)vocab - 1);
   const uint16_t* src = table + id * ldt;
   uint16_t* dst = out + (int64_t)r * ldo;
   const int nseg = H >> 3;  // 16-byte segments of a row
@@ -270,10 +281,12 @@ extern "C" int32_t nsg_row_sumsq(const void* x, int64_t ldx, int32_t num_tokens,
   return launch_status("row_sumsq_kernel");
 }
 
-extern "C" int32_t nsg_embed_rows(const int64_t* ids, int64_t id_stride_b, int64_t id_stride_j,
-                                  int32_t batch, int32_t per_batch, const void* table,
-                                  int64_t ld_table, int32_t vocab, int32_t hidden, void* out,
-                                  int64_t ld_out, float* sumsq_out, nsg_stream_t stream) {
+namespace {
+
+int32_t embed_impl(int64_t* ids, int64_t id_stride_b, int64_t id_stride_j, int32_t batch,
+                   int32_t per_batch, const uint64_t* keys, int32_t key_cols, int32_t key_j,
+                   const void* table, int64_t ld_table, int32_t vocab, int32_t hidden, void* out,
+                   int64_t ld_out, float* sumsq_out, nsg_stream_t stream) {
   NSG_CHECK_ARG(batch >= 0 && per_batch >= 0, "batch %d, per_batch %d", batch, per_batch);
   const int64_t rows = (int64_t)batch * per_batch;
   if (rows == 0) {
@@ -287,11 +300,39 @@ extern "C" int32_t nsg_embed_rows(const int64_t* ids, int64_t id_stride_b, int64
                     (uintptr_t)table % 16 == 0 && (uintptr_t)out % 16 == 0,
                 "table and out rows must be 16-byte aligned");
   const dim3 grid((unsigned)((rows + kNormThreads / 64 - 1) / (kNormThreads / 64)));
+  NSG_CHECK_ARG(!keys || (key_cols >= 1 && key_j >= 0 && key_j < per_batch &&
+                          (uintptr_t)keys % 8 == 0),
+                "keys: key_cols %d >= 1, key_j %d in [0, per_batch %d), 8-byte aligned",
+                key_cols, key_j, per_batch);
   hipLaunchKernelGGL(embed_rows_kernel, grid, dim3(kNormThreads), 0,
                      static_cast<hipStream_t>(stream), ids, id_stride_b, id_stride_j, per_batch,
                      (int)rows, static_cast<const uint16_t*>(table), ld_table, vocab, hidden,
-                     static_cast<uint16_t*>(out), ld_out, sumsq_out);
+                     static_cast<uint16_t*>(out), ld_out, sumsq_out, keys, key_cols, key_j);
   return launch_status("embed_rows_kernel");
+}
+
+}  // namespace
+
+extern "C" int32_t nsg_embed_rows(const int64_t* ids, int64_t id_stride_b, int64_t id_stride_j,
+                                  int32_t batch, int32_t per_batch, const void* table,
+                                  int64_t ld_table, int32_t vocab, int32_t hidden, void* out,
+                                  int64_t ld_out, float* sumsq_out, nsg_stream_t stream) {
+  // without keys the kernel only reads ids
+  return embed_impl(const_cast<int64_t*>(ids), id_stride_b, id_stride_j, batch, per_batch,
+                    nullptr, 0, 0, table, ld_table, vocab, hidden, out, ld_out, sumsq_out,
+                    stream);
+}
+
+extern "C" int32_t nsg_embed_rows_keys(int64_t* ids, int64_t id_stride_b, int64_t id_stride_j,
+                                       int32_t batch, int32_t per_batch, int32_t key_j,
+                                       const void* keys, int32_t key_cols, const void* table,
+                                       int64_t ld_table, int32_t vocab, int32_t hidden,
+                                       void* out, int64_t ld_out, float* sumsq_out,
+                                       nsg_stream_t stream) {
+  NSG_CHECK_ARG(keys != nullptr, "null keys");
+  return embed_impl(ids, id_stride_b, id_stride_j, batch, per_batch,
+                    static_cast<const uint64_t*>(keys), key_cols, key_j, table, ld_table, vocab,
+                    hidden, out, ld_out, sumsq_out, stream);
 }
 
 extern "C" int32_t nsg_silu_mul(const void* gate_up, void* out, int64_t num_tokens,

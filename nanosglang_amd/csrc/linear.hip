@@ -1164,6 +1164,27 @@ extern "C" int32_t nsg_lm_head_fold_argmax(const void* x, int64_t ldx, const voi
   return launch_status("argmax_keys_kernel");
 }
 
+extern "C" int32_t nsg_lm_head_fold_keys(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                         int32_t M, int32_t N, int32_t K,
+                                         const float* sumsq_in, int32_t sumsq_parts,
+                                         int32_t norm_dim, float eps, void* keys,
+                                         int64_t keys_bytes, int32_t* key_cols,
+                                         nsg_stream_t stream) {
+  HeadParams hp{};
+  if (int32_t rc = head_fold_params(x, ldx, w, ldw, M, N, K, sumsq_in, sumsq_parts, norm_dim,
+                                    eps, &hp))
+    return rc;
+  NSG_CHECK_ARG(keys && key_cols && (uintptr_t)keys % 8 == 0,
+                "null keys or key_cols, or keys not 8-byte aligned");
+  NSG_CHECK_ARG(keys_bytes >= nsg_linear_argmax_workspace_bytes(M, N), "keys %lld bytes < %lld",
+                (long long)keys_bytes, (long long)nsg_linear_argmax_workspace_bytes(M, N));
+  hp.out = keys;
+  int kc = 0;
+  if (int32_t rc = launch_lm_head(hp, true, static_cast<hipStream_t>(stream), &kc)) return rc;
+  *key_cols = kc;
+  return NSG_OK;
+}
+
 // ---- FP8 weights for a library GEMM (many rows, prefill) ----
 // The dequantisation of FP8Linear.forward (w8.to(bf16) * scale,
 // quantization.py:49-52) in one pass: 16 weight bytes per thread in, 32

@@ -1424,16 +1424,12 @@ extern "C" int32_t nsg_spec_accept_noalloc(
 // request, lane i <= k holding target token i and lane i < k draft token i.
 namespace nsg {
 namespace {
-__global__ __launch_bounds__(64) void greedy_tokens_kernel(AccParams p,
-                                                           const int64_t* __restrict__ ttok,
-                                                           int64_t ds_b, int64_t ds_j) {
-  const int b = blockIdx.x;
-  const int lane = threadIdx.x;
+// The rule for request b on one wave, lane i <= k holding target token t.
+__device__ __forceinline__ void greedy_rule(const AccParams& p, int b, int lane, int64_t t,
+                                            int64_t ds_b, int64_t ds_j, int64_t pre) {
   const int k = p.k;
-  const int64_t pre = rollback_prefetch(p, b, lane);
-  int64_t x = -1, t = -1;
+  int64_t x = -1;
   if (lane < k) x = p.dtok[b * ds_b + lane * ds_j];
-  if (lane <= k) t = ttok[(int64_t)b * (k + 1) + lane];
   if (lane < k && (x < 0 || x >= p.V) && p.flags) atomicOr(p.flags, 4);  // never matches
   const uint64_t miss = __builtin_amdgcn_ballot_w64(lane < k && x != t);
   const int j = miss ? (int)__builtin_ctzll(miss) : k;  // first mismatch, or k
@@ -1441,27 +1437,58 @@ __global__ __launch_bounds__(64) void greedy_tokens_kernel(AccParams p,
   if (lane == 0) p.n_out[b] = j + 1;
   rollback_lanes(p, b, j + 1, lane, pre);
 }
+
+__global__ __launch_bounds__(64) void greedy_tokens_kernel(AccParams p,
+                                                           const int64_t* __restrict__ ttok,
+                                                           int64_t ds_b, int64_t ds_j) {
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int k = p.k;
+  const int64_t pre = rollback_prefetch(p, b, lane);
+  const int64_t t = lane <= k ? ttok[(int64_t)b * (k + 1) + lane] : -1;
+  greedy_rule(p, b, lane, t, ds_b, ds_j, pre);
+}
+
+// The same with each target row's token reduced from the lm_head's argmax
+// keys in this launch (no separate reduction launch): wave w of the request's
+// workgroup reduces rows w, w + waves, ... into LDS (and ttok_out, when
+// given), then wave 0 applies the rule.
+constexpr int kKeyWaves = 16;
+__global__ __launch_bounds__(64 * kKeyWaves) void greedy_keys_kernel(
+    AccParams p, const uint64_t* __restrict__ keys, int key_cols, int64_t* __restrict__ ttok_out,
+    int64_t ds_b, int64_t ds_j) {
+  __shared__ int64_t tok[kMaxK + 1];
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int waves = blockDim.x >> 6;
+  const int k = p.k;
+  int64_t pre = 0;
+  if (wave == 0) pre = rollback_prefetch(p, b, lane);
+  for (int row = wave; row <= k; row += waves) {
+    const int64_t r = (int64_t)b * (k + 1) + row;
+    const int64_t t = key_token(wave_max_key(keys + r * key_cols, key_cols, lane));
+    if (lane == 0) {
+      tok[row] = t;
+      if (ttok_out) ttok_out[r] = t;
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  greedy_rule(p, b, lane, lane <= k ? tok[lane] : -1, ds_b, ds_j, pre);
+}
 }  // namespace
 }  // namespace nsg
 
-extern "C" int32_t nsg_spec_accept_greedy_tokens(const int64_t* target_tokens,
-                                                 const int64_t* draft_tokens,
-                                                 int64_t draft_stride_b, int64_t draft_stride_j,
-                                                 int32_t batch, int32_t k, int32_t vocab,
-                                                 const int32_t* kv_indptr,
-                                                 const int32_t* kv_indices,
-                                                 const int32_t* start_pos, int32_t page_size,
-                                                 int32_t* num_emitted, int64_t* emitted,
-                                                 int64_t* rollback_slots, int32_t* flags,
-                                                 nsg_stream_t stream) {
-  NSG_CHECK_ARG(batch >= 0 && batch <= kMaxBatch, "batch %d outside [0, %d]", batch, kMaxBatch);
-  NSG_CHECK_ARG(k >= 0 && k <= kMaxK, "k %d outside [0, %d]", k, kMaxK);
-  NSG_CHECK_ARG(vocab > 0, "vocab %d", vocab);
-  if (batch == 0) {
-    clear_error();
-    return NSG_OK;
-  }
-  NSG_CHECK_ARG(target_tokens && num_emitted && emitted, "null pointer argument");
+namespace {
+
+// The shared checks and parameters of the two greedy-from-argmax entries.
+int32_t greedy_params(const int64_t* draft_tokens, int64_t draft_stride_b,
+                      int64_t draft_stride_j, int32_t batch, int32_t k, int32_t vocab,
+                      const int32_t* kv_indptr, const int32_t* kv_indices,
+                      const int32_t* start_pos, int32_t page_size, int32_t* num_emitted,
+                      int64_t* emitted, int64_t* rollback_slots, int32_t* flags, AccParams* out) {
+  NSG_CHECK_ARG(num_emitted && emitted, "null pointer argument");
   NSG_CHECK_ARG(k == 0 || draft_tokens, "draft_tokens required when k > 0");
   NSG_CHECK_ARG(k == 0 || (draft_stride_b >= 0 && draft_stride_j >= 0),
                 "draft token strides %lld, %lld", (long long)draft_stride_b,
@@ -1488,10 +1515,72 @@ extern "C" int32_t nsg_spec_accept_greedy_tokens(const int64_t* target_tokens,
   p.emitted = emitted;
   p.rollback = k > 0 ? rollback_slots : nullptr;
   p.flags = flags;
+  *out = p;
+  return NSG_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t nsg_spec_accept_greedy_tokens(const int64_t* target_tokens,
+                                                 const int64_t* draft_tokens,
+                                                 int64_t draft_stride_b, int64_t draft_stride_j,
+                                                 int32_t batch, int32_t k, int32_t vocab,
+                                                 const int32_t* kv_indptr,
+                                                 const int32_t* kv_indices,
+                                                 const int32_t* start_pos, int32_t page_size,
+                                                 int32_t* num_emitted, int64_t* emitted,
+                                                 int64_t* rollback_slots, int32_t* flags,
+                                                 nsg_stream_t stream) {
+  NSG_CHECK_ARG(batch >= 0 && batch <= kMaxBatch, "batch %d outside [0, %d]", batch, kMaxBatch);
+  NSG_CHECK_ARG(k >= 0 && k <= kMaxK, "k %d outside [0, %d]", k, kMaxK);
+  NSG_CHECK_ARG(vocab > 0, "vocab %d", vocab);
+  if (batch == 0) {
+    clear_error();
+    return NSG_OK;
+  }
+  NSG_CHECK_ARG(target_tokens, "null pointer argument");
+  AccParams p{};
+  if (int32_t rc = greedy_params(draft_tokens, draft_stride_b, draft_stride_j, batch, k, vocab,
+                                 kv_indptr, kv_indices, start_pos, page_size, num_emitted,
+                                 emitted, rollback_slots, flags, &p))
+    return rc;
   hipLaunchKernelGGL(greedy_tokens_kernel, dim3(batch), dim3(64), 0,
                      static_cast<hipStream_t>(stream), p, target_tokens, draft_stride_b,
                      draft_stride_j);
   return launch_status("greedy_tokens_kernel");
+}
+
+extern "C" int32_t nsg_spec_accept_greedy_keys(const void* target_keys, int32_t key_cols,
+                                               int64_t* target_tokens_out,
+                                               const int64_t* draft_tokens,
+                                               int64_t draft_stride_b, int64_t draft_stride_j,
+                                               int32_t batch, int32_t k, int32_t vocab,
+                                               const int32_t* kv_indptr,
+                                               const int32_t* kv_indices,
+                                               const int32_t* start_pos, int32_t page_size,
+                                               int32_t* num_emitted, int64_t* emitted,
+                                               int64_t* rollback_slots, int32_t* flags,
+                                               nsg_stream_t stream) {
+  NSG_CHECK_ARG(batch >= 0 && batch <= kMaxBatch, "batch %d outside [0, %d]", batch, kMaxBatch);
+  NSG_CHECK_ARG(k >= 0 && k <= kMaxK, "k %d outside [0, %d]", k, kMaxK);
+  NSG_CHECK_ARG(vocab > 0, "vocab %d", vocab);
+  if (batch == 0) {
+    clear_error();
+    return NSG_OK;
+  }
+  NSG_CHECK_ARG(target_keys && key_cols >= 1 && (uintptr_t)target_keys % 8 == 0,
+                "target_keys (8-byte aligned) and key_cols %d >= 1 required", key_cols);
+  AccParams p{};
+  if (int32_t rc = greedy_params(draft_tokens, draft_stride_b, draft_stride_j, batch, k, vocab,
+                                 kv_indptr, kv_indices, start_pos, page_size, num_emitted,
+                                 emitted, rollback_slots, flags, &p))
+    return rc;
+  const int waves = std::min(k + 1, kKeyWaves);
+  hipLaunchKernelGGL(greedy_keys_kernel, dim3(batch), dim3(64 * waves), 0,
+                     static_cast<hipStream_t>(stream), p,
+                     static_cast<const uint64_t*>(target_keys), key_cols, target_tokens_out,
+                     draft_stride_b, draft_stride_j);
+  return launch_status("greedy_keys_kernel");
 }
 
 extern "C" int32_t nsg_spec_accept_check_flags(void* workspace, int64_t workspace_bytes,

@@ -323,6 +323,15 @@ class SpecEngine:
         rows of vocabulary 151,936) are never written nor read back."""
         return self._argmax_drafts(batch * (self.k + 1))
 
+    def _keys_mode(self, batch: int) -> bool:
+        """Greedy drafts and verify hand their tokens on as the lm_head's
+        argmax keys: each draft token is reduced by the next forward's
+        embedding lookup (which also writes it into the step's ids), the
+        verify tokens by the acceptance kernel -- no reduction launches."""
+        return (self.k >= 1 and self._argmax_drafts(batch) and self._argmax_verify(batch)
+                and self.model.keys_supported(batch)
+                and self.model.keys_supported(batch * (self.k + 1)))
+
     def _bonus(self, tl: torch.Tensor, u: torch.Tensor | None, workspace=None, out=None):
         """speculative.py:174-182: the bonus after k accepted drafts is
         sample_token(target row k) with top-k / top-p; None without filters
@@ -391,6 +400,28 @@ class SpecEngine:
         pool = self._pool()
         tok = g.ids[0]
         direct = self._argmax_drafts(bs)
+        if self._keys_mode(bs):
+            V = m.config.vocab_size
+            keys = self._argmax_ws.get(kernels._lib().nsg_linear_argmax_workspace_bytes(
+                self.max_batch * (k + 1), V))
+            kc = 0
+            for i in range(k):
+                # draft i's token column is written by draft i + 1's lookup
+                # (the last one's by the verify's), from draft i's keys
+                kc = m.forward_packed(g.ids[i], g.pos[i], pool, g.attn[i], g.slot[i], None,
+                                      self.draft_layers, argmax_keys_out=keys,
+                                      ids_keys=None if i == 0 else (keys, kc, 0))
+            kcv = m.forward_packed(g.vids, A["vpos"], pool, g.attn[k], A["vslot"],
+                                   argmax_keys_out=keys, argmax_logits=g.tlog,
+                                   ids_keys=(keys, kc, k))
+            g.tl = g.tlog
+            kernels.spec_accept_greedy_keys(keys, kcv, bs, k, g.vids[:, 1:], V, g.kvp[k],
+                                            g.idx[k], A["start"], page_size=self.P,
+                                            workspace=self._accept_ws,
+                                            out=(g.n_out, g.emitted, g.rollback),
+                                            target_tokens_out=g.ttok)
+            self._export(g)
+            return
         for i in range(k):
             if direct:
                 # the token lands in its row of the step's ids: the next

@@ -472,25 +472,7 @@ def spec_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor | None,
     return n_out, emitted, rollback
 
 
-def spec_accept_greedy_tokens(target_tokens: torch.Tensor, draft_tokens: torch.Tensor | None,
-                              vocab: int, kv_indptr: torch.Tensor | None = None,
-                              kv_indices: torch.Tensor | None = None,
-                              start_pos: torch.Tensor | None = None, page_size: int = 16,
-                              workspace: AcceptWorkspace | None = None, out: tuple | None = None):
-    """Greedy acceptance from each target row's greedy token (C ABI:
-    nsg_spec_accept_greedy_tokens): :func:`spec_accept` at temperature 0 with
-    ``target_tokens`` int64 (B, k+1) = the first argmax of each target row
-    (e.g. :func:`linear_argmax` of the verify forward), so the verify logits
-    are never stored; ``draft_tokens`` (B, k) may have any strides.  Same outputs and rollback slots; draft tokens outside
-    [0, vocab) set the error flag in ``workspace``'s header (read with its
-    ``check_flags``)."""
-    _require_gpu(target_tokens, "target_tokens")
-    dev = target_tokens.device
-    if target_tokens.dim() != 2 or target_tokens.dtype != torch.int64 \
-            or not target_tokens.is_contiguous():
-        raise ValueError("target_tokens must be contiguous int64 (B, k+1)")
-    B, k1 = target_tokens.shape
-    k = k1 - 1
+def _greedy_args(B, k, dev, draft_tokens, kv_indptr, kv_indices, start_pos, out):
     ds = (0, 0)
     if k > 0:
         if draft_tokens is None or tuple(draft_tokens.shape) != (B, k):
@@ -515,14 +497,71 @@ def spec_accept_greedy_tokens(target_tokens: torch.Tensor, draft_tokens: torch.T
         rollback = torch.full((B, k), -1, dtype=torch.int64, device=dev)
     else:
         n_out, emitted, rollback = out
+    tail = (_ptr(kv_indptr) if rb_ok else None, _ptr(kv_indices) if rb_ok else None,
+            _ptr(start_pos) if rb_ok else None)
+    return (draft_tokens, ds, tail, rb_ok, (n_out, emitted, rollback))
+
+
+def spec_accept_greedy_tokens(target_tokens: torch.Tensor, draft_tokens: torch.Tensor | None,
+                              vocab: int, kv_indptr: torch.Tensor | None = None,
+                              kv_indices: torch.Tensor | None = None,
+                              start_pos: torch.Tensor | None = None, page_size: int = 16,
+                              workspace: AcceptWorkspace | None = None, out: tuple | None = None):
+    """Greedy acceptance from each target row's greedy token (C ABI:
+    nsg_spec_accept_greedy_tokens): :func:`spec_accept` at temperature 0 with
+    ``target_tokens`` int64 (B, k+1) = the first argmax of each target row
+    (e.g. :func:`linear_argmax` of the verify forward), so the verify logits
+    are never stored; ``draft_tokens`` (B, k) may have any strides.  Same
+    outputs and rollback slots; draft tokens outside [0, vocab) set the error
+    flag in ``workspace``'s header (read with its ``check_flags``)."""
+    _require_gpu(target_tokens, "target_tokens")
+    dev = target_tokens.device
+    if target_tokens.dim() != 2 or target_tokens.dtype != torch.int64 \
+            or not target_tokens.is_contiguous():
+        raise ValueError("target_tokens must be contiguous int64 (B, k+1)")
+    B, k1 = target_tokens.shape
+    k = k1 - 1
+    draft_tokens, ds, tail, rb_ok, (n_out, emitted, rollback) = _greedy_args(
+        B, k, dev, draft_tokens, kv_indptr, kv_indices, start_pos, out)
     flags = (workspace or _accept_ws(dev)).get(256)
     rc = _lib().nsg_spec_accept_greedy_tokens(
         target_tokens.data_ptr(), _ptr(draft_tokens) if k > 0 else None, ds[0], ds[1], B, k,
-        int(vocab),
-        _ptr(kv_indptr) if rb_ok else None, _ptr(kv_indices) if rb_ok else None,
-        _ptr(start_pos) if rb_ok else None, page_size, n_out.data_ptr(), emitted.data_ptr(),
+        int(vocab), *tail, page_size, n_out.data_ptr(), emitted.data_ptr(),
         rollback.data_ptr() if rb_ok else None, flags.data_ptr(), _stream_ptr(dev))
     check(rc, "nsg_spec_accept_greedy_tokens")
+    return n_out, emitted, rollback
+
+
+def spec_accept_greedy_keys(target_keys: torch.Tensor, key_cols: int, B: int, k: int,
+                            draft_tokens: torch.Tensor | None, vocab: int,
+                            kv_indptr: torch.Tensor | None = None,
+                            kv_indices: torch.Tensor | None = None,
+                            start_pos: torch.Tensor | None = None, page_size: int = 16,
+                            workspace: AcceptWorkspace | None = None, out: tuple | None = None,
+                            target_tokens_out: torch.Tensor | None = None):
+    """:func:`spec_accept_greedy_tokens` with each target row's token reduced
+    in the same launch from the verify lm_head's argmax keys (C ABI:
+    nsg_spec_accept_greedy_keys): ``target_keys`` holds B * (k + 1) rows of
+    ``key_cols`` keys (:func:`lm_head_fold` with ``keys_out``);
+    ``target_tokens_out`` (contiguous int64, B * (k + 1)) receives the tokens
+    when given."""
+    _require_gpu(target_keys, "target_keys")
+    dev = target_keys.device
+    if target_keys.numel() * target_keys.element_size() < B * (k + 1) * key_cols * 8:
+        raise ValueError("target_keys holds fewer than B * (k + 1) * key_cols keys")
+    if target_tokens_out is not None and (target_tokens_out.dtype != torch.int64
+                                          or not target_tokens_out.is_contiguous()
+                                          or target_tokens_out.numel() != B * (k + 1)):
+        raise ValueError("target_tokens_out must be contiguous int64 (B * (k + 1),)")
+    draft_tokens, ds, tail, rb_ok, (n_out, emitted, rollback) = _greedy_args(
+        B, k, dev, draft_tokens, kv_indptr, kv_indices, start_pos, out)
+    flags = (workspace or _accept_ws(dev)).get(256)
+    rc = _lib().nsg_spec_accept_greedy_keys(
+        target_keys.data_ptr(), int(key_cols), _ptr(target_tokens_out),
+        _ptr(draft_tokens) if k > 0 else None, ds[0], ds[1], B, k, int(vocab), *tail,
+        page_size, n_out.data_ptr(), emitted.data_ptr(),
+        rollback.data_ptr() if rb_ok else None, flags.data_ptr(), _stream_ptr(dev))
+    check(rc, "nsg_spec_accept_greedy_keys")
     return n_out, emitted, rollback
 
 
@@ -696,7 +735,8 @@ def lm_head_fold_supported(M: int, N: int, K: int, parts: int) -> bool:
 
 def lm_head_fold(x: torch.Tensor, weight: torch.Tensor, sumsq_in: torch.Tensor, eps: float,
                  out: torch.Tensor | None = None, argmax_out: torch.Tensor | None = None,
-                 workspace: AcceptWorkspace | None = None) -> torch.Tensor:
+                 workspace: AcceptWorkspace | None = None,
+                 keys_out: torch.Tensor | None = None):
     """The lm_head after the final RMSNorm with that norm folded in (C ABI:
     nsg_lm_head_fold / nsg_lm_head_fold_argmax): ``x`` (M, K) holds the
     un-normalised rows, ``weight`` (N, K) the norm weight folded into its
@@ -705,7 +745,10 @@ def lm_head_fold(x: torch.Tensor, weight: torch.Tensor, sumsq_in: torch.Tensor, 
     is scaled by rsqrt(mean(x_m^2) + eps) before its bf16 rounding.  Returns
     the (M, N) bf16 logits, or with ``argmax_out`` (int64 (M,), any positive
     stride) each row's greedy token (the lowest column of its largest
-    logit), written there and returned."""
+    logit), written there and returned; or with ``keys_out`` (a device
+    buffer of at least nsg_linear_argmax_workspace_bytes(M, N) bytes) only
+    the argmax keys, for a consumer that reduces them (:func:`embed_rows`,
+    :func:`spec_accept_greedy_keys`), returning the keys per row."""
     _require_gpu(x, "x")
     M, K = x.shape
     N = weight.shape[0]
@@ -718,6 +761,15 @@ def lm_head_fold(x: torch.Tensor, weight: torch.Tensor, sumsq_in: torch.Tensor, 
     parts = sumsq_in.shape[0]
     lib = _lib()
     stream = _stream_ptr(x.device)
+    if keys_out is not None:
+        _require_gpu(keys_out, "keys_out")
+        kc = C.c_int32(0)
+        check(lib.nsg_lm_head_fold_keys(x.data_ptr(), x.stride(0), weight.data_ptr(),
+                                        weight.stride(0), M, N, K, sumsq_in.data_ptr(), parts,
+                                        K, float(eps), keys_out.data_ptr(),
+                                        keys_out.numel() * keys_out.element_size(),
+                                        C.byref(kc), stream), "nsg_lm_head_fold_keys")
+        return kc.value
     if argmax_out is None:
         if out is None:
             out = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
@@ -742,12 +794,15 @@ def lm_head_fold(x: torch.Tensor, weight: torch.Tensor, sumsq_in: torch.Tensor, 
 
 
 def embed_rows(ids: torch.Tensor, table: torch.Tensor, out: torch.Tensor | None = None,
-               sumsq_out: torch.Tensor | None = None) -> torch.Tensor:
+               sumsq_out: torch.Tensor | None = None, keys: tuple | None = None) -> torch.Tensor:
     """table[ids] for int64 ids of shape (T,) or (B, J), any strides, as
     (T or B * J, H) rows (C ABI: nsg_embed_rows); with ``sumsq_out``
     ((H / 16, rows) float32) also the rows' partial sums of squares, the
     layout :func:`row_sumsq` writes.  Ids outside [0, vocab) read the
-    nearest valid row."""
+    nearest valid row.  With ``keys`` = (key tensor, key_cols, key_j)
+    (C ABI: nsg_embed_rows_keys), column key_j of ``ids`` first receives the
+    greedy token of each key row b (the previous :func:`lm_head_fold` call's
+    ``keys_out``), which is then looked up."""
     _require_gpu(table, "table")
     _require_gpu(ids, "ids")
     if ids.dtype != torch.int64 or ids.dim() not in (1, 2):
@@ -764,6 +819,16 @@ def embed_rows(ids: torch.Tensor, table: torch.Tensor, out: torch.Tensor | None 
     if sumsq_out is not None and (sumsq_out.dtype != torch.float32 or not sumsq_out.is_contiguous()
                                   or tuple(sumsq_out.shape) != (H // 16, rows)):
         raise ValueError("sumsq_out must be contiguous float32 (H / 16, rows)")
+    if keys is not None:
+        kt, key_cols, key_j = keys
+        _require_gpu(kt, "keys")
+        if kt.numel() * kt.element_size() < B * int(key_cols) * 8:
+            raise ValueError("keys holds fewer than batch * key_cols keys")
+        check(_lib().nsg_embed_rows_keys(ids.data_ptr(), sb, sj, B, J, int(key_j), kt.data_ptr(),
+                                         int(key_cols), table.data_ptr(), table.stride(0), V, H,
+                                         out.data_ptr(), out.stride(0), _ptr(sumsq_out),
+                                         _stream_ptr(table.device)), "nsg_embed_rows_keys")
+        return out
     check(_lib().nsg_embed_rows(ids.data_ptr(), sb, sj, B, J, table.data_ptr(), table.stride(0), V,
                                 H, out.data_ptr(), out.stride(0), _ptr(sumsq_out),
                                 _stream_ptr(table.device)), "nsg_embed_rows")

@@ -198,6 +198,17 @@ class CausalLM:
                     L[n + "_d"] = kernels.dequant_fp8(L[n], L[n + "_s"])
         return self
 
+    def keys_supported(self, T: int) -> bool:
+        """Whether a forward over T rows can hand its greedy tokens to the
+        next one as argmax keys (``forward_packed(argmax_keys_out=...)``,
+        ``ids_keys``): the folded norms, the bf16 embedding lookup and the
+        folded lm_head all take T rows."""
+        c = self.config
+        return (self._fold and T <= kernels._lib().nsg_linear_max_rows()
+                and self.embed.dtype == torch.bfloat16 and c.hidden_size % 16 == 0
+                and kernels.lm_head_fold_supported(T, c.vocab_size, c.hidden_size,
+                                                   c.hidden_size // 16))
+
     @property
     def num_layers(self) -> int:
         return self.config.num_hidden_layers
@@ -207,7 +218,9 @@ class CausalLM:
                        attn_wrapper, write_indices: torch.Tensor,
                        logit_indices: torch.Tensor | None = None,
                        num_layers: int | None = None, argmax_out: torch.Tensor | None = None,
-                       argmax_ws=None, argmax_logits: torch.Tensor | None = None) -> torch.Tensor:
+                       argmax_ws=None, argmax_logits: torch.Tensor | None = None,
+                       argmax_keys_out: torch.Tensor | None = None,
+                       ids_keys: tuple | None = None):
         """Packed forward over ``T`` tokens of several requests.
 
         kv_cache: (k_cache, v_cache) pools (L, N, P, Hkv, D); attn_wrapper: a
@@ -217,7 +230,12 @@ class CausalLM:
         written there (``kernels.linear_argmax``: the logits are never
         stored); ``argmax_logits`` (T, V) bf16 then also receives the logits
         those tokens are the argmax of (same kernel and rounding; for tests
-        and traces)."""
+        and traces).  With ``argmax_keys_out`` (a device buffer) instead, only
+        the rows' argmax keys are written there and the keys per row returned
+        (``kernels.lm_head_fold``), for the next call's ``ids_keys`` =
+        (keys, key_cols, j): column j of ``input_ids`` (B, J) then receives
+        those greedy tokens inside the embedding lookup -- no reduction
+        launch between the two forwards.  Both need ``keys_supported``."""
         c = self.config
         Hq, Hkv, D, I = (c.num_attention_heads, c.num_key_value_heads, c.head_dim,
                          c.intermediate_size)
@@ -228,13 +246,18 @@ class CausalLM:
         folded = self._fold and T <= kernels._lib().nsg_linear_max_rows()
         self.last_forward_folded = folded     # which norm path the call took
         ssa = None
+        if (argmax_keys_out is not None or ids_keys is not None) and (
+                not self.keys_supported(T)
+                or (argmax_keys_out is not None and logit_indices is not None)):
+            raise ValueError(f"argmax keys need the folded forward with the folded lm_head "
+                             f"at {T} rows")
         if self.embed.dtype == torch.bfloat16 and c.hidden_size % 16 == 0:
             # causal_lm.py:613 -- ids may be any (T,) or (B, J) view; with the
             # folded norms the lookup also writes the first partial sums
             if folded:
                 ssa = torch.empty(c.hidden_size // 16, T, dtype=torch.float32,
                                   device=self.device)
-            residual = kernels.embed_rows(input_ids, self.embed, sumsq_out=ssa)
+            residual = kernels.embed_rows(input_ids, self.embed, sumsq_out=ssa, keys=ids_keys)
         else:
             residual = F.embedding(input_ids.reshape(-1), self.embed)
         # residual: owned, updated in place below
@@ -260,6 +283,12 @@ class CausalLM:
                     T, c.vocab_size, c.hidden_size, ssa.shape[0]):
                 # the final norm folded into the lm_head (causal_lm.py:643-645):
                 # the residual rows and their partial sums go straight in
+                if argmax_keys_out is not None:
+                    if argmax_logits is not None:
+                        kernels.lm_head_fold(residual, self.lm_head_g, ssa, eps,
+                                             out=argmax_logits)
+                    return kernels.lm_head_fold(residual, self.lm_head_g, ssa, eps,
+                                                keys_out=argmax_keys_out)
                 if argmax_out is not None:
                     if argmax_logits is not None:
                         kernels.lm_head_fold(residual, self.lm_head_g, ssa, eps,

@@ -237,3 +237,19 @@ def test_lm_head_fold_shape_rule_and_argument_checks(lib):
     rc = lib.nsg_lm_head_fold_argmax(16, 896, 16, 896, 161, 1000, 896, 16, 56, 896, 1e-6, None,
                                      0, None, 1, None)
     assert rc == 1 and "M 161" in lib.nsg_last_error().decode()
+
+
+def test_argmax_key_consumers_check_arguments(lib):
+    """The keyed entry points refuse missing keys before any GPU work."""
+    rc = lib.nsg_embed_rows_keys(8, 1, 0, 4, 1, 0, None, 16, 16, 896, 1000, 896, 16, 896, None,
+                                 None)
+    assert rc == 1 and "keys" in lib.nsg_last_error().decode()
+    rc = lib.nsg_embed_rows_keys(8, 1, 0, 4, 1, 1, 8, 16, 16, 896, 1000, 896, 16, 896, None,
+                                 None)   # key_j outside [0, per_batch)
+    assert rc == 1 and "key_j" in lib.nsg_last_error().decode()
+    rc = lib.nsg_spec_accept_greedy_keys(8, 0, None, 8, 4, 1, 2, 4, 1000, None, None, None, 16,
+                                         8, 8, None, None, None)
+    assert rc == 1 and "key_cols" in lib.nsg_last_error().decode()
+    rc = lib.nsg_lm_head_fold_keys(16, 896, 16, 896, 32, 1000, 896, 16, 56, 896, 1e-6, 16,
+                                   1 << 20, None, None)
+    assert rc == 1 and "key_cols" in lib.nsg_last_error().decode()

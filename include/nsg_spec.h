@@ -545,7 +545,7 @@ int32_t nsg_linear_argmax(const void* x, int64_t ldx, const void* w, int64_t ldw
  * N % 4 == 0, K % 64 == 0, K >= 192, bf16 weights, x / w rows and sumsq_in
  * 16-byte aligned; nsg_lm_head_fold_supported(M, N, K, sumsq_parts) tells
  * whether a shape fits (M * sumsq_parts a multiple of 4, the partials within
- * one LDS ring slot: sumsq_parts <= 56 at 160 rows), else the calls return
+ * one LDS ring slot, at most 64 partials: sumsq_parts <= 56 at 160 rows), else the calls return
  * NSG_ERR_UNSUPPORTED.
  * nsg_lm_head_fold: the logits, y (M x N, ldy elements apart, 8-byte aligned
  * rows); nsg_lm_head_fold_argmax: the greedy token of each row, as

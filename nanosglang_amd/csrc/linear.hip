@@ -839,6 +839,11 @@ int32_t apply_fold(LinParams& p, const NormFold* nf, int32_t N, bool consumer_ok
 // for rows shorter than 2048 (151,936 x 896: 45 against 53 - 59 us at 1 - 32
 // rows), above 32 rows for longer ones (128,256 x 4096: there this kernel's
 // eight-tile shapes stream faster up to 32 rows, 177 against 198 us).
+// gate/up + SwiGLU (bf16 weights) from this many rows on: lm_head.hip's ring
+// kernel (80-row x 48-column workgroups, W once per XCD) instead of the
+// weight-streaming kernel's 32-row groups.
+constexpr int kRingSwigluMinRows = 33;
+
 bool head_route(const LinParams& p) {
   return p.w && !p.bias && p.w_rows == p.N && !p.sumsq_in && !p.residual && p.N >= kWideN &&
          (p.K < kLongRow || p.M > 32) && p.M <= kHeadMaxRows && p.K % kHeadStep == 0 &&
@@ -888,6 +893,12 @@ int32_t linear_impl(const void* x, int64_t ldx, const void* w, const void* w8, i
   if (int32_t rc = apply_fold(p, nf, N, epilogue == NSG_LINEAR_SILU_MUL, epilogue == NSG_LINEAR_BIAS))
     return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (epilogue == NSG_LINEAR_SILU_MUL && p.w && M >= kRingSwigluMinRows &&
+      ring_swiglu_fits(M, N, K, p.sumsq_in ? p.sumsq_parts : 0)) {
+    const GuParams gp{p.x, p.w, p.y, ldx, ldw, ldy, M, N, K,
+                      p.sumsq_in, p.sumsq_parts, p.norm_dim, p.norm_eps};
+    return launch_ring_swiglu(gp, s);
+  }
   if (head_route(p)) {
     const HeadParams hp{p.x, p.w, p.y, p.ldx, p.ldw, p.ldy, M, N, K};
     int key_cols = 0;

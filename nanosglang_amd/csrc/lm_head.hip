@@ -49,6 +49,7 @@ constexpr int kNT = 2;                     // 16-column W tiles per wave
 constexpr int kCols = kWaves * kNT * 16;   // output columns per workgroup tile
 constexpr int kRowBytes = kHeadStep * 2;   // one row's bytes per step
 constexpr int kLdsMax = 160 * 1024;
+constexpr int kHeadMaxParts = 64;  // folded norm: partial sums per row
 constexpr int kMaxStages = 8;
 
 template <int MT>
@@ -203,9 +204,14 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
     float* scale = reinterpret_cast<float*>(ring + kStages * SB - 1024);
     const int t = threadIdx.x;
     if (t < MT * 16) {
+      // every read in flight at once, then the sum in order c = 0, 1, ..
+      float v[kHeadMaxParts];
+      const int tr = min(t, p.M - 1);
+#pragma unroll
+      for (int c = 0; c < kHeadMaxParts; ++c) v[c] = part[min(c, p.parts - 1) * p.M + tr];
       float sq = 0.f;
-      if (t < p.M)
-        for (int c = 0; c < p.parts; ++c) sq += part[c * p.M + t];
+#pragma unroll
+      for (int c = 0; c < kHeadMaxParts; ++c) sq += c < p.parts ? v[c] : 0.f;
       scale[t] = t < p.M ? 1.f / sqrtf(sq / (float)p.norm_dim + p.eps) : 0.f;
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -313,6 +319,232 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
   }
 }
 
+// ---- gate/up + SwiGLU on the same ring (GuParams) ----
+// At 160 rows the weight-streaming linear kernel (linear.hip) takes 32-row
+// groups, so a CU holds three workgroups and pulls about 510 KB through its
+// L1 per call; one CU streams at most a few tens of GB/s (the bytes a ring
+// or a register pipeline keeps in flight over the memory latency), so that
+// traffic, not HBM, sets the time.  Here a workgroup takes 80 rows and 48
+// output columns (96 W rows): x once per workgroup, W once per XCD (the two
+// row groups of a column tile sit on one XCD), about 315 KB per CU.  Three
+// waves, one 16-column gate tile and its up tile each, so the SwiGLU pairs
+// sit in one lane; x and W reach LDS by DMA, as in the lm_head kernel.
+constexpr int kGuWaves = 3;
+constexpr int kGuCols = kGuWaves * 16;   // output columns per workgroup
+constexpr int kGuWRows = kGuWaves * 32;  // their gate and up rows of W
+constexpr int kGuMaxParts = 64;          // folded norm: partial sums per row
+
+template <int MT>
+constexpr int gu_stage_bytes() {
+  return (MT * 16 + kGuWRows) * kRowBytes;
+}
+template <int MT>
+constexpr int gu_stages() {
+  return kLdsMax / gu_stage_bytes<MT>() < kMaxStages ? kLdsMax / gu_stage_bytes<MT>() : kMaxStages;
+}
+
+// 4-byte LDS DMA: lane l lands at lds + 4 l.
+__device__ __forceinline__ void dma4(uint32_t lds, const void* src) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+               :
+               : "s"(lds), "v"(src)
+               : "memory", "m0");
+}
+
+// bf16(silu(g)) for a bf16 value g: F.silu on a bf16 tensor (fp32 math,
+// one rounding), the same expression as linear.hip's SwiGLU epilogue.
+__device__ __forceinline__ float silu_round(float g) {
+  return bf16_bits_to_float(float_to_bf16_bits(g / (1.f + __expf(-g))));
+}
+
+template <int MT, bool FOLD>
+__global__ __launch_bounds__(kGuWaves * 64) void ring_swiglu_kernel(GuParams p, int row_groups,
+                                                                     int col_tiles) {
+  constexpr int R = MT * 16;  // rows per workgroup
+  constexpr int kXAll = 2 * MT;
+  constexpr int kX = (kXAll + kGuWaves - 1) / kGuWaves;
+  constexpr int kW = 4;  // the wave's 32 W rows: 4 copies of 8 rows
+  constexpr int NI = kX + kW;
+  constexpr int SB = gu_stage_bytes<MT>();
+  constexpr int kStages = gu_stages<MT>();
+  static_assert(kStages >= 3 && (kStages - 1) * NI <= 63, "vmcnt counts to 63");
+  static_assert(kGuMaxParts * R * 4 + R * 4 <= SB, "the partials and row scales fit one slot");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[kStages * SB];
+
+  // workgroup -> (column tile, row group); the row groups of a column tile
+  // on one XCD (workgroups go round-robin over the 8 XCDs)
+  const int xcd = blockIdx.x & 7, slot_id = blockIdx.x >> 3;
+  const int tile = xcd + 8 * (slot_id / row_groups);
+  if (tile >= col_tiles) return;  // workgroup-uniform, before any barrier
+  const int m0 = (slot_id % row_groups) * R;
+  const int Mg = min(R, p.M - m0);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nst = p.K / kHeadStep;
+  const uint32_t ring_lds = lds_addr(ring);
+
+  // DMA sources (the lm_head kernel's layout and swizzle): x copy i of a wave
+  // fills rows 8 copy .. + 8 of the x region; rows past the group repeat its
+  // last row.  W: the wave's region holds its gate tile (rows 0-15) and up
+  // tile (16-31); columns past N repeat column N - 1.
+  const bf16* xsrc[kX];
+  uint32_t x_lds[kX];
+#pragma unroll
+  for (int i = 0; i < kX; ++i) {
+    const int copy = min(wave * kX + i, kXAll - 1);
+    x_lds[i] = ring_lds + copy * 1024;
+    const int sl = copy * 64 + lane;
+    const int r = sl >> 3;
+    const int seg = (sl & 7) ^ ((r >> 1) & 7);
+    xsrc[i] = p.x + (int64_t)(m0 + min(r, Mg - 1)) * p.ldx + seg * 8;
+  }
+  const int c0 = tile * kGuCols + wave * 16;  // the wave's first output column
+  const bf16* wsrc[kW];
+#pragma unroll
+  for (int i = 0; i < kW; ++i) {
+    const int sl = i * 64 + lane;
+    const int wr = sl >> 3;
+    const int seg = (sl & 7) ^ ((wr >> 1) & 7);
+    const int row = (wr < 16 ? 0 : p.N) + min(c0 + (wr & 15), p.N - 1);
+    wsrc[i] = p.w + (int64_t)row * p.ldw + seg * 8;
+  }
+  const uint32_t w_lds = ring_lds + R * kRowBytes + wave * 32 * kRowBytes;
+
+  int issued = 0, i_slot = 0;
+  auto issue = [&]() {
+    const uint32_t sb = (uint32_t)i_slot * SB;
+    i_slot = i_slot + 1 == kStages ? 0 : i_slot + 1;
+    const int64_t k0 = (int64_t)issued * kHeadStep;
+#pragma unroll
+    for (int i = 0; i < kX; ++i) dma16(x_lds[i] + sb, xsrc[i] + k0);
+#pragma unroll
+    for (int i = 0; i < kW; ++i) dma16_nt(w_lds + sb + i * 1024, wsrc[i] + k0);
+    ++issued;
+  };
+
+  const int r16 = lane & 15;
+  uint32_t frag_off[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) frag_off[h] = r16 * kRowBytes + 16 * ((4 * h + (lane >> 4)) ^ (r16 >> 1));
+
+  floatx4 acc[2][MT];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  // folded norm: the group's partial sums, part[c * R + r], by LDS DMA into
+  // the ring's last slot (first filled by the main loop, after its first
+  // barrier), issued before the ring's first copies: waiting for them leaves
+  // those in flight.  Thread t < R adds row t's partials (all reads in flight
+  // at once, then the sum in order c = 0, 1, ..) and leaves the row scale
+  // behind the partials, from where each lane takes its rows' scales.
+  const uint32_t part_lds = ring_lds + (kStages - 1) * SB;
+  if constexpr (FOLD) {
+    if ((p.M & 3) == 0 && (Mg & 3) == 0) {
+      // 16 bytes (4 rows of one partial) per lane: rows m0 .. m0 + Mg of
+      // partial c are contiguous and 16-byte aligned
+      const int n16 = p.parts * (R / 4);
+      for (int i = wave; i * 64 < n16; i += kGuWaves) {
+        const int u = i * 64 + lane;
+        const int c = u / (R / 4);
+        const int q = min(u - c * (R / 4), Mg / 4 - 1);
+        dma16(part_lds + i * 1024, p.sumsq + (int64_t)min(c, p.parts - 1) * p.M + m0 + 4 * q);
+      }
+    } else {
+      const int n_el = p.parts * R;
+      for (int i = wave; i * 64 < n_el; i += kGuWaves) {
+        const int e = i * 64 + lane;
+        const int c = e / R;
+        dma4(part_lds + i * 256,
+             p.sumsq + (int64_t)min(c, p.parts - 1) * p.M + m0 + min(e - c * R, Mg - 1));
+      }
+    }
+  }
+  for (int g = 0; g < kStages - 1 && g < nst; ++g) issue();
+
+  float rs[FOLD ? MT : 1];
+  if constexpr (FOLD) {
+    wait_steps<NI, kStages - 1>(issued);  // this wave's partial copies have landed
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // ... and every wave's
+    asm volatile("" ::: "memory");
+    const float* part = reinterpret_cast<const float*>(ring + (kStages - 1) * SB);
+    float* scale = reinterpret_cast<float*>(ring + (kStages - 1) * SB + kGuMaxParts * R * 4);
+    const int t = threadIdx.x;
+    if (t < R) {
+      float v[kGuMaxParts];
+#pragma unroll
+      for (int c = 0; c < kGuMaxParts; ++c) v[c] = part[min(c, p.parts - 1) * R + t];
+      float sq = 0.f;
+#pragma unroll
+      for (int c = 0; c < kGuMaxParts; ++c) sq += c < p.parts ? v[c] : 0.f;
+      scale[t] = t < Mg ? 1.f / sqrtf(sq / (float)p.norm_dim + p.eps) : 0.f;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) rs[mt] = scale[mt * 16 + r16];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // before the slot is refilled
+  }
+
+  int c_slot = 0;
+  for (int g = 0; g < nst; ++g) {
+    wait_steps<NI, kStages - 2>(issued - 1 - g);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (issued < nst) issue();
+    const uint8_t* st = ring + c_slot * SB;
+    c_slot = c_slot + 1 == kStages ? 0 : c_slot + 1;
+    const uint8_t* ws = st + R * kRowBytes + wave * 32 * kRowBytes;
+    bf16x8 wf[2][2], xf[2][MT];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+        wf[h][nt] = *reinterpret_cast<const bf16x8*>(ws + nt * 16 * kRowBytes + frag_off[h]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        xf[h][mt] = *reinterpret_cast<const bf16x8*>(st + mt * 16 * kRowBytes + frag_off[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[h][nt], xf[h][mt], acc[nt][mt],
+                                                                0, 0, 0);
+  }
+
+  // lane l of (nt, mt) holds row 16 mt + l % 16, columns c0 + 4 (l / 16) + i
+  // of the gate (nt 0) and up (nt 1) products
+  const int n = c0 + 4 * (lane >> 4);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + r16;
+    if (m < Mg && n < p.N) {
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float gs = acc[0][mt][i], us = acc[1][mt][i];
+        if constexpr (FOLD) {
+          gs *= rs[mt];
+          us *= rs[mt];
+        }
+        const float g = bf16_bits_to_float(float_to_bf16_bits(gs));
+        const float u = bf16_bits_to_float(float_to_bf16_bits(us));
+        v[i] = silu_round(g) * u;
+      }
+      bf16* y = p.y + (int64_t)(m0 + m) * p.ldy + n;
+      *reinterpret_cast<uint2*>(y) = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    }
+  }
+}
+
 int device_cus() {
   static int cus[64] = {};
   int dev = 0;
@@ -356,7 +588,8 @@ bool fold_fits_mt(int M, int parts) {
 }  // namespace
 
 bool lm_head_fold_fits(int M, int parts) {
-  if (M < kHeadMinRows || M > kHeadMaxRows || parts < 1 || ((int64_t)M * parts) % 4 != 0)
+  if (M < kHeadMinRows || M > kHeadMaxRows || parts < 1 || parts > kHeadMaxParts ||
+      ((int64_t)M * parts) % 4 != 0)
     return false;
   const int mt = (M + 15) / 16;
   if (mt <= 2) return fold_fits_mt<2>(M, parts);
@@ -364,6 +597,37 @@ bool lm_head_fold_fits(int M, int parts) {
   if (mt <= 6) return fold_fits_mt<6>(M, parts);
   if (mt <= 8) return fold_fits_mt<8>(M, parts);
   return fold_fits_mt<10>(M, parts);
+}
+
+bool ring_swiglu_fits(int M, int N, int K, int parts) {
+  return M >= 1 && M <= kHeadMaxRows && N >= 4 && N % 4 == 0 && K % kHeadStep == 0 &&
+         K >= 3 * kHeadStep && parts <= kGuMaxParts;
+}
+
+namespace {
+template <int MT>
+int32_t launch_gu_mt(const GuParams& p, hipStream_t s) {
+  const int row_groups = (p.M + MT * 16 - 1) / (MT * 16);
+  const int col_tiles = (p.N + kGuCols - 1) / kGuCols;
+  const int grid = 8 * ((col_tiles + 7) / 8) * row_groups;
+  if (p.sumsq)
+    hipLaunchKernelGGL((ring_swiglu_kernel<MT, true>), dim3(grid), dim3(kGuWaves * 64), 0, s, p,
+                       row_groups, col_tiles);
+  else
+    hipLaunchKernelGGL((ring_swiglu_kernel<MT, false>), dim3(grid), dim3(kGuWaves * 64), 0, s, p,
+                       row_groups, col_tiles);
+  return launch_status("ring_swiglu_kernel");
+}
+}  // namespace
+
+// Rows per workgroup: two row groups above 32 rows (16-row tiles: 160 rows
+// as 2 x 80, 128 as 2 x 64, 96 as 2 x 48, 64 as 2 x 32), one group up to 32.
+int32_t launch_ring_swiglu(const GuParams& p, hipStream_t s) {
+  const int mt = p.M <= 32 ? 2 : std::max(2, ((p.M + 1) / 2 + 15) / 16);
+  if (mt <= 2) return launch_gu_mt<2>(p, s);
+  if (mt <= 3) return launch_gu_mt<3>(p, s);
+  if (mt <= 4) return launch_gu_mt<4>(p, s);
+  return launch_gu_mt<5>(p, s);
 }
 
 int32_t launch_lm_head(const HeadParams& p, bool argmax, hipStream_t s, int* key_cols) {

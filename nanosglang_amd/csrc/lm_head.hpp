@@ -44,4 +44,28 @@ int32_t launch_lm_head(const HeadParams& p, bool argmax, hipStream_t s, int* key
 // scales).
 bool lm_head_fold_fits(int M, int parts);
 
+// gate/up projection + SwiGLU (the MLP's first half, causal_lm.py:481-482)
+// at verify row counts on the same LDS ring: y[m, n] = bf16(silu(bf16(g)) *
+// bf16(u)) with g = x_m . W[n], u = x_m . W[N + n] (W holds the gate rows,
+// then the up rows), n < N; with sumsq set, both scaled by the folded norm's
+// row scale first (as HeadParams).  A workgroup takes 48 output columns
+// (three waves, one 16-column gate tile and its up tile each) and a group of
+// up to 80 rows.
+struct GuParams {
+  const bf16* x;
+  const bf16* w;
+  bf16* y;
+  int64_t ldx, ldw, ldy;
+  int M, N, K;
+  const float* sumsq;
+  int parts;
+  int norm_dim;
+  float eps;
+};
+
+// Shape rule: 1 <= M <= kHeadMaxRows, K % kHeadStep == 0, K >= 3 * kHeadStep,
+// N % 4 == 0, sumsq_parts <= 64 when folded.
+bool ring_swiglu_fits(int M, int N, int K, int parts);
+int32_t launch_ring_swiglu(const GuParams& p, hipStream_t s);
+
 }  // namespace nsg

@@ -68,7 +68,7 @@ def test_producer_adds_residual_and_writes_partials(M, N, K):
     assert torch.allclose(ss, _partials(res), rtol=1e-5, atol=1e-6)
 
 
-@pytest.mark.parametrize("M", [1, 16, 33, 96, 160])
+@pytest.mark.parametrize("M", [1, 16, 33, 96, 120, 150, 160])
 def test_consumer_swiglu_scales_rows(M):
     from nanosglang_amd import kernels
     H, I = 896, 4864
@@ -100,7 +100,7 @@ def _power_of_two_rows(M, K, seed):
     return (s * sign).bfloat16().cuda(), sign.bfloat16().cuda()
 
 
-@pytest.mark.parametrize("M", [1, 16, 33, 96, 160])
+@pytest.mark.parametrize("M", [1, 16, 33, 96, 120, 150, 160])
 def test_consumer_swiglu_exact_rows(M):
     from nanosglang_amd import kernels
     H, I = 896, 4864

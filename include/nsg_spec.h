@@ -43,7 +43,7 @@ enum {
 const char* nsg_last_error(void);
 /* ABI version of this header (NSG_ABI_VERSION). */
 int32_t nsg_abi_version(void);
-#define NSG_ABI_VERSION 20
+#define NSG_ABI_VERSION 21
 
 /* ------------------------------------------------------------------------
  * Verify attention: ragged multi-query attention over the paged KV cache
@@ -635,6 +635,17 @@ int32_t nsg_host_gate_alloc(int32_t** flag);
 int32_t nsg_host_gate_free(int32_t* flag);
 int32_t nsg_host_gate_wait(int32_t* flag, int32_t* err, int64_t timeout_us,
                            const void* src_host, void* dst, int64_t nbytes, nsg_stream_t stream);
+
+/* nsg_host_gate_wait copying only n_segs (<= 8) byte ranges [seg_offsets[i],
+ * + seg_bytes[i]) of the nbytes-byte staging buffer (16-byte multiples), in
+ * place: a step's staging holds fixed-capacity arrays (page ids per attention
+ * call) of which a step uses a prefix, and the GPU pulls host memory at about
+ * 10 KB per microsecond.  No reference counterpart (the reference's loop is
+ * synchronous); it serves the same pipelined loop. */
+int32_t nsg_host_gate_wait_segments(int32_t* flag, int32_t* err, int64_t timeout_us,
+                                    const void* src_host, void* dst, int64_t nbytes,
+                                    const int64_t* seg_offsets, const int64_t* seg_bytes,
+                                    int32_t n_segs, nsg_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -13,7 +13,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libnsg_spec.so")
 
 NSG_ATTN_WORK_INTS = 8
-ABI_VERSION = 20
+ABI_VERSION = 21
 
 i32, i64, u32, u64, f32 = C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_float
 vp = C.c_void_p
@@ -99,6 +99,7 @@ SIGNATURES = {
     "nsg_silu_mul": (i32, [vp, vp, i64, i32, vp]),
     "nsg_philox_uniform": (i32, [u64, u32, u64, i64, vp, vp]),
     "nsg_export_step": (i32, [vp, vp, i32, i32, vp, vp, vp, vp]),
+    "nsg_host_gate_wait_segments": (i32, [vp, vp, i64, vp, vp, i64, vp, vp, i32, vp]),
     "nsg_host_gate_alloc": (i32, [C.POINTER(C.c_void_p)]),
     "nsg_host_gate_free": (i32, [vp]),
     "nsg_host_gate_wait": (i32, [vp, vp, i64, vp, vp, i64, vp]),

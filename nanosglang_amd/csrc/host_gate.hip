@@ -61,6 +61,60 @@ __global__ __launch_bounds__(kGateThreads) void host_gate_kernel(int32_t* flag, 
   if (threadIdx.x == 0) __hip_atomic_store(flag, 0, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+// The same with the copy limited to up to kGateMaxSegs byte ranges of the
+// staging buffer (the rest of the buffer is capacity a step does not use:
+// the pull over PCIe costs about 1 us per 10 KB).  Segment i is
+// [off[i], off[i] + len[i]), 16-byte aligned; units are numbered across the
+// segments in order.
+constexpr int kGateMaxSegs = 8;
+struct GateSegs {
+  int64_t off[kGateMaxSegs];   // in 16-byte units
+  int64_t len[kGateMaxSegs];   // in 16-byte units
+  int32_t n;
+};
+
+__global__ __launch_bounds__(kGateThreads) void host_gate_segs_kernel(int32_t* flag, int32_t* err,
+                                                                      uint64_t timeout_ticks,
+                                                                      const uint4* src, uint4* dst,
+                                                                      GateSegs segs) {
+  if (threadIdx.x == 0) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();  // 100 MHz
+    for (;;) {
+      if (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) != 0) break;
+      if (__builtin_amdgcn_s_memrealtime() - t0 > timeout_ticks) {
+        __hip_atomic_fetch_or(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(4);
+    }
+  }
+  __syncthreads();
+  (void)__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+  int64_t total = 0;
+  for (int i = 0; i < segs.n; ++i) total += segs.len[i];
+  // unit u -> (segment, offset): segments in order, a short scan per unit
+  auto addr = [&](int64_t u) -> int64_t {
+    int i = 0;
+    while (u >= segs.len[i]) u -= segs.len[i++];
+    return segs.off[i] + u;
+  };
+  for (int64_t u0 = threadIdx.x; u0 < total; u0 += kGateThreads * kGateUnroll) {
+    uint4 v[kGateUnroll];
+    int64_t a[kGateUnroll];
+#pragma unroll
+    for (int k = 0; k < kGateUnroll; ++k) {
+      const int64_t u = u0 + k * kGateThreads;
+      a[k] = u < total ? addr(u) : 0;
+      if (u < total) v[k] = src[a[k]];
+    }
+#pragma unroll
+    for (int k = 0; k < kGateUnroll; ++k)
+      if (u0 + k * kGateThreads < total) dst[a[k]] = v[k];
+  }
+  __syncthreads();  // every thread has read the flag before it is reset
+  if (threadIdx.x == 0) __hip_atomic_store(flag, 0, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // The step's results to pinned host memory, by a kernel at the end of the
 // step's graph (two copy commands after it cost about 4 us each), then the
 // done word: the host polls it instead of waiting on an event.
@@ -80,6 +134,37 @@ __global__ __launch_bounds__(256) void export_kernel(const int32_t* n, const int
 }  // namespace nsg
 
 using namespace nsg;
+
+extern "C" int32_t nsg_host_gate_wait_segments(int32_t* flag, int32_t* err, int64_t timeout_us,
+                                               const void* src_host, void* dst, int64_t nbytes,
+                                               const int64_t* seg_offsets,
+                                               const int64_t* seg_bytes, int32_t n_segs,
+                                               nsg_stream_t stream) {
+  NSG_CHECK_ARG(flag != nullptr && err != nullptr, "flag and err must be set");
+  NSG_CHECK_ARG(timeout_us > 0 && timeout_us <= 60000000, "timeout_us %lld outside (0, 60 s]",
+                (long long)timeout_us);
+  NSG_CHECK_ARG(n_segs >= 0 && n_segs <= kGateMaxSegs, "n_segs %d outside [0, %d]", n_segs,
+                kGateMaxSegs);
+  NSG_CHECK_ARG(n_segs == 0 || (seg_offsets && seg_bytes && src_host && dst &&
+                                (reinterpret_cast<uintptr_t>(src_host) |
+                                 reinterpret_cast<uintptr_t>(dst)) % 16 == 0),
+                "segments need offsets, sizes and 16-byte aligned src_host and dst");
+  GateSegs g{};
+  g.n = n_segs;
+  for (int i = 0; i < n_segs; ++i) {
+    NSG_CHECK_ARG(seg_offsets[i] >= 0 && seg_bytes[i] >= 0 && seg_offsets[i] % 16 == 0 &&
+                      seg_bytes[i] % 16 == 0 && seg_offsets[i] + seg_bytes[i] <= nbytes,
+                  "segment %d: offset %lld and size %lld must be non-negative multiples of 16 "
+                  "within the %lld-byte buffers", i, (long long)seg_offsets[i],
+                  (long long)seg_bytes[i], (long long)nbytes);
+    g.off[i] = seg_offsets[i] / 16;
+    g.len[i] = seg_bytes[i] / 16;
+  }
+  hipLaunchKernelGGL(host_gate_segs_kernel, dim3(1), dim3(kGateThreads), 0,
+                     static_cast<hipStream_t>(stream), flag, err, (uint64_t)timeout_us * 100u,
+                     static_cast<const uint4*>(src_host), static_cast<uint4*>(dst), g);
+  return launch_status("host_gate_segs_kernel");
+}
 
 extern "C" int32_t nsg_export_step(const int32_t* n_emitted, const int64_t* emitted,
                                    int32_t rows, int32_t cols, int32_t* n_host,

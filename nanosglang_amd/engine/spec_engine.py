@@ -94,6 +94,7 @@ class _Arena:
             offs[name] = (o, dt, n, es)
             o += n * es
         self.nbytes = max(256, (o + 255) // 256 * 256)
+        self.off = {name: v[0] for name, v in offs.items()}   # byte offset of each array
         self.host = torch.zeros(self.nbytes, dtype=torch.uint8, pin_memory=True)
         self.dev = torch.zeros(self.nbytes, dtype=torch.uint8, device=device)
         self.h, self.d = {}, {}
@@ -569,7 +570,21 @@ class SpecEngine:
                 raise RuntimeError(f"speculative step (graph of {g.bs} rows) did not finish "
                                    f"within {self.STEP_TIMEOUT_S} s")
 
-    def _launch(self, g: _StepGraph, gated: bool) -> None:
+    def _gate_segments(self, g: _StepGraph, pages: int):
+        """The byte ranges of g's staging a step uses when its attention calls
+        hold at most ``pages`` page ids each: every array before the page
+        ids (the ids are the arena's last array) and the first ``pages`` ids of
+        each call's block."""
+        A, sx = g.arena, g.strides[1]
+        base = A.off["idx"]
+        n = min(sx, pages) * 4
+        n = (n + 15) // 16 * 16
+        offs = [0] + [base + a * sx * 4 for a in range(self.k + 1)]
+        lens = [base] + [min(n, A.nbytes - o) for o in offs[1:]]
+        return ((kernels.C.c_int64 * len(offs))(*offs),
+                (kernels.C.c_int64 * len(lens))(*lens), len(offs))
+
+    def _launch(self, g: _StepGraph, gated: bool, pages: int | None = None) -> None:
         """Queues one speculative step of graph g on the current stream: the
         host gate (gated: the step waits until _raise_gate), the upload of
         its staging buffer, the Philox uniforms (sampling), the replay, whose
@@ -583,10 +598,17 @@ class SpecEngine:
             g.done.value = 0
         if gated:    # the gate also uploads the staging buffer once released
             A = g.arena
-            kernels.check(lib.nsg_host_gate_wait(self._gate(), self._gate_err.data_ptr(),
-                                                 self.GATE_TIMEOUT_US, A.host.data_ptr(),
-                                                 A.dev.data_ptr(), A.nbytes, sp),
-                          "nsg_host_gate_wait")
+            if pages is None:
+                kernels.check(lib.nsg_host_gate_wait(self._gate(), self._gate_err.data_ptr(),
+                                                     self.GATE_TIMEOUT_US, A.host.data_ptr(),
+                                                     A.dev.data_ptr(), A.nbytes, sp),
+                              "nsg_host_gate_wait")
+            else:    # only the arrays' used prefixes: the pull over PCIe is slow
+                offs, lens, n = self._gate_segments(g, pages)
+                kernels.check(lib.nsg_host_gate_wait_segments(
+                    self._gate(), self._gate_err.data_ptr(), self.GATE_TIMEOUT_US,
+                    A.host.data_ptr(), A.dev.data_ptr(), A.nbytes, offs, lens, n, sp),
+                    "nsg_host_gate_wait_segments")
         else:
             g.arena.upload()
         if not self.greedy:
@@ -797,14 +819,23 @@ class SpecEngine:
                         self.kv.reserve(r.table, r.start + 2 * (k + 1))
                         self._sync_table(r)
                     nxt = self._graph_for(len(cur))
+                    # page ids per attention call of step s + 1: at most every
+                    # page reserved now, plus the padding rows' dummy pages
+                    pages = (sum(len(r.table.block_indices) for r in cur)
+                             + (nxt.bs - len(cur)) * ((k + self.P) // self.P))
                     pending = True
-                    self._launch(nxt, gated=True)
+                    self._launch(nxt, gated=True, pages=pages)
                     # step s + 1's fill, but for step s's results (n_out,
                     # emitted), prepared while step s runs
                     fill_next = self._fill_next_args(nxt, g, cur)
                 self._wait_done(g)
                 if nxt is not None:    # release step s + 1 first, bookkeeping after
                     self._run_fill_next(fill_next)
+                    si = nxt.strides[0]
+                    kvp = nxt.arena.h["kvp"]
+                    if max(int(kvp[a * si + nxt.bs]) for a in range(k + 1)) > pages:
+                        raise RuntimeError("step fill wrote more page ids than the gate "
+                                           f"copies ({pages})")
                     nxt.done.value = 0
                     self._raise_gate()
                     pending = False

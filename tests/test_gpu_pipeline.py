@@ -81,6 +81,40 @@ def test_host_gate_releases_on_flag_and_gives_up_after_timeout():
         _native.check(lib.nsg_host_gate_free(p.value), "nsg_host_gate_free")
 
 
+def test_host_gate_segments_copy_only_their_ranges():
+    """nsg_host_gate_wait_segments: after release, exactly the listed byte
+    ranges of the pinned buffer reach the device buffer (zero-length and
+    adjacent segments included); every other byte keeps its old value."""
+    lib = _native.load()
+    print("case: host gate segments", flush=True)
+    p = C.c_void_p()
+    _native.check(lib.nsg_host_gate_alloc(C.byref(p)), "nsg_host_gate_alloc")
+    flag = C.c_int32.from_address(p.value)
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    n = 200_000
+    src = torch.randint(0, 256, (n,), dtype=torch.uint8).pin_memory()
+    dst = torch.full((n,), 7, dtype=torch.uint8, device="cuda")
+    segs = [(0, 4096), (4096, 0), (4096, 160), (65536, 70_000), (199_984, 16)]
+    offs = (C.c_int64 * len(segs))(*[o for o, _ in segs])
+    lens = (C.c_int64 * len(segs))(*[l for _, l in segs])
+    stream = torch.cuda.current_stream().cuda_stream
+    try:
+        flag.value = 1
+        _native.check(lib.nsg_host_gate_wait_segments(p.value, err.data_ptr(), 2_000_000,
+                                                      src.data_ptr(), dst.data_ptr(), n, offs,
+                                                      lens, len(segs), stream),
+                      "nsg_host_gate_wait_segments")
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0 and flag.value == 0
+        expect = torch.full((n,), 7, dtype=torch.uint8)
+        for o, l in segs:
+            expect[o:o + l] = src[o:o + l]
+        assert torch.equal(dst.cpu(), expect)
+    finally:
+        torch.cuda.synchronize()
+        _native.check(lib.nsg_host_gate_free(p.value), "nsg_host_gate_free")
+
+
 @pytest.mark.parametrize("temperature", [0.0, 0.8])
 def test_pipelined_generate_equals_unpipelined(temperature):
     from nanosglang_amd.engine.spec_engine import SpecEngine

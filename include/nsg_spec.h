@@ -636,16 +636,23 @@ int32_t nsg_host_gate_free(int32_t* flag);
 int32_t nsg_host_gate_wait(int32_t* flag, int32_t* err, int64_t timeout_us,
                            const void* src_host, void* dst, int64_t nbytes, nsg_stream_t stream);
 
-/* nsg_host_gate_wait copying only n_segs (<= 8) byte ranges [seg_offsets[i],
+/* A host gate that copies only n_segs (<= 8) byte ranges [seg_offsets[i],
  * + seg_bytes[i]) of the nbytes-byte staging buffer (16-byte multiples), in
- * place: a step's staging holds fixed-capacity arrays (page ids per attention
- * call) of which a step uses a prefix, and the GPU pulls host memory at about
- * 10 KB per microsecond.  No reference counterpart (the reference's loop is
- * synchronous); it serves the same pipelined loop. */
-int32_t nsg_host_gate_wait_segments(int32_t* flag, int32_t* err, int64_t timeout_us,
-                                    const void* src_host, void* dst, int64_t nbytes,
-                                    const int64_t* seg_offsets, const int64_t* seg_bytes,
-                                    int32_t n_segs, nsg_stream_t stream);
+ * place, with several workgroups: a step's staging holds fixed-capacity
+ * arrays (page ids per attention call) of which a step uses a prefix, and one
+ * workgroup pulls host memory at about 10 KB per microsecond.  The queued
+ * work is held until *flag >= target (target >= 1): the host releases it by
+ * writing target (or more) to the flag word, which this gate never resets,
+ * so the host's targets must grow from call to call (a word used with
+ * nsg_host_gate_wait, which waits for non-zero and resets, must not be
+ * shared with it).  Timeout and error bit as nsg_host_gate_wait.  No
+ * reference counterpart (the reference's loop is synchronous); it serves the
+ * same pipelined loop. */
+int32_t nsg_host_gate_wait_segments(int32_t* flag, int32_t target, int32_t* err,
+                                    int64_t timeout_us, const void* src_host, void* dst,
+                                    int64_t nbytes, const int64_t* seg_offsets,
+                                    const int64_t* seg_bytes, int32_t n_segs,
+                                    nsg_stream_t stream);
 
 #ifdef __cplusplus
 }

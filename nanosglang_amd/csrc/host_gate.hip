@@ -62,25 +62,30 @@ __global__ __launch_bounds__(kGateThreads) void host_gate_kernel(int32_t* flag, 
 }
 
 // The same with the copy limited to up to kGateMaxSegs byte ranges of the
-// staging buffer (the rest of the buffer is capacity a step does not use:
-// the pull over PCIe costs about 1 us per 10 KB).  Segment i is
-// [off[i], off[i] + len[i]), 16-byte aligned; units are numbered across the
-// segments in order.
+// staging buffer (the rest of the buffer is capacity a step does not use),
+// spread over kGateSegGroups workgroups: one workgroup pulls pinned host
+// memory at about 10 KB per microsecond.  Segment i is [off[i], off[i] +
+// len[i]), 16-byte aligned; units are numbered across the segments in order
+// and dealt round-robin to the threads of all workgroups.  Each workgroup
+// waits on its own for *flag >= target: the host raises a gate by writing its
+// target (a count that only grows), so no workgroup resets the word another
+// may not have read yet.
 constexpr int kGateMaxSegs = 8;
+constexpr int kGateSegGroups = 8;
+constexpr int kGateSegThreads = 256;
 struct GateSegs {
   int64_t off[kGateMaxSegs];   // in 16-byte units
   int64_t len[kGateMaxSegs];   // in 16-byte units
   int32_t n;
 };
 
-__global__ __launch_bounds__(kGateThreads) void host_gate_segs_kernel(int32_t* flag, int32_t* err,
-                                                                      uint64_t timeout_ticks,
-                                                                      const uint4* src, uint4* dst,
-                                                                      GateSegs segs) {
+__global__ __launch_bounds__(kGateSegThreads) void host_gate_segs_kernel(
+    int32_t* flag, int32_t target, int32_t* err, uint64_t timeout_ticks, const uint4* src,
+    uint4* dst, GateSegs segs) {
   if (threadIdx.x == 0) {
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();  // 100 MHz
     for (;;) {
-      if (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) != 0) break;
+      if (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) >= target) break;
       if (__builtin_amdgcn_s_memrealtime() - t0 > timeout_ticks) {
         __hip_atomic_fetch_or(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
@@ -98,21 +103,21 @@ __global__ __launch_bounds__(kGateThreads) void host_gate_segs_kernel(int32_t* f
     while (u >= segs.len[i]) u -= segs.len[i++];
     return segs.off[i] + u;
   };
-  for (int64_t u0 = threadIdx.x; u0 < total; u0 += kGateThreads * kGateUnroll) {
+  constexpr int kStride = kGateSegGroups * kGateSegThreads;
+  for (int64_t u0 = (int64_t)blockIdx.x * kGateSegThreads + threadIdx.x; u0 < total;
+       u0 += (int64_t)kStride * kGateUnroll) {
     uint4 v[kGateUnroll];
     int64_t a[kGateUnroll];
 #pragma unroll
     for (int k = 0; k < kGateUnroll; ++k) {
-      const int64_t u = u0 + k * kGateThreads;
+      const int64_t u = u0 + (int64_t)k * kStride;
       a[k] = u < total ? addr(u) : 0;
       if (u < total) v[k] = src[a[k]];
     }
 #pragma unroll
     for (int k = 0; k < kGateUnroll; ++k)
-      if (u0 + k * kGateThreads < total) dst[a[k]] = v[k];
+      if (u0 + (int64_t)k * kStride < total) dst[a[k]] = v[k];
   }
-  __syncthreads();  // every thread has read the flag before it is reset
-  if (threadIdx.x == 0) __hip_atomic_store(flag, 0, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // The step's results to pinned host memory, by a kernel at the end of the
@@ -135,8 +140,9 @@ __global__ __launch_bounds__(256) void export_kernel(const int32_t* n, const int
 
 using namespace nsg;
 
-extern "C" int32_t nsg_host_gate_wait_segments(int32_t* flag, int32_t* err, int64_t timeout_us,
-                                               const void* src_host, void* dst, int64_t nbytes,
+extern "C" int32_t nsg_host_gate_wait_segments(int32_t* flag, int32_t target, int32_t* err,
+                                               int64_t timeout_us, const void* src_host,
+                                               void* dst, int64_t nbytes,
                                                const int64_t* seg_offsets,
                                                const int64_t* seg_bytes, int32_t n_segs,
                                                nsg_stream_t stream) {
@@ -160,9 +166,11 @@ extern "C" int32_t nsg_host_gate_wait_segments(int32_t* flag, int32_t* err, int6
     g.off[i] = seg_offsets[i] / 16;
     g.len[i] = seg_bytes[i] / 16;
   }
-  hipLaunchKernelGGL(host_gate_segs_kernel, dim3(1), dim3(kGateThreads), 0,
-                     static_cast<hipStream_t>(stream), flag, err, (uint64_t)timeout_us * 100u,
-                     static_cast<const uint4*>(src_host), static_cast<uint4*>(dst), g);
+  NSG_CHECK_ARG(target >= 1, "target %d must be positive", target);
+  hipLaunchKernelGGL(host_gate_segs_kernel, dim3(kGateSegGroups), dim3(kGateSegThreads), 0,
+                     static_cast<hipStream_t>(stream), flag, target, err,
+                     (uint64_t)timeout_us * 100u, static_cast<const uint4*>(src_host),
+                     static_cast<uint4*>(dst), g);
   return launch_status("host_gate_segs_kernel");
 }
 

@@ -254,6 +254,7 @@ class SpecEngine:
         # overlap the GPU's work (see _decode_pipelined)
         self.pipeline = pipeline
         self._gate_flag = None          # coherent pinned host word (nsg_host_gate_alloc)
+        self._gate_seq = 0              # the last gated step's release target
         self._gate_err = torch.zeros(1, dtype=torch.int32, device=self.device)
 
     # ---- helpers ----
@@ -552,7 +553,9 @@ class SpecEngine:
         return self._gate_flag
 
     def _raise_gate(self) -> None:
-        kernels.C.c_int32.from_address(self._gate_flag).value = 1
+        """Releases the queued gated step (the flag word counts up to each
+        gated launch's target; it is never reset)."""
+        kernels.C.c_int32.from_address(self._gate_flag).value = self._gate_seq
 
     # a step that has not finished after this long is reported as hung
     STEP_TIMEOUT_S = 60.0
@@ -599,16 +602,16 @@ class SpecEngine:
         if gated:    # the gate also uploads the staging buffer once released
             A = g.arena
             if pages is None:
-                kernels.check(lib.nsg_host_gate_wait(self._gate(), self._gate_err.data_ptr(),
-                                                     self.GATE_TIMEOUT_US, A.host.data_ptr(),
-                                                     A.dev.data_ptr(), A.nbytes, sp),
-                              "nsg_host_gate_wait")
+                offs, lens, n = ((kernels.C.c_int64 * 1)(0), (kernels.C.c_int64 * 1)(A.nbytes),
+                                 1)
             else:    # only the arrays' used prefixes: the pull over PCIe is slow
                 offs, lens, n = self._gate_segments(g, pages)
-                kernels.check(lib.nsg_host_gate_wait_segments(
-                    self._gate(), self._gate_err.data_ptr(), self.GATE_TIMEOUT_US,
-                    A.host.data_ptr(), A.dev.data_ptr(), A.nbytes, offs, lens, n, sp),
-                    "nsg_host_gate_wait_segments")
+            flag = self._gate()
+            self._gate_seq += 1
+            kernels.check(lib.nsg_host_gate_wait_segments(
+                flag, self._gate_seq, self._gate_err.data_ptr(), self.GATE_TIMEOUT_US,
+                A.host.data_ptr(), A.dev.data_ptr(), A.nbytes, offs, lens, n, sp),
+                "nsg_host_gate_wait_segments")
         else:
             g.arena.upload()
         if not self.greedy:
@@ -831,14 +834,14 @@ class SpecEngine:
                 self._wait_done(g)
                 if nxt is not None:    # release step s + 1 first, bookkeeping after
                     self._run_fill_next(fill_next)
+                    nxt.done.value = 0
+                    self._raise_gate()
+                    pending = False
                     si = nxt.strides[0]
                     kvp = nxt.arena.h["kvp"]
                     if max(int(kvp[a * si + nxt.bs]) for a in range(k + 1)) > pages:
                         raise RuntimeError("step fill wrote more page ids than the gate "
-                                           f"copies ({pages})")
-                    nxt.done.value = 0
-                    self._raise_gate()
-                    pending = False
+                                           f"copied ({pages}): that step ran on stale page ids")
                 B = len(cur)
                 n_h = g.n_h.numpy()[:B].copy()
                 em_h = g.em_h.numpy()[:B].copy()

@@ -259,11 +259,14 @@ def test_host_gate_segments_check_arguments(lib):
     """Segment lists the gate cannot copy are refused before any GPU work."""
     I64 = C.c_int64 * 9
     offs, lens = I64(*([0] * 9)), I64(*([16] * 9))
-    rc = lib.nsg_host_gate_wait_segments(8, 8, 1000, 16, 16, 4096, offs, lens, 9, None)
+    rc = lib.nsg_host_gate_wait_segments(8, 1, 8, 1000, 16, 16, 4096, offs, lens, 9, None)
     assert rc == 1 and "n_segs 9" in lib.nsg_last_error().decode()
     offs2, lens2 = (C.c_int64 * 2)(0, 8), (C.c_int64 * 2)(16, 16)
-    rc = lib.nsg_host_gate_wait_segments(8, 8, 1000, 16, 16, 4096, offs2, lens2, 2, None)
+    rc = lib.nsg_host_gate_wait_segments(8, 1, 8, 1000, 16, 16, 4096, offs2, lens2, 2, None)
     assert rc == 1 and "segment 1" in lib.nsg_last_error().decode()
     offs3, lens3 = (C.c_int64 * 1)(4080,), (C.c_int64 * 1)(32,)
-    rc = lib.nsg_host_gate_wait_segments(8, 8, 1000, 16, 16, 4096, offs3, lens3, 1, None)
+    rc = lib.nsg_host_gate_wait_segments(8, 1, 8, 1000, 16, 16, 4096, offs3, lens3, 1, None)
     assert rc == 1 and "within the 4096-byte" in lib.nsg_last_error().decode()
+    rc = lib.nsg_host_gate_wait_segments(8, 0, 8, 1000, 16, 16, 4096, offs3, (C.c_int64 * 1)(16), 1,
+                                         None)
+    assert rc == 1 and "target 0" in lib.nsg_last_error().decode()

@@ -82,9 +82,11 @@ def test_host_gate_releases_on_flag_and_gives_up_after_timeout():
 
 
 def test_host_gate_segments_copy_only_their_ranges():
-    """nsg_host_gate_wait_segments: after release, exactly the listed byte
-    ranges of the pinned buffer reach the device buffer (zero-length and
-    adjacent segments included); every other byte keeps its old value."""
+    """nsg_host_gate_wait_segments: held until the flag reaches its target
+    (a lower value does not release it), then exactly the listed byte ranges
+    of the pinned buffer reach the device buffer (zero-length and adjacent
+    segments included); every other byte keeps its old value, and the flag
+    is left as the host wrote it."""
     lib = _native.load()
     print("case: host gate segments", flush=True)
     p = C.c_void_p()
@@ -99,13 +101,16 @@ def test_host_gate_segments_copy_only_their_ranges():
     lens = (C.c_int64 * len(segs))(*[l for _, l in segs])
     stream = torch.cuda.current_stream().cuda_stream
     try:
-        flag.value = 1
-        _native.check(lib.nsg_host_gate_wait_segments(p.value, err.data_ptr(), 2_000_000,
+        flag.value = 4
+        _native.check(lib.nsg_host_gate_wait_segments(p.value, 5, err.data_ptr(), 5_000_000,
                                                       src.data_ptr(), dst.data_ptr(), n, offs,
                                                       lens, len(segs), stream),
                       "nsg_host_gate_wait_segments")
+        time.sleep(0.05)
+        assert not torch.cuda.current_stream().query()      # 4 < 5: still held
+        flag.value = 5
         torch.cuda.synchronize()
-        assert int(err.item()) == 0 and flag.value == 0
+        assert int(err.item()) == 0 and flag.value == 5
         expect = torch.full((n,), 7, dtype=torch.uint8)
         for o, l in segs:
             expect[o:o + l] = src[o:o + l]

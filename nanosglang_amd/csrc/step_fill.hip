@@ -188,13 +188,34 @@ int32_t fill_impl(const int32_t* page_table, int64_t page_table_stride, const in
       kvp[j + 1] = (int32_t)nnz;
       last[j] = (int32_t)(L - (np - 1) * P);
     }
+    int32_t* work = o.work + (size_t)a * o.work_stride;
+    const nsg_attn_plan_t& p0 = plans[0];
+    if (a >= 1 && a < k && p0.q_tile_tokens == 1 && p0.max_splits == 1 && p0.num_merge == 0 &&
+        p0.num_work == S && p0.num_groups == S) {
+      // a later draft call: one query token per row, so the plan of draft
+      // call 0 with each row's KV range moved (its work item n is row n, one
+      // KV split): the planner would write exactly this
+      plans[a] = p0;
+      for (int j = 0; j < S; ++j) {
+        const int32_t L = (kvp[j + 1] - kvp[j] - 1) * P + last[j];
+        int32_t* w = work + (size_t)j * NSG_ATTN_WORK_INTS;
+        w[0] = j;
+        w[1] = 1;
+        w[2] = L - 1;
+        w[3] = kvp[j];
+        w[4] = 0;
+        w[5] = L;
+        w[6] = 1;
+        w[7] = 0;
+      }
+      continue;
+    }
     int32_t mw = 0, mm = 0;
     int32_t rc = nsg_attn_fixed_capacity(S, ql, num_qo_heads, num_kv_heads, num_cus, max_kv_len,
                                          &mw, &mm);
     if (rc != NSG_OK) return rc;
     rc = nsg_attn_plan_fixed(qo, kvp, last, S, num_qo_heads, num_kv_heads, head_dim, P,
-                             /*causal=*/1, num_cus, ql, max_kv_len, mw, mm,
-                             o.work + (size_t)a * o.work_stride,
+                             /*causal=*/1, num_cus, ql, max_kv_len, mw, mm, work,
                              o.work_stride / NSG_ATTN_WORK_INTS, plans + a);
     if (rc != NSG_OK) return rc;
   }

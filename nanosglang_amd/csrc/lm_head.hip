@@ -86,6 +86,12 @@ __device__ __forceinline__ void dma16_nt(uint32_t lds, const void* src) {
 
 __device__ __forceinline__ uint64_t key_max(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
+// Row groups of waves in the lm_head kernel: 2 from 96 rows (MT 6), else 1.
+template <int MT>
+constexpr int lm_row_split() {
+  return MT >= 6 ? 2 : 1;
+}
+
 template <int MT, bool ARG, bool FOLD>
 __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
   static_assert(MT % 2 == 0 && MT >= 2 && MT <= kHeadMaxRows / 16, "whole x copies");
@@ -96,6 +102,14 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
   constexpr int kX = (kXAll + kWaves - 1) / kWaves;
   constexpr int kW = 2 * kNT;      // W copies per wave and step (its 32 rows x 8 segments)
   constexpr int NI = kX + kW;      // vector-memory instructions per wave and step
+  // MFMA work of a step: RS row groups x kWaves / RS column groups of waves,
+  // each wave XT x tiles by WT W tiles (from 96 rows two row groups: each
+  // wave reads half of x's fragments and twice the W fragments, 9 instead of
+  // 12 fragment reads per 32-k at 160 rows)
+  constexpr int RS = lm_row_split<MT>();
+  constexpr int XT = MT / RS;
+  constexpr int WT = kNT * RS;
+  constexpr int CG = kWaves / RS;
   constexpr int SB = stage_bytes<MT>();
   constexpr int kStages = ring_stages<MT>();
   static_assert(kStages >= 3 && (kStages - 2) * NI <= 63, "vmcnt counts to 63");
@@ -103,6 +117,7 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rh = wave % RS, cg = wave / RS;  // the wave's row group and column group
   const int nst = p.K / kHeadStep;
   const int tiles = (p.N + kCols - 1) / kCols;
   const int my_tiles = (tiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
@@ -168,18 +183,18 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) frag_off[h] = r16 * kRowBytes + 16 * ((4 * h + (lane >> 4)) ^ (r16 >> 1));
 
-  floatx4 acc[kNT][MT];
+  floatx4 acc[WT][XT];
 #pragma unroll
-  for (int nt = 0; nt < kNT; ++nt)
+  for (int nt = 0; nt < WT; ++nt)
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < XT; ++mt) acc[nt][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
   // argmax: per row, this lane's largest bf16 logit and its column so far
   // (columns come in increasing order, so a strict > keeps the lowest
   // column of equal values; -0 equals +0)
-  float bv[ARG ? MT : 1];
-  int bc[ARG ? MT : 1];
+  float bv[ARG ? XT : 1];
+  int bc[ARG ? XT : 1];
 #pragma unroll
-  for (int mt = 0; mt < (ARG ? MT : 1); ++mt) {
+  for (int mt = 0; mt < (ARG ? XT : 1); ++mt) {
     bv[mt] = 0.f;
     bc[mt] = -1;
   }
@@ -194,7 +209,7 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
   set_w(0);
   for (int g = 0; g < kStages - 1 && g < total; ++g) issue();
 
-  float rs[FOLD ? MT : 1];  // the row scales of this lane's rows 16 mt + lane % 16
+  float rs[FOLD ? XT : 1];  // the row scales of this lane's rows 16 (rh XT + mt) + lane % 16
   if constexpr (FOLD) {
     wait_steps<NI, kStages - 1>(issued);  // this wave's partial copies have landed
     asm volatile("" ::: "memory");
@@ -218,7 +233,7 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) rs[mt] = scale[mt * 16 + r16];
+    for (int mt = 0; mt < XT; ++mt) rs[mt] = scale[(rh * XT + mt) * 16 + r16];
     // read before the main loop's first copies refill the slot
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
@@ -236,36 +251,37 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
       const uint8_t* st = ring + c_slot * SB;
       c_slot = c_slot + 1 == kStages ? 0 : c_slot + 1;
       const uint8_t* xs = st;
-      const uint8_t* ws = st + MT * 16 * kRowBytes + wave * kNT * 16 * kRowBytes;
-      bf16x8 wf[2][kNT], xf[2][MT];
+      const uint8_t* ws = st + MT * 16 * kRowBytes + cg * WT * 16 * kRowBytes;
+      bf16x8 wf[2][WT], xf[2][XT];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int nt = 0; nt < kNT; ++nt)
+        for (int nt = 0; nt < WT; ++nt)
           wf[h][nt] = *reinterpret_cast<const bf16x8*>(ws + nt * 16 * kRowBytes + frag_off[h]);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          xf[h][mt] = *reinterpret_cast<const bf16x8*>(xs + mt * 16 * kRowBytes + frag_off[h]);
+        for (int mt = 0; mt < XT; ++mt)
+          xf[h][mt] = *reinterpret_cast<const bf16x8*>(xs + (rh * XT + mt) * 16 * kRowBytes +
+                                                       frag_off[h]);
       }
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int nt = 0; nt < kNT; ++nt)
+        for (int nt = 0; nt < WT; ++nt)
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
+          for (int mt = 0; mt < XT; ++mt)
             acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[h][nt], xf[h][mt],
                                                                   acc[nt][mt], 0, 0, 0);
     }
 
-    // tile j done.  Lane l of (nt, mt) holds rows m = 16 mt + l % 16,
-    // columns n = c0 + 16 nt + 4 (l / 16) + i.
-    const int c0 = ((int)blockIdx.x + j * (int)gridDim.x) * kCols + wave * kNT * 16;
+    // tile j done.  Lane l of (nt, mt) holds rows m = 16 (rh XT + mt) +
+    // l % 16, columns n = c0 + 16 nt + 4 (l / 16) + i.
+    const int c0 = ((int)blockIdx.x + j * (int)gridDim.x) * kCols + cg * WT * 16;
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) {
+    for (int nt = 0; nt < WT; ++nt) {
       const int n = c0 + nt * 16 + 4 * (lane >> 4);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int m = mt * 16 + r16;
+      for (int mt = 0; mt < XT; ++mt) {
+        const int m = (rh * XT + mt) * 16 + r16;
         const floatx4 v = acc[nt][mt];
         if constexpr (ARG) {
           const bool ok = n < p.N;
@@ -295,12 +311,12 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
   }
 
   if constexpr (ARG) {
-    // the four lanes of a row meet; one stores the row's key for this wave:
-    // keys[m * (4 * grid) + 4 * workgroup + wave]
+    // the four lanes of a row meet; one stores the row's key for this
+    // wave's column group: keys[m * (CG * grid) + CG * workgroup + cg]
     uint64_t* keys = static_cast<uint64_t*>(p.out);
-    const int cols = kWaves * (int)gridDim.x;
+    const int cols = CG * (int)gridDim.x;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
+    for (int mt = 0; mt < XT; ++mt) {
       // key = (order-preserving bits of the bf16 value, ~column): the max
       // key is the largest value at its lowest column; 0 for no column
       uint32_t b = float_to_bf16_bits(bv[mt]);
@@ -313,8 +329,8 @@ __global__ __launch_bounds__(kWaves * 64) void lm_head_kernel(HeadParams p) {
                                (uint32_t)__shfl_xor((int)(uint32_t)k, o, 64);
         k = key_max(k, other);
       }
-      const int m = mt * 16 + r16;
-      if ((lane >> 4) == 0 && m < p.M) keys[(int64_t)m * cols + kWaves * blockIdx.x + wave] = k;
+      const int m = (rh * XT + mt) * 16 + r16;
+      if ((lane >> 4) == 0 && m < p.M) keys[(int64_t)m * cols + CG * blockIdx.x + cg] = k;
     }
   }
 }
@@ -568,7 +584,7 @@ int32_t launch_mt(const HeadParams& p, bool argmax, hipStream_t s, int* key_cols
   const int tiles = (p.N + kCols - 1) / kCols;
   const int per_cu = kLdsMax / (ring_stages<MT>() * stage_bytes<MT>());
   const int grid = std::min(tiles, device_cus() * std::max(per_cu, 1));
-  *key_cols = kWaves * grid;
+  *key_cols = kWaves / lm_row_split<MT>() * grid;
   const dim3 g(grid), b(kWaves * 64);
   if (p.sumsq) {
     if (argmax)

@@ -15,16 +15,18 @@
 //   of an LDS ring (4 to 8 slots, as many as fit) by LDS DMA
 //   (global_load_lds_dwordx4), all but one slot in flight ahead of the math:
 //   W is read from HBM exactly once, x once per tile from L2;
-// * each wave multiplies its two W tiles by all M / 16 x tiles
+// * up to 80 rows each wave multiplies its two W tiles by all M / 16 x tiles
 //   (v_mfma_f32_16x16x32_bf16, A = W, B = x^T): a W fragment feeds MT MFMAs,
-//   an x fragment two;
+//   an x fragment two; from 96 rows the waves split the rows in two and the
+//   columns in two (half the x tiles by four W tiles each: fewer fragment
+//   reads);
 // * an output element's whole K sum stays in one wave, in k order, so the
 //   result does not depend on the grid;
 // * the logits are bf16(acc), one rounding (lm_head has no bias); the argmax
 //   form keeps, per row and lane, the largest bf16 value and its lowest
 //   column over all the wave's tiles, and at the end stores one key per row
-//   and wave (linear.hip's argmax keys: ordered bf16 bits, then the inverted
-//   column).
+//   and column group of waves (linear.hip's argmax keys: ordered bf16 bits,
+//   then the inverted column).
 //
 // The ring's 16-byte segments are XOR-swizzled per row pair (segment s of row
 // r sits at s ^ ((r >> 1) & 7)): the 16 rows of an MFMA fragment read then

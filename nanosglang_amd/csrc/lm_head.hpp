@@ -8,7 +8,8 @@ namespace nsg {
 
 // y = x W^T (no bias) for kHeadMinRows <= M <= kHeadMaxRows rows of x and a
 // wide W (vocabulary rows): logits in bf16 (out: M x N, ldy elements apart)
-// or, with keys, one argmax key per row and wave of the persistent grid
+// or, with keys, one argmax key per row and column group of waves of the
+// persistent grid
 // (out: M x key_cols uint64, the keys of linear.hip's argmax epilogue).
 //
 // With sumsq set, the final RMSNorm is folded in (its weight already folded

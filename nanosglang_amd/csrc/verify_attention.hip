@@ -785,7 +785,13 @@ __global__ __launch_bounds__(RT * KS * 64) void verify_attn_kernel(AttnParams p)
 // A separate launch: partials written by workgroups on other XCDs become
 // visible at the kernel boundary, so no in-kernel cross-workgroup fence (an
 // L2 write-back + invalidate on gfx950) is needed.  Each thread owns one
-// (row, 8-column) piece and streams the splits with independent loads.
+// (row, 8-column) piece (blockIdx.z picks the group's kThreads-piece
+// slice) and issues the loads of up to kMergeBatch splits at once, then
+// combines them in split order: one memory round trip per kMergeBatch
+// splits (a 4-deep rolling loop over a strided item loop took 11 us at the
+// large shape: 64 groups x 8 heads, up to 7 splits).
+constexpr int kMergeBatch = 8;
+
 template <int D, int RT>
 __global__ __launch_bounds__(kThreads) void verify_merge_kernel(AttnParams p, const int* merge,
                                                                int num_merge) {
@@ -801,39 +807,46 @@ __global__ __launch_bounds__(kThreads) void verify_merge_kernel(AttnParams p, co
   if (nsplit < 2) return;  // padding item of a fixed-size (graph-captured) work list
   const int G = p.G;
   const int nrows = qn * G;
-  for (int item = threadIdx.x; item < nrows * CH; item += kThreads) {
-    const int row = item / CH;
-    const int c0 = (item - row * CH) * 8;
-    const float* base = p.partials + ((size_t)wi0 * p.Hkv + h) * ROWS * PSTRIDE +
-                        (size_t)row * PSTRIDE;
-    const size_t sstride = (size_t)p.Hkv * ROWS * PSTRIDE;
-    float M = kMaskVal, lsum = 0.f;
-    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-    for (int sp = 0; sp < nsplit; ++sp) {
-      const float* prow = base + sp * sstride;
-      const floatx4 ml = *reinterpret_cast<const floatx4*>(prow + D);  // m, l, pad, pad
-      const floatx4 a = *reinterpret_cast<const floatx4*>(prow + c0);
-      const floatx4 b = *reinterpret_cast<const floatx4*>(prow + c0 + 4);
-      const float Mn = fmaxf(M, ml[0]);
+  const int item = (int)blockIdx.z * kThreads + (int)threadIdx.x;
+  if (item >= nrows * CH) return;
+  const int row = item / CH;
+  const int c0 = (item - row * CH) * 8;
+  const float* base = p.partials + ((size_t)wi0 * p.Hkv + h) * ROWS * PSTRIDE +
+                      (size_t)row * PSTRIDE;
+  const size_t sstride = (size_t)p.Hkv * ROWS * PSTRIDE;
+  float M = kMaskVal, lsum = 0.f;
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < nsplit; s0 += kMergeBatch) {
+    floatx4 ml[kMergeBatch], a[kMergeBatch], b[kMergeBatch];
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; ++j) {  // splits past nsplit re-read the last one
+      const float* prow = base + min(s0 + j, nsplit - 1) * sstride;
+      ml[j] = *reinterpret_cast<const floatx4*>(prow + D);  // m, l, pad, pad
+      a[j] = *reinterpret_cast<const floatx4*>(prow + c0);
+      b[j] = *reinterpret_cast<const floatx4*>(prow + c0 + 4);
+    }
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; ++j) {
+      if (s0 + j >= nsplit) break;
+      const float Mn = fmaxf(M, ml[j][0]);
       const float sc = __builtin_amdgcn_exp2f(M - Mn);
-      const float wt = __builtin_amdgcn_exp2f(ml[0] - Mn);
-      lsum = lsum * sc + wt * ml[1];
+      const float wt = __builtin_amdgcn_exp2f(ml[j][0] - Mn);
+      lsum = lsum * sc + wt * ml[j][1];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        o[i] = o[i] * sc + wt * a[i];
-        o[4 + i] = o[4 + i] * sc + wt * b[i];
+        o[i] = o[i] * sc + wt * a[j][i];
+        o[4 + i] = o[4 + i] * sc + wt * b[j][i];
       }
       M = Mn;
     }
-    const int tau = row / G;
-    const int gam = row - tau * G;
-    bf16* orow = p.out + ((size_t)(qs + tau) * p.Hq + h * G + gam) * D + c0;
-    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-    *reinterpret_cast<u32x4*>(orow) =
-        u32x4{cvt_pk_bf16(o[0] * inv, o[1] * inv), cvt_pk_bf16(o[2] * inv, o[3] * inv),
-              cvt_pk_bf16(o[4] * inv, o[5] * inv), cvt_pk_bf16(o[6] * inv, o[7] * inv)};
   }
+  const int tau = row / G;
+  const int gam = row - tau * G;
+  bf16* orow = p.out + ((size_t)(qs + tau) * p.Hq + h * G + gam) * D + c0;
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  *reinterpret_cast<u32x4*>(orow) =
+      u32x4{cvt_pk_bf16(o[0] * inv, o[1] * inv), cvt_pk_bf16(o[2] * inv, o[3] * inv),
+            cvt_pk_bf16(o[4] * inv, o[5] * inv), cvt_pk_bf16(o[6] * inv, o[7] * inv)};
 }
 
 template <int D, int RT>
@@ -851,8 +864,10 @@ int32_t launch_rt(const nsg_attn_plan_t* plan, const AttnParams& prm, const int*
   }
   int32_t rc = launch_status("verify_attn_kernel");
   if (rc || plan->num_merge == 0) return rc;
-  hipLaunchKernelGGL((verify_merge_kernel<D, RT>), dim3(plan->num_merge, plan->num_kv_heads),
-                     dim3(kThreads), 0, stream, prm, merge, plan->num_merge);
+  constexpr int kSlices = (RT * 16 * (D / 8) + kThreads - 1) / kThreads;  // a group's pieces
+  hipLaunchKernelGGL((verify_merge_kernel<D, RT>),
+                     dim3(plan->num_merge, plan->num_kv_heads, kSlices), dim3(kThreads), 0, stream,
+                     prm, merge, plan->num_merge);
   return launch_status("verify_merge_kernel");
 }
 

@@ -172,6 +172,38 @@ __device__ __forceinline__ void wave_am(float& v, int& i) {
   }
 }
 
+// Greedy, bf16 logits: (value, column) of a chunk's best logit as one
+// 32-bit key whose unsigned order is "larger value, then lower column": the
+// bf16 bits made order-preserving (-0 ranks with +0), then the column's
+// distance from the chunk end (columns inside a chunk of < 65,536).  0 = no
+// column.
+__device__ __forceinline__ uint32_t am_key(float v, int i, int v0) {
+  if (i == INT_MAX) return 0u;
+  uint32_t b = __float_as_uint(v) >> 16;   // v is a bf16 value
+  b = b == 0x8000u ? 0u : b;
+  const uint32_t ord = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+  return (ord << 16) | (0xffffu - (uint32_t)(i - v0));
+}
+__device__ __forceinline__ void am_unkey(uint32_t key, int v0, float& v, int& i) {
+  const uint32_t ord = key >> 16;
+  const uint32_t b = (ord & 0x8000u) ? (ord & 0x7fffu) : (~ord & 0xffffu);
+  v = __uint_as_float(b << 16);
+  i = v0 + (int)(0xffffu - (key & 0xffffu));
+}
+// Max of a 32-bit key over the wave in the VALU: DPP quad swaps and row
+// mirrors inside each 16-lane row, then gfx950's row swaps (no LDS trips,
+// unlike the shuffles of wave_am).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t k) {
+  k = max(k, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0xb1, 0xf, 0xf, false));   // lane ^ 1
+  k = max(k, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0x4e, 0xf, 0xf, false));   // lane ^ 2
+  k = max(k, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0x141, 0xf, 0xf, false));  // 7 - lane in 8
+  k = max(k, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0x140, 0xf, 0xf, false));  // 15 - lane in 16
+  const auto a = __builtin_amdgcn_permlane16_swap(k, k, false, false);
+  k = max((uint32_t)a[0], (uint32_t)a[1]);
+  const auto c = __builtin_amdgcn_permlane32_swap(k, k, false, false);
+  return max((uint32_t)c[0], (uint32_t)c[1]);
+}
+
 __device__ __forceinline__ int64_t trow(const AccParams& p, int b, int i) {
   return (int64_t)b * p.t_req + (int64_t)i * p.t_row;
 }
@@ -450,10 +482,15 @@ __device__ void row_chunk_stats(const AccParams& p, int b, int lr, int chunk) {
       while (e < 7 && !(x[e] == vbest)) ++e;   // NaN-free rows
       am_merge(bv, bi, vbest, vidx + e);
     }
-    wave_am(bv, bi);
-    if (lane == 0) {
-      sm_a[wave] = bv;
-      sm_b[wave] = __int_as_float(bi);
+    if (sizeof(T) == 2 && p.cs < 65536) {   // workgroup-uniform
+      const uint32_t key = wave_max_u32(am_key(bv, bi, v0));
+      if (lane == 0) sm_a[wave] = __uint_as_float(key);
+    } else {
+      wave_am(bv, bi);
+      if (lane == 0) {
+        sm_a[wave] = bv;
+        sm_b[wave] = __int_as_float(bi);
+      }
     }
   } else {
     if (m == -INFINITY) s = 0.f;
@@ -466,13 +503,22 @@ __device__ void row_chunk_stats(const AccParams& p, int b, int lr, int chunk) {
   __syncthreads();
   if (tid == 0) {
     float a = sm_a[0], c2 = sm_b[0];
-    for (int w = 1; w < kThreads / 64; ++w) {
-      if constexpr (GREEDY) {
-        int ia = __float_as_int(c2);
-        am_merge(a, ia, sm_a[w], __float_as_int(sm_b[w]));
-        c2 = __int_as_float(ia);
-      } else {
-        ms_merge(a, c2, sm_a[w], sm_b[w]);
+    if (GREEDY && sizeof(T) == 2 && p.cs < 65536) {
+      uint32_t key = __float_as_uint(sm_a[0]);
+      for (int w = 1; w < kThreads / 64; ++w) key = max(key, __float_as_uint(sm_a[w]));
+      int ia = INT_MAX;   // (an empty chunk: no column, as in the other form)
+      a = -INFINITY;
+      if (key != 0u) am_unkey(key, v0, a, ia);
+      c2 = __int_as_float(ia);
+    } else {
+      for (int w = 1; w < kThreads / 64; ++w) {
+        if constexpr (GREEDY) {
+          int ia = __float_as_int(c2);
+          am_merge(a, ia, sm_a[w], __float_as_int(sm_b[w]));
+          c2 = __int_as_float(ia);
+        } else {
+          ms_merge(a, c2, sm_a[w], sm_b[w]);
+        }
       }
     }
     if constexpr (GREEDY) c2 = __int_as_float(~__float_as_int(c2));  // never all-zero bits

@@ -423,7 +423,10 @@ __device__ void row_chunk_stats(const AccParams& p, int b, int lr, int chunk) {
   // off, so a chunk costs one or two memory round trips, not one per vector.
   const int vfull = v0 + ((v1 - v0) & ~7);
   if (vec) {
-    constexpr int U = 8;
+    // (stochastic bf16: 12 loads, so that a chunk of up to 24,576 logits is
+    // one round trip: 46.2 -> 45.2 us at batch 64, k 4, vocab 151,936 and
+    // 58.6 -> 57.3 us at k 8, vocab 128,256 against 8)
+    constexpr int U = !GREEDY && sizeof(T) == 2 ? 12 : 8;
     constexpr int STRIDE = kThreads * 8;
     auto batch = [&](int vb, auto full) {
       u32x4 raw[U][W];
@@ -1193,7 +1196,7 @@ Layout layout(int B, int k, int V, bool greedy) {
   // a request's chunk records fit one wave's two registers per lane
   const int max_ch = std::max(1, std::min({kMaxChunks, (V + 2047) / 2048, kRecCap / rpr}));
   // at least kTargetWgs workgroups, and chunks of at most about one batch
-  // of loads per thread (greedy) or two (stochastic): measured best at
+  // of loads per thread (8 loads greedy, 12 stochastic): measured best at
   // B 64, k 4 and k 8 (V 151,936 and 128,256)
   const int cs_target = greedy ? 12288 : 20480;
   L.nch = std::max(1, std::min(max_ch, std::max((V + cs_target - 1) / cs_target,

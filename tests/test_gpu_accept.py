@@ -90,10 +90,15 @@ def test_greedy_ties_lowest_index():
     a["target"][:] = 0.0
     a["target"][0, 0, [7, 3000]] = 1.0     # tie across chunks -> 7
     a["target"][1, 0, [100, 101]] = 5.0
+    a["target"][3, 0] = -1.0               # -0 and +0 tie (the kernel's keys rank them equal)
+    a["target"][3, 0, 5] = -0.0
+    a["target"][3, 0, 4000] = 0.0
+    a["target"][2, 1] = -0.0               # a row of -0 only -> column 0
     a["draft_tokens"][:] = 0
     n, em, rb, ref = _run(a, 0.0, None)
     _assert_exact(n, em, rb, ref)
-    assert em[0, 0] == 7 and em[1, 0] == 100 and em[2, 0] == 0
+    assert em[0, 0] == 7 and em[1, 0] == 100 and em[2, 0] == 0 and em[3, 0] == 5
+    assert n[2] >= 2 and em[2, 1] == 0
 
 
 def test_stochastic_c3_shape():

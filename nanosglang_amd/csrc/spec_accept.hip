@@ -83,7 +83,7 @@ struct AccParams {
   float* dec;     // [B][kDecStride]: decision slots
   float* psum;    // [B][nch2]
   float2* rsum;   // [B][kRsRanges][kRsMaxSteps] step sums (residual, target)
-  float* xlog;    // [B][rpr] logit at the row's draft token (stochastic rows)
+  float2* xlog;   // [B][rpr] (logit at the row's draft token, 1): marked hand-off slots
   int* flags;
 };
 
@@ -473,7 +473,9 @@ __device__ void row_chunk_stats(const AccParams& p, int b, int lr, int chunk) {
   for (int vv = (vec ? vfull : v0) + tid; vv < v1; vv += kThreads) take(Logit<T>::at(base, roff + vv), vv);
 
   if constexpr (!GREEDY) {
-    if (xhit) hand_put_sync(p.xlog + r, xval);  // in place before the record vouching for it
+    // the draft token's logit, with a marker word (the slot is never all-zero
+    // bits once published; the decision polls it beside the records)
+    if (xhit) hand_put(p.xlog + r, make_float2(xval, __int_as_float(1)));
   }
   const int lane = tid & 63, wave = tid >> 6;
   if constexpr (GREEDY) {
@@ -648,13 +650,22 @@ __device__ Decision decide(const AccParams& p, int b, int64_t pre) {
     u = p.u[(int64_t)b * (k + 1) + lane];
   }
   float2* recs = p.stats + (int64_t)b * n;
+  // the draft-token logits of target row i and draft row i (lane i < k; an
+  // out-of-vocabulary draft token has none), loaded in the same round as
+  // the records and polled until published
+  const bool xok = lane < k && x >= 0 && x < p.V;
+  float2* xs_t = p.xlog + (int64_t)b * rpr + min(lane, k - 1);
+  float2* xs_d = p.xlog + (int64_t)b * rpr + k + 1 + min(lane, k - 1);
+  uint64_t bt = xok ? hand_get_bits(xs_t) : 1, bd = xok ? hand_get_bits(xs_d) : 1;
   const Recs rc = poll_recs(p, recs, n);
   float xt = 0.f, xd = 0.f;
-  if (lane < k) {  // published before the records that vouch for them
-    xt = hand_get(p.xlog + (int64_t)b * rpr + lane);
-    xd = hand_get(p.xlog + (int64_t)b * rpr + k + 1 + lane);
-    hand_put(p.xlog + (int64_t)b * rpr + lane, 0.f);          // the workspace ends zero
-    hand_put(p.xlog + (int64_t)b * rpr + k + 1 + lane, 0.f);
+  if (xok) {
+    bt = repoll(p, xs_t, bt);
+    bd = repoll(p, xs_d, bd);
+    xt = __uint_as_float((uint32_t)bt);
+    xd = __uint_as_float((uint32_t)bd);
+    clear_slot(xs_t);                        // the workspace ends zero
+    clear_slot(xs_d);
   }
   float mt = -INFINITY, zt = 0.f, md = -INFINITY, zd = 0.f;
   for (int c = 0; c < p.nch; ++c) {
@@ -1217,7 +1228,7 @@ Layout layout(int B, int k, int V, bool greedy) {
   L.psum_off = L.dec_off + al((int64_t)B * kDecStride * 4);
   L.rsum_off = L.psum_off + al((int64_t)B * kMaxChunks * 4);
   L.xlog_off = L.rsum_off + al((int64_t)B * kRsRanges * kRsMaxSteps * 8);
-  L.total = L.xlog_off + al((int64_t)rows_max * 4);
+  L.total = L.xlog_off + al((int64_t)rows_max * 8);
   return L;
 }
 
@@ -1342,7 +1353,7 @@ int32_t accept_impl(const void* target_logits, int64_t target_req_stride,
   p.dec = reinterpret_cast<float*>(ws + L.dec_off);
   p.psum = reinterpret_cast<float*>(ws + L.psum_off);
   p.rsum = reinterpret_cast<float2*>(ws + L.rsum_off);
-  p.xlog = reinterpret_cast<float*>(ws + L.xlog_off);
+  p.xlog = reinterpret_cast<float2*>(ws + L.xlog_off);
   // 16-byte vector loads need 16-byte aligned bases; rows are checked per row
   const uintptr_t mis = reinterpret_cast<uintptr_t>(target_logits) |
                         (greedy ? 0 : reinterpret_cast<uintptr_t>(draft_logits));

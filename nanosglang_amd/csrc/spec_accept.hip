@@ -1023,10 +1023,12 @@ template <typename T>
 __device__ __forceinline__ void stream_step_sums(const AccParams& p, const Decision& d,
                                                  int64_t to, int64_t dof, int ns, int v0,
                                                  int lane, float2* out) {
-  // steps whose loads are in flight together: 5 covers a range of vocab up
-  // to 163,840 in one round trip (batch 64, k 4, vocab 151,936: 46.2 -> 45.3
-  // us per call against 4; 6 takes 8 more registers and 8 ran slower)
-  constexpr int G = 5;
+  // steps whose loads are in flight together: with bf16 logits 5 covers a
+  // range of vocab up to 163,840 in one round trip (batch 64, k 4, vocab
+  // 151,936: 46.2 -> 45.3 us per call against 4; 6 takes 8 more registers
+  // and 8 ran slower); fp32 logits keep 4 (5 would raise the kernel from 92
+  // to 109 registers, one wave per SIMD fewer)
+  constexpr int G = sizeof(T) == 2 ? 5 : 4;
   for (int q0 = 0; q0 < ns; q0 += G) {
     StepRaw<T> raw[G];
 #pragma unroll
